@@ -1,0 +1,321 @@
+/*
+ * osm_hip.h -- C ABI of libosm_hip.so, the MI355X (gfx950) implementation of
+ * the q4 routed-MoE hot path of orbi-streammoe.
+ *
+ * This is the drop-in boundary: plain C types, opaque handles, explicit
+ * sizes. Each entry point names the reference interface it replaces
+ * (paths relative to the orbi-streammoe source tree). Every call returns an
+ * osm_status; on failure osm_last_error() holds the diagnostic of the calling
+ * thread, the counterpart of the reference's {executed, diagnostic} results.
+ * No exception crosses this boundary, and invalid geometry is rejected before
+ * any device work is enqueued, as in the reference.
+ *
+ * Expert weights use the MLX affine 4-bit format: uint32 words carrying 8
+ * nibbles (low nibble first), one scale and one bias per group of columns
+ * (src/cpu/reference_ops.cpp:48-63). An expert "blob" is the qpack cache-slot
+ * layout: gate/up/down x {weight u32, scales, biases} in that order, each
+ * section contiguous; osm_expert_blob_bytes() gives its size.
+ */
+#ifndef OSM_HIP_H
+#define OSM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- common --------------------------------------------------------------- */
+typedef enum osm_status {
+  OSM_OK = 0,
+  OSM_E_INVALID = 1, /* rejected arguments/geometry (reference: std::invalid_argument or a failed precondition) */
+  OSM_E_RUNTIME = 2, /* runtime failure (reference: std::runtime_error / executed=false) */
+  OSM_E_DEVICE = 3   /* HIP runtime error */
+} osm_status;
+
+enum osm_meta_dtype_c { OSM_F32 = 0, OSM_F16 = 1, OSM_BF16 = 2 };
+
+typedef struct osm_expert_geometry_c {
+  uint32_t hidden;     /* model width D: gate/up input, down output */
+  uint32_t inter;      /* expert intermediate width I */
+  uint32_t group;      /* quantisation group size */
+  uint32_t meta_dtype; /* OSM_F32 / OSM_F16 / OSM_BF16 scales and biases */
+} osm_expert_geometry_c;
+
+typedef struct osm_context_s* osm_context;
+typedef struct osm_buffer_s* osm_buffer;
+typedef struct osm_q4_projection_s* osm_q4_projection;
+typedef struct osm_expert_s* osm_expert;
+typedef struct osm_shared_expert_s* osm_shared_expert;
+typedef struct osm_expert_slab_s* osm_expert_slab;
+typedef struct osm_expert_store_s* osm_expert_store;
+typedef struct osm_host_cache_s* osm_host_cache;
+typedef struct osm_expert_cache_s* osm_expert_cache;
+typedef struct osm_cache_policy_s* osm_cache_policy;
+typedef struct osm_moe_layer_s* osm_moe_layer;
+typedef struct osm_event_s* osm_event;
+
+/* Diagnostic of the last failed call on this thread (empty string if none). */
+const char* osm_last_error(void);
+int osm_device_count(int* count);
+
+/* ---- context: VulkanComputeContext (include/orbi/streammoe/backend/vulkan_compute_context.hpp:19-49) */
+int osm_context_create(int device, osm_context* out);
+void osm_context_destroy(osm_context ctx);
+int osm_context_synchronize(osm_context ctx);
+/* Device name, NUL-terminated into buf. */
+int osm_context_device_name(osm_context ctx, char* buf, size_t n);
+/* The hipStream_t all operators of this context are ordered on. */
+void* osm_context_stream(osm_context ctx);
+
+/* Events on the context's compute stream (timing; no reference counterpart). */
+int osm_event_create(osm_context ctx, osm_event* out);
+void osm_event_destroy(osm_event e);
+int osm_event_record(osm_event e);
+int osm_event_elapsed_ms(osm_event start, osm_event stop, float* ms);
+
+/* Raw device memory for callers that pass device pointers. */
+int osm_device_alloc(osm_context ctx, size_t bytes, void** out);
+int osm_device_free(osm_context ctx, void* ptr);
+int osm_memcpy_h2d(osm_context ctx, void* dst, const void* src, size_t bytes);
+int osm_memcpy_d2h(osm_context ctx, void* dst, const void* src, size_t bytes);
+
+/* ---- float buffer: VulkanFloatBuffer (vulkan_float_buffer.hpp:23-58) ------- */
+int osm_buffer_create(osm_context ctx, size_t element_count, osm_buffer* out);
+void osm_buffer_destroy(osm_buffer b);
+size_t osm_buffer_size(osm_buffer b);
+float* osm_buffer_device_ptr(osm_buffer b);
+int osm_buffer_upload(osm_buffer b, const float* values, size_t count);
+int osm_buffer_download(osm_buffer b, float* values, size_t count);
+
+/* ---- single operators over host arrays -------------------------------------
+ * run_vulkan_q4_dequant (vulkan_q4_dequant.hpp:23-30): out has rows*packed_cols*8 floats. */
+int osm_q4_dequant(osm_context ctx, const uint32_t* packed, size_t packed_len, size_t rows,
+                   size_t packed_cols, const float* scales, const float* biases,
+                   size_t meta_len, size_t group_size, float* out, size_t out_len);
+/* run_vulkan_q4_gemv (vulkan_q4_gemv.hpp:25-33). */
+int osm_q4_gemv(osm_context ctx, const uint32_t* packed, size_t packed_len, size_t out_dim,
+                size_t packed_cols, const float* scales, const float* biases, size_t meta_len,
+                size_t group_size, const float* x, size_t x_len, float* y, size_t y_len);
+/* run_vulkan_swiglu (vulkan_swiglu.hpp:19-23). */
+int osm_swiglu(osm_context ctx, const float* gate, size_t gate_len, const float* up,
+               size_t up_len, float* out);
+/* run_vulkan_rms_norm (vulkan_rmsnorm.hpp:25-31): out has rows*dim floats. */
+int osm_rms_norm(osm_context ctx, const float* input, size_t input_len, size_t rows, size_t dim,
+                 const float* weight, size_t weight_len, float eps, float* out);
+/* Integer-exact nibble unpack of the packed layout: out[8*w + j] = nibble j
+ * (low first) of word w (the lane order of reference_ops.cpp:48-63). */
+int osm_unpack_nibbles(osm_context ctx, const uint32_t* packed, size_t words, uint8_t* out);
+
+/* ---- operators over device buffers ----------------------------------------
+ * run_vulkan_q4_gemv_buffers (vulkan_q4_gemv.hpp:39-48). */
+int osm_q4_gemv_buffers(osm_context ctx, const uint32_t* packed, size_t packed_len,
+                        size_t out_dim, size_t packed_cols, const float* scales,
+                        const float* biases, size_t meta_len, size_t group_size, osm_buffer x,
+                        osm_buffer y);
+/* VulkanQ4ProjectionWeights::create (vulkan_q4_weights.hpp:30-38); scales and
+ * biases are meta_len entries of meta_dtype (the reference passes OSM_F32). */
+int osm_q4_projection_create(osm_context ctx, const uint32_t* packed, size_t packed_len,
+                             size_t out_dim, size_t packed_cols, const void* scales,
+                             const void* biases, uint32_t meta_dtype, size_t group_size,
+                             osm_q4_projection* out);
+void osm_q4_projection_destroy(osm_q4_projection p);
+/* run_vulkan_q4_gemv_preloaded (vulkan_q4_gemv.hpp:53-57). */
+int osm_q4_gemv_preloaded(osm_context ctx, osm_q4_projection weights, osm_buffer x, osm_buffer y);
+/* run_vulkan_swiglu_buffers (vulkan_swiglu.hpp:25-30). */
+int osm_swiglu_buffers(osm_context ctx, osm_buffer gate, osm_buffer up, osm_buffer out);
+/* run_vulkan_weighted_accumulate (vulkan_weighted_accumulate.hpp:12-16):
+ * accumulator[i] += weight * source[i]. */
+int osm_weighted_accumulate(osm_context ctx, osm_buffer source, float weight,
+                            osm_buffer accumulator);
+
+/* ---- experts ----------------------------------------------------------------
+ * Blob size of one expert (docs/OSM-39B-QPACK-EXPERT-GEOMETRY.md:61-74 byte
+ * arithmetic); 0 for a geometry the fused kernels do not support. */
+size_t osm_expert_blob_bytes(const osm_expert_geometry_c* g);
+/* VulkanResidentExpert::create (vulkan_resident_expert.hpp:41-45). */
+int osm_expert_create(osm_context ctx, const void* blob, size_t bytes,
+                      const osm_expert_geometry_c* g, osm_expert* out);
+void osm_expert_destroy(osm_expert e);
+/* VulkanResidentExpert::run (vulkan_resident_expert.hpp:57-59). */
+int osm_expert_run(osm_context ctx, osm_expert e, const float* x, size_t x_len, float* out,
+                   size_t out_len);
+/* VulkanResidentExpert::run_from_buffer / output_buffer (vulkan_resident_expert.hpp:61-69). */
+int osm_expert_run_from_buffer(osm_context ctx, osm_expert e, osm_buffer x);
+int osm_expert_download_output(osm_expert e, float* out, size_t out_len);
+size_t osm_expert_accounted_bytes(osm_expert e);
+
+/* VulkanResidentSharedExpert (vulkan_resident_shared_expert.hpp:49-69). */
+int osm_shared_expert_create(osm_context ctx, const void* blob, size_t bytes,
+                             const osm_expert_geometry_c* g, const float* scalar_gate,
+                             size_t scalar_len, osm_shared_expert* out);
+void osm_shared_expert_destroy(osm_shared_expert s);
+int osm_shared_expert_scalar_scale(osm_shared_expert s, const float* hidden, size_t len,
+                                   float* out_scale);
+int osm_shared_expert_run_from_buffer(osm_context ctx, osm_shared_expert s, osm_buffer hidden);
+int osm_shared_expert_download_output(osm_shared_expert s, float* out, size_t out_len);
+
+/* ---- HBM-resident expert stack (all experts of `layers` layers) ------------
+ * The all-resident mode of the resident cache: every expert in one slab,
+ * addressed through a device pointer table, no host round trip per token. */
+int osm_expert_slab_create(osm_context ctx, const osm_expert_geometry_c* g, uint32_t layers,
+                           uint32_t experts, osm_expert_slab* out);
+void osm_expert_slab_destroy(osm_expert_slab s);
+size_t osm_expert_slab_stride(osm_expert_slab s);
+int osm_expert_slab_upload(osm_expert_slab s, uint32_t layer, uint32_t expert, const void* blob,
+                           size_t bytes);
+int osm_expert_slab_download(osm_expert_slab s, uint32_t layer, uint32_t expert, void* out,
+                             size_t bytes);
+/* Fills every expert from the seeded generator on the device. */
+int osm_expert_slab_synthesize(osm_expert_slab s, uint64_t seed);
+
+/* ---- routed-MoE layer -------------------------------------------------------
+ * Layer state of QwenCheckpointSparseMoeLayer / QwenCheckpointMoeSublayer
+ * (checkpoint_sparse_moe.hpp, checkpoint_moe_sublayer.hpp): router [E, D] and
+ * shared-expert gate vector [D] in router_dtype, optional RMSNorm weight [D]
+ * (fp32, NULL for none), the shared expert blob (NULL when has_shared == 0). */
+typedef struct osm_moe_config {
+  osm_expert_geometry_c geometry;
+  uint32_t expert_count;   /* E (<= 1024) */
+  uint32_t top_k;          /* k (<= 16) */
+  uint32_t norm_topk_prob; /* renormalise selected probabilities (qwen_router.hpp:10-15) */
+  uint32_t has_shared;     /* add sigmoid(w_sg . x) * shared(x) */
+  float rms_eps;           /* RMSNorm epsilon of the sublayer form */
+} osm_moe_config;
+
+int osm_moe_layer_create(osm_context ctx, const osm_moe_config* cfg, const void* router,
+                         uint32_t router_dtype, const void* shared_gate_vec,
+                         const float* norm_weight, const void* shared_blob, size_t shared_bytes,
+                         uint32_t max_tokens, osm_moe_layer* out);
+void osm_moe_layer_destroy(osm_moe_layer l);
+
+/* Outputs of one decode; any pointer may be NULL. */
+typedef struct osm_moe_outputs {
+  float* out;            /* [tokens, D] */
+  float* normalized;     /* [tokens, D] RMSNorm output (sublayer form) */
+  uint32_t* ids;         /* [tokens, k] picks by descending probability, ties to the lower id */
+  float* weights;        /* [tokens, k] routing weights */
+  float* mass;           /* [tokens] selected probability mass (QwenRouterResult) */
+  float* shared_gate;    /* [tokens] sigmoid(w_sg . x) */
+  float* logits;         /* [tokens, E] router logits */
+} osm_moe_outputs;
+
+/* run_qwen_sparse_moe_vulkan_accum (src/model/routed_moe.hpp:58-65) with every
+ * expert of slab layer `slab_layer` resident; sublayer != 0 gives
+ * QwenCheckpointMoeSublayer::run (checkpoint_moe_sublayer.hpp:55):
+ * out = hidden + MoE(RMSNorm(hidden)). Host arrays in and out. */
+int osm_moe_layer_run_slab(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                           uint32_t slab_layer, const float* hidden, uint32_t tokens,
+                           int sublayer, const osm_moe_outputs* outputs);
+/* Same through the GPU resident cache: routing on the device, residency
+ * decided on the host from the routed ids, misses filled on a side stream. */
+int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache cache,
+                             uint32_t layer, const float* hidden, uint32_t tokens, int sublayer,
+                             const osm_moe_outputs* outputs);
+/* Device pointers in and out, stream-ordered, no synchronisation. */
+int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                                uint32_t slab_layer, const float* x_dev, float* y_dev,
+                                uint32_t tokens, int sublayer);
+/* Enqueues n_layers decodes back to back. chained != 0: sublayer form,
+ * layer i reads the output of layer i-1 (x_dev [tokens, D] in, y_dev
+ * [tokens, D] out, scratch_dev [tokens, D] ping-pong). chained == 0: layer i
+ * reads x_dev + i*tokens*D and writes y_dev + i*tokens*D (MoE form). Layer i
+ * uses layers[i] and slab layer slab_layers[i]. */
+int osm_moe_decode_layers(osm_context ctx, const osm_moe_layer* layers,
+                          const uint32_t* slab_layers, uint32_t n_layers, osm_expert_slab slab,
+                          const float* x_dev, float* y_dev, float* scratch_dev, uint32_t tokens,
+                          int chained);
+/* Launches one phase of a decode whose routing already ran for this layer
+ * (phase 0 route, 1 gate/up + SwiGLU, 2 down + accumulate); for per-kernel
+ * timing. */
+int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                               uint32_t slab_layer, const float* x_dev, float* y_dev,
+                               uint32_t tokens, int sublayer, int phase);
+
+/* ---- expert sources and caches ---------------------------------------------
+ * Whole model in pinned host memory: the fill source of the capped cache. */
+int osm_expert_store_create(const osm_expert_geometry_c* g, uint32_t layers, uint32_t experts,
+                            osm_expert_store* out);
+void osm_expert_store_destroy(osm_expert_store s);
+void* osm_expert_store_blob(osm_expert_store s, uint32_t layer, uint32_t expert);
+/* Generates every expert on the device and copies it down. */
+int osm_expert_store_synthesize(osm_context ctx, osm_expert_store s, uint64_t seed);
+
+/* Storage callback of the host L1 cache (storage/expert_storage.hpp:20-29):
+ * fill count destinations of `stride` bytes each; non-zero means the read
+ * failed (the reference's storage throws). */
+typedef int (*osm_read_experts_fn)(void* user, const uint32_t* layers, const uint32_t* experts,
+                                   void* const* destinations, size_t count, size_t stride);
+
+typedef struct osm_host_cache_stats {
+  uint64_t hits, misses, allocated_slots, capacity_slots, logical_bytes, budget_bytes;
+} osm_host_cache_stats;
+
+/* ExpertCache (cache/expert_cache.hpp:30-87). pinned != 0 puts slots in
+ * pinned memory (needs a device). */
+int osm_host_cache_create(size_t stride, size_t budget_bytes, size_t minimum_slots, int pinned,
+                          osm_read_experts_fn read, void* user, osm_host_cache* out);
+void osm_host_cache_destroy(osm_host_cache c);
+/* ExpertCache::fetch: out_slots[i] is the slot of experts[i]; out_bytes[i]
+ * (optional) points at its bytes until the next fetch. */
+int osm_host_cache_fetch(osm_host_cache c, uint32_t layer, const uint32_t* experts, size_t n,
+                         uint64_t* out_slots, const void** out_bytes);
+/* ExpertCache::resident_slot: slot or -1. */
+int64_t osm_host_cache_resident_slot(osm_host_cache c, uint32_t layer, uint32_t expert);
+void osm_host_cache_stats_get(osm_host_cache c, osm_host_cache_stats* out);
+
+typedef struct osm_expert_cache_stats {
+  uint64_t hits, misses, loads, evictions, resident_entries, resident_bytes, budget_bytes;
+} osm_expert_cache_stats;
+
+/* VulkanResidentExpertCache (vulkan_resident_expert_cache.hpp:27-83) over a
+ * pinned store, or over a host L1 cache (the reference's miss path). */
+int osm_expert_cache_create_from_store(osm_context ctx, osm_expert_store store,
+                                       size_t budget_bytes, osm_expert_cache* out);
+int osm_expert_cache_create_from_host_cache(osm_context ctx, osm_host_cache host,
+                                            const osm_expert_geometry_c* g, size_t budget_bytes,
+                                            osm_expert_cache* out);
+void osm_expert_cache_destroy(osm_expert_cache c);
+/* VulkanResidentExpertCache::get: device blob pointer of the resident expert. */
+int osm_expert_cache_get(osm_expert_cache c, uint32_t layer, uint32_t expert,
+                         const void** out_device_blob);
+/* VulkanResidentExpertCache::run. */
+int osm_expert_cache_run(osm_expert_cache c, uint32_t layer, uint32_t expert, const float* x,
+                         size_t x_len, float* out, size_t out_len);
+int osm_expert_cache_contains(osm_expert_cache c, uint32_t layer, uint32_t expert);
+void osm_expert_cache_stats_get(osm_expert_cache c, osm_expert_cache_stats* out);
+uint64_t osm_expert_cache_bytes_filled(osm_expert_cache c);
+
+/* The resident cache's LFU+recency policy alone (host only, no device):
+ * vulkan_resident_expert_cache.cpp:44-188. Returns 1 on a hit, 0 on a miss
+ * (the key is admitted; evicted keys (layer<<32)|expert go to `evicted`,
+ * their count to *n_evicted), or an osm_status error as a negative value. */
+int osm_cache_policy_create(size_t budget_bytes, osm_cache_policy* out);
+void osm_cache_policy_destroy(osm_cache_policy p);
+int osm_cache_policy_get(osm_cache_policy p, uint32_t layer, uint32_t expert,
+                         size_t accounted_bytes, uint64_t* evicted, size_t cap,
+                         size_t* n_evicted);
+int osm_cache_policy_contains(osm_cache_policy p, uint32_t layer, uint32_t expert);
+void osm_cache_policy_stats_get(osm_cache_policy p, osm_expert_cache_stats* out);
+
+/* ---- seeded synthetic inputs, generated on the device ---------------------
+ * Bit-identical to the host generator described in the repository docs. */
+int osm_synth_expert_blob(osm_context ctx, uint64_t seed, uint32_t layer, uint32_t expert,
+                          const osm_expert_geometry_c* g, void* host_out, size_t bytes);
+int osm_synth_router_bf16(osm_context ctx, uint64_t seed, uint32_t layer, uint32_t experts,
+                          uint32_t hidden, uint16_t* host_out);
+int osm_synth_shared_gate_bf16(osm_context ctx, uint64_t seed, uint32_t layer, uint32_t hidden,
+                               uint16_t* host_out);
+int osm_synth_norm_weight(osm_context ctx, uint64_t seed, uint32_t layer, uint32_t hidden,
+                          float* host_out);
+int osm_synth_tokens(osm_context ctx, uint64_t seed, uint32_t first_token, uint32_t count,
+                     uint32_t hidden, float* host_out);
+int osm_synth_tokens_device(osm_context ctx, uint64_t seed, uint32_t first_token, uint32_t count,
+                            uint32_t hidden, float* dev_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OSM_HIP_H */

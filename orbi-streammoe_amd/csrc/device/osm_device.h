@@ -1,0 +1,145 @@
+/*
+ * osm_device.h -- the thin C ABI between the C++ host code and the HIP
+ * device code of libosm_hip.so.
+ *
+ * Host translation units (csrc/host, csrc/capi.cpp) are plain C++20 and never
+ * include HIP headers: every device allocation, copy, stream, event and
+ * kernel launch goes through the functions below, which are implemented in
+ * the .hip translation units. All functions return 0 on success or a HIP
+ * error code; osmd_error_string() names it. Streams and events are opaque.
+ */
+#ifndef OSM_DEVICE_H
+#define OSM_DEVICE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../osm_layout.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* osmd_stream;
+typedef void* osmd_event;
+
+const char* osmd_error_string(int code);
+
+/* ---- runtime ------------------------------------------------------------ */
+int osmd_device_count(int* count);
+int osmd_set_device(int device);
+int osmd_device_name(int device, char* buf, size_t n);
+int osmd_device_mem_info(size_t* free_bytes, size_t* total_bytes);
+int osmd_malloc(void** ptr, size_t bytes);
+int osmd_free(void* ptr);
+int osmd_host_malloc(void** ptr, size_t bytes); /* pinned */
+int osmd_host_free(void* ptr);
+int osmd_memcpy_h2d(void* dst, const void* src, size_t bytes, osmd_stream s);
+int osmd_memcpy_d2h(void* dst, const void* src, size_t bytes, osmd_stream s);
+int osmd_memcpy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s);
+/* Zero-fill with a kernel (safe inside captured graphs). */
+int osmd_zero(void* dst, size_t bytes, osmd_stream s);
+int osmd_stream_create(osmd_stream* s);
+int osmd_stream_destroy(osmd_stream s);
+int osmd_stream_synchronize(osmd_stream s);
+int osmd_event_create(osmd_event* e);
+int osmd_event_destroy(osmd_event e);
+int osmd_event_record(osmd_event e, osmd_stream s);
+int osmd_event_synchronize(osmd_event e);
+int osmd_stream_wait_event(osmd_stream s, osmd_event e);
+int osmd_event_elapsed_ms(osmd_event start, osmd_event stop, float* ms);
+int osmd_device_synchronize(void);
+
+/* ---- elementwise / projection kernels ----------------------------------- */
+typedef struct osmd_q4_proj {
+  const uint32_t* packed; /* [out_dim, packed_cols] */
+  const void* scales;     /* [out_dim, groups] meta */
+  const void* biases;     /* [out_dim, groups] meta */
+  uint32_t out_dim;
+  uint32_t packed_cols;
+  uint32_t group;
+  uint32_t meta_dtype;
+} osmd_q4_proj;
+
+int osmd_q4_dequant(const osmd_q4_proj* p, float* out, osmd_stream s);
+int osmd_q4_gemv(const osmd_q4_proj* p, const float* x, float* y, osmd_stream s);
+int osmd_unpack_nibbles(const uint32_t* packed, size_t words, uint8_t* out,
+                        osmd_stream s);
+int osmd_swiglu(const float* gate, const float* up, float* out, size_t n,
+                osmd_stream s);
+int osmd_weighted_accumulate(const float* src, float weight, float* acc,
+                             size_t n, osmd_stream s);
+int osmd_rms_norm(const float* in, const float* weight, float* out,
+                  uint32_t rows, uint32_t dim, float eps, osmd_stream s);
+/* One expert MLP (gate/up GEMV with fused SwiGLU, then down GEMV) for one
+ * token, used by the resident-expert operator. h is [inter] scratch. */
+int osmd_expert_forward(const uint8_t* blob, osm_expert_geometry g,
+                        const float* x, float* h, float* out, osmd_stream s);
+
+/* ---- fused routed-MoE decode ------------------------------------------- */
+enum {
+  OSMD_MOE_RMSNORM = 1u,  /* x is the residual stream; normalise it first */
+  OSMD_MOE_RESIDUAL = 2u, /* y = x + moe(norm(x)) */
+  OSMD_MOE_SHARED = 4u    /* add the sigmoid-gated shared expert */
+};
+
+typedef struct osmd_moe_args {
+  osm_expert_geometry geom;
+  uint32_t expert_count;   /* E */
+  uint32_t top_k;          /* k */
+  uint32_t norm_topk_prob; /* renormalise the selected probabilities */
+  uint32_t router_dtype;   /* OSM_META_F32 / F16 / BF16 for router, w_sg */
+  uint32_t flags;          /* OSMD_MOE_* */
+  uint32_t tokens;         /* B */
+  float rms_eps;
+  const float* x;                     /* [B, D] */
+  float* y;                           /* [B, D] */
+  const void* router;                 /* [E, D] */
+  const void* shared_gate_vec;        /* [D] */
+  const float* norm_weight;           /* [D] */
+  const uint8_t* shared_expert;       /* blob */
+  const uint8_t* const* expert_table; /* [E] device pointers to blobs */
+  float* logits;      /* [B, E]   out */
+  uint32_t* ids;      /* [B, k]   out */
+  float* weights;     /* [B, k]   out */
+  float* shared_gate; /* [B]      out */
+  float* mass;        /* [B]      out */
+  float* x_norm;      /* [B, D]   scratch/out */
+  float* h;           /* [B, k+1, I] scratch */
+  const uint8_t** slot_ptrs; /* [B, k+1] scratch: blob of each pick, shared last */
+  uint32_t* counter;  /* [B] zero on entry, zero again on exit */
+} osmd_moe_args;
+
+/* Largest top-k and expert count the fused decode kernels accept. */
+#define OSMD_MAX_TOP_K 16u
+#define OSMD_MAX_EXPERTS 1024u
+
+/* route: RMSNorm + router + shared gate + top-k; writes ids/weights/mass/
+ * shared_gate and slot_ptrs (from expert_table; an absent expert gives a
+ * null pointer, which the expert phase skips). experts: gate/up + SwiGLU and
+ * down + weighted accumulate over slot_ptrs. decode = route then experts. */
+int osmd_moe_route(const osmd_moe_args* a, osmd_stream s);
+int osmd_moe_experts(const osmd_moe_args* a, osmd_stream s);
+int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s);
+/* The two halves of the expert phase, for per-kernel timing. */
+int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s);
+int osmd_moe_down(const osmd_moe_args* a, osmd_stream s);
+
+/* ---- seeded synthetic inputs (bit-identical to the host generator) ------ */
+int osmd_synth_expert_blobs(uint64_t seed, uint32_t layer, uint32_t first_expert,
+                            uint32_t count, osm_expert_geometry g, uint8_t* dst,
+                            size_t stride, osmd_stream s);
+int osmd_synth_router_bf16(uint64_t seed, uint32_t layer, uint32_t experts,
+                           uint32_t hidden, uint16_t* dst, osmd_stream s);
+int osmd_synth_shared_gate_bf16(uint64_t seed, uint32_t layer, uint32_t hidden,
+                                uint16_t* dst, osmd_stream s);
+int osmd_synth_norm_weight(uint64_t seed, uint32_t layer, uint32_t hidden,
+                           float* dst, osmd_stream s);
+int osmd_synth_tokens(uint64_t seed, uint32_t first_token, uint32_t count,
+                      uint32_t hidden, float* dst, osmd_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OSM_DEVICE_H */

@@ -1,0 +1,118 @@
+// runtime.hip -- device memory, streams and events behind osm_device.h.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "device_common.hpp"
+
+namespace {
+
+int rc(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
+
+__global__ void zero_kernel(uint4* __restrict__ dst16, size_t n16,
+                            uint8_t* __restrict__ tail, size_t ntail) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+    dst16[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (blockIdx.x == 0)
+    for (size_t i = threadIdx.x; i < ntail; i += blockDim.x) tail[i] = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* osmd_error_string(int code) {
+  return hipGetErrorString(static_cast<hipError_t>(code));
+}
+
+int osmd_device_count(int* count) { return rc(hipGetDeviceCount(count)); }
+int osmd_set_device(int device) { return rc(hipSetDevice(device)); }
+
+int osmd_device_name(int device, char* buf, size_t n) {
+  hipDeviceProp_t prop;
+  const int r = rc(hipGetDeviceProperties(&prop, device));
+  if (r != 0) return r;
+  if (n > 0) {
+    std::strncpy(buf, prop.name, n - 1);
+    buf[n - 1] = '\0';
+  }
+  return 0;
+}
+
+int osmd_device_mem_info(size_t* free_bytes, size_t* total_bytes) {
+  return rc(hipMemGetInfo(free_bytes, total_bytes));
+}
+
+int osmd_malloc(void** ptr, size_t bytes) { return rc(hipMalloc(ptr, bytes)); }
+int osmd_free(void* ptr) { return ptr ? rc(hipFree(ptr)) : 0; }
+int osmd_host_malloc(void** ptr, size_t bytes) {
+  return rc(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+}
+int osmd_host_free(void* ptr) { return ptr ? rc(hipHostFree(ptr)) : 0; }
+
+int osmd_memcpy_h2d(void* dst, const void* src, size_t bytes, osmd_stream s) {
+  return rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(s)));
+}
+int osmd_memcpy_d2h(void* dst, const void* src, size_t bytes, osmd_stream s) {
+  return rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(s)));
+}
+int osmd_memcpy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s) {
+  return rc(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(s)));
+}
+
+int osmd_zero(void* dst, size_t bytes, osmd_stream s) {
+  if (bytes == 0) return 0;
+  // Split into an aligned 16-byte body and a byte tail.
+  const uintptr_t p = reinterpret_cast<uintptr_t>(dst);
+  if (p % 16 != 0) {
+    zero_kernel<<<1, 256, 0, static_cast<hipStream_t>(s)>>>(nullptr, 0, static_cast<uint8_t*>(dst), bytes);
+    return osmk::launch_status();
+  }
+  const size_t n16 = bytes / 16;
+  const size_t ntail = bytes - n16 * 16;
+  size_t blocks = (n16 + 255) / 256;
+  if (blocks == 0) blocks = 1;
+  if (blocks > 4096) blocks = 4096;
+  zero_kernel<<<static_cast<unsigned>(blocks), 256, 0, static_cast<hipStream_t>(s)>>>(
+      static_cast<uint4*>(dst), n16, static_cast<uint8_t*>(dst) + n16 * 16, ntail);
+  return osmk::launch_status();
+}
+
+int osmd_stream_create(osmd_stream* s) {
+  hipStream_t h = nullptr;
+  // Default priority, non-blocking with respect to the null stream.
+  const int r = rc(hipStreamCreateWithFlags(&h, hipStreamNonBlocking));
+  *s = h;
+  return r;
+}
+int osmd_stream_destroy(osmd_stream s) {
+  return s ? rc(hipStreamDestroy(static_cast<hipStream_t>(s))) : 0;
+}
+int osmd_stream_synchronize(osmd_stream s) {
+  return rc(hipStreamSynchronize(static_cast<hipStream_t>(s)));
+}
+int osmd_event_create(osmd_event* e) {
+  hipEvent_t h = nullptr;
+  const int r = rc(hipEventCreate(&h));
+  *e = h;
+  return r;
+}
+int osmd_event_destroy(osmd_event e) {
+  return e ? rc(hipEventDestroy(static_cast<hipEvent_t>(e))) : 0;
+}
+int osmd_event_record(osmd_event e, osmd_stream s) {
+  return rc(hipEventRecord(static_cast<hipEvent_t>(e), static_cast<hipStream_t>(s)));
+}
+int osmd_event_synchronize(osmd_event e) {
+  return rc(hipEventSynchronize(static_cast<hipEvent_t>(e)));
+}
+int osmd_stream_wait_event(osmd_stream s, osmd_event e) {
+  return rc(hipStreamWaitEvent(static_cast<hipStream_t>(s), static_cast<hipEvent_t>(e), 0));
+}
+int osmd_event_elapsed_ms(osmd_event start, osmd_event stop, float* ms) {
+  return rc(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+}
+int osmd_device_synchronize(void) { return rc(hipDeviceSynchronize()); }
+
+}  // extern "C"

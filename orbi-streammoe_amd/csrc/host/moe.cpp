@@ -1,0 +1,451 @@
+// moe.cpp -- routed-MoE layer state and decode (the HIP counterparts of
+// src/model/checkpoint_sparse_moe.cpp, checkpoint_moe_sublayer.cpp and
+// routed_moe.cpp:254-430).
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <unordered_set>
+#include <utility>
+#include <vector>
+
+#include "host_util.hpp"
+#include "osm_hip.hpp"
+
+namespace osm {
+namespace {
+
+bool finite_weights(const void* p, std::size_t n, std::uint32_t dtype) {
+  if (dtype == OSM_META_F32) return all_finite(std::span<const float>(static_cast<const float*>(p), n));
+  const auto* h = static_cast<const std::uint16_t*>(p);
+  const std::uint16_t exp_mask = dtype == OSM_META_BF16 ? 0x7F80U : 0x7C00U;
+  for (std::size_t i = 0; i < n; ++i)
+    if ((h[i] & exp_mask) == exp_mask) return false;
+  return true;
+}
+
+}  // namespace
+
+struct HipMoeLayer::Impl {
+  HipMoeLayerConfig cfg{};
+  std::uint32_t router_dtype = OSM_META_BF16;
+  std::uint32_t max_tokens = 0;
+  int device = -1;
+  DeviceBytes router, shared_gate_vec, norm_weight, shared_blob;
+  // workspace
+  DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs, counter;
+  PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
+
+  std::uint32_t nslot() const { return cfg.top_k + (cfg.has_shared_expert ? 1U : 0U); }
+
+  osmd_moe_args args(const float* x, float* y, std::uint32_t tokens,
+                     const std::uint8_t* const* table, bool sublayer) const {
+    osmd_moe_args a{};
+    a.geom = cfg.geometry;
+    a.expert_count = cfg.expert_count;
+    a.top_k = cfg.top_k;
+    a.norm_topk_prob = cfg.norm_topk_prob ? 1U : 0U;
+    a.router_dtype = router_dtype;
+    a.flags = (cfg.has_shared_expert ? static_cast<std::uint32_t>(OSMD_MOE_SHARED) : 0U) |
+              (sublayer ? static_cast<std::uint32_t>(OSMD_MOE_RMSNORM | OSMD_MOE_RESIDUAL) : 0U);
+    a.tokens = tokens;
+    a.rms_eps = cfg.rms_eps;
+    a.x = x;
+    a.y = y;
+    a.router = router.get();
+    a.shared_gate_vec = shared_gate_vec.get();
+    a.norm_weight = norm_weight.as<const float>();
+    a.shared_expert = shared_blob.as<const std::uint8_t>();
+    a.expert_table = table;
+    a.logits = logits.as<float>();
+    a.ids = ids.as<std::uint32_t>();
+    a.weights = weights.as<float>();
+    a.shared_gate = shared_gate.as<float>();
+    a.mass = mass.as<float>();
+    a.x_norm = x_norm.as<float>();
+    a.h = h.as<float>();
+    a.slot_ptrs = slot_ptrs.as<const std::uint8_t*>();
+    a.counter = counter.as<std::uint32_t>();
+    return a;
+  }
+};
+
+HipMoeLayer::HipMoeLayer() = default;
+HipMoeLayer::~HipMoeLayer() = default;
+HipMoeLayer::HipMoeLayer(HipMoeLayer&&) noexcept = default;
+HipMoeLayer& HipMoeLayer::operator=(HipMoeLayer&&) noexcept = default;
+
+std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const HipMoeLayerConfig& config,
+                                               const void* router, std::uint32_t router_dtype,
+                                               const void* shared_gate_vec,
+                                               std::span<const float> norm_weight,
+                                               std::span<const std::byte> shared_blob,
+                                               std::uint32_t max_tokens,
+                                               std::string* diagnostic) noexcept {
+  try {
+    if (!context.activate(diagnostic)) return std::nullopt;
+    const osm_expert_geometry& g = config.geometry;
+    if (!check_expert_geometry(g, diagnostic)) return std::nullopt;
+    if (config.expert_count == 0 || config.top_k == 0) {
+      set_diag(diagnostic, "qwen router: dimensions and top_k must be non-zero");
+      return std::nullopt;
+    }
+    if (config.top_k > config.expert_count) {
+      set_diag(diagnostic, "qwen router: top_k cannot exceed expert_count");
+      return std::nullopt;
+    }
+    if (config.top_k > OSMD_MAX_TOP_K || config.expert_count > OSMD_MAX_EXPERTS) {
+      set_diag(diagnostic, "MoE layer: top_k <= 16 and expert_count <= 1024 are supported");
+      return std::nullopt;
+    }
+    const std::size_t nslot = config.top_k + (config.has_shared_expert ? 1U : 0U);
+    if (nslot * (g.inter + g.inter / 32U) * sizeof(float) > 65536U) {
+      set_diag(diagnostic, "MoE layer: (top_k + shared) * intermediate exceeds the 64 KiB LDS staging");
+      return std::nullopt;
+    }
+    if (router_dtype > OSM_META_BF16 || router == nullptr) {
+      set_diag(diagnostic, "MoE layer: router must be F32, F16 or BF16");
+      return std::nullopt;
+    }
+    if (max_tokens == 0 || max_tokens > 65535U) {
+      set_diag(diagnostic, "MoE layer: max_tokens must be in [1, 65535]");
+      return std::nullopt;
+    }
+    if (!norm_weight.empty() && norm_weight.size() != g.hidden) {
+      set_diag(diagnostic, "MoE sublayer: RMSNorm weight size does not match hidden");
+      return std::nullopt;
+    }
+    if (config.has_shared_expert) {
+      if (shared_blob.size() != expert_blob_bytes(g) || shared_gate_vec == nullptr) {
+        set_diag(diagnostic, "Qwen sparse MoE shared expert geometry does not match hidden size");
+        return std::nullopt;
+      }
+    }
+    const std::size_t esz = osm_meta_bytes(router_dtype);
+    const std::size_t router_n = static_cast<std::size_t>(config.expert_count) * g.hidden;
+    if (!finite_weights(router, router_n, router_dtype)) {
+      set_diag(diagnostic, "qwen router: router weight contains non-finite value");
+      return std::nullopt;
+    }
+    if (config.has_shared_expert && !finite_weights(shared_gate_vec, g.hidden, router_dtype)) {
+      set_diag(diagnostic, "shared expert scalar gate contains non-finite value");
+      return std::nullopt;
+    }
+    auto impl = std::make_unique<Impl>();
+    impl->cfg = config;
+    impl->router_dtype = router_dtype;
+    impl->max_tokens = max_tokens;
+    impl->device = context.device();
+    const osmd_stream st = context.stream();
+    auto up = [&](DeviceBytes& d, const void* src, std::size_t bytes) {
+      int rc = d.allocate(bytes);
+      if (rc == 0 && bytes) rc = osmd_memcpy_h2d(d.get(), src, bytes, st);
+      return rc;
+    };
+    const std::size_t T = max_tokens, D = g.hidden, E = config.expert_count, K = config.top_k;
+    int rc = up(impl->router, router, router_n * esz);
+    if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_gate_vec, shared_gate_vec, D * esz);
+    if (rc == 0 && !norm_weight.empty()) rc = up(impl->norm_weight, norm_weight.data(), norm_weight.size_bytes());
+    if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_blob, shared_blob.data(), shared_blob.size());
+    if (rc == 0) rc = impl->x_in.allocate(T * D * sizeof(float));
+    if (rc == 0) rc = impl->y_out.allocate(T * D * sizeof(float));
+    if (rc == 0) rc = impl->logits.allocate(T * E * sizeof(float));
+    if (rc == 0) rc = impl->ids.allocate(T * K * sizeof(std::uint32_t));
+    if (rc == 0) rc = impl->weights.allocate(T * K * sizeof(float));
+    if (rc == 0) rc = impl->mass.allocate(T * sizeof(float));
+    if (rc == 0) rc = impl->shared_gate.allocate(T * sizeof(float));
+    if (rc == 0) rc = impl->x_norm.allocate(T * D * sizeof(float));
+    if (rc == 0) rc = impl->h.allocate(T * nslot * g.inter * sizeof(float));
+    if (rc == 0) rc = impl->slot_ptrs.allocate(T * nslot * sizeof(void*));
+    if (rc == 0) rc = impl->counter.allocate(T * sizeof(std::uint32_t));
+    if (rc == 0) rc = osmd_zero(impl->counter.get(), T * sizeof(std::uint32_t), st);
+    if (rc == 0) rc = osmd_zero(impl->shared_gate.get(), T * sizeof(float), st);
+    if (rc == 0) rc = impl->host_ptrs.allocate(T * nslot * sizeof(void*));
+    if (rc == 0) rc = osmd_stream_synchronize(st);
+    if (rc != 0) {
+      set_diag(diagnostic, hip_error("MoE layer allocation/upload failed", rc));
+      return std::nullopt;
+    }
+    HipMoeLayer layer;
+    layer.impl_ = std::move(impl);
+    set_diag(diagnostic, "HIP MoE layer state resident in HBM");
+    return layer;
+  } catch (const std::exception& e) {
+    set_diag(diagnostic, std::string("MoE layer creation exception: ") + e.what());
+    return std::nullopt;
+  }
+}
+
+bool HipMoeLayer::valid() const noexcept { return impl_ && impl_->router.get(); }
+const HipMoeLayerConfig& HipMoeLayer::config() const noexcept {
+  static const HipMoeLayerConfig none{};
+  return impl_ ? impl_->cfg : none;
+}
+std::uint32_t HipMoeLayer::max_tokens() const noexcept { return impl_ ? impl_->max_tokens : 0; }
+const std::uint8_t* HipMoeLayer::shared_blob() const noexcept {
+  return impl_ ? impl_->shared_blob.as<const std::uint8_t>() : nullptr;
+}
+const std::uint32_t* HipMoeLayer::device_ids() const noexcept {
+  return impl_ ? impl_->ids.as<const std::uint32_t>() : nullptr;
+}
+
+HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const float* x, float* y,
+                                             std::uint32_t tokens,
+                                             const std::uint8_t* const* expert_table,
+                                             bool sublayer) noexcept {
+  HipDispatchResult r;
+  if (!valid()) {
+    r.diagnostic = "MoE layer is not valid";
+    return r;
+  }
+  if (!context.activate(&r.diagnostic)) return r;
+  if (context.device() != impl_->device) {
+    r.diagnostic = "MoE layer belongs to a different device";
+    return r;
+  }
+  if (tokens == 0 || tokens > impl_->max_tokens) {
+    r.diagnostic = "MoE decode token count must be in [1, max_tokens]";
+    return r;
+  }
+  if (x == nullptr || y == nullptr || expert_table == nullptr) {
+    r.diagnostic = "MoE decode needs device input, output and expert table";
+    return r;
+  }
+  if (sublayer && impl_->norm_weight.get() == nullptr) {
+    r.diagnostic = "MoE sublayer decode needs an RMSNorm weight";
+    return r;
+  }
+  const osmd_moe_args a = impl_->args(x, y, tokens, expert_table, sublayer);
+  const int rc = osmd_moe_decode(&a, context.stream());
+  if (rc != 0) {
+    r.diagnostic = hip_error("MoE decode launch failed", rc);
+    return r;
+  }
+  r.executed = true;
+  r.diagnostic = "HIP routed MoE decode enqueued";
+  return r;
+}
+
+HipDispatchResult HipMoeLayer::launch_phase(HipComputeContext& context, const float* x, float* y,
+                                            std::uint32_t tokens,
+                                            const std::uint8_t* const* expert_table, bool sublayer,
+                                            int phase) noexcept {
+  HipDispatchResult r;
+  if (!valid() || !context.activate(&r.diagnostic)) {
+    if (r.diagnostic.empty()) r.diagnostic = "MoE layer is not valid";
+    return r;
+  }
+  if (tokens == 0 || tokens > impl_->max_tokens || x == nullptr || y == nullptr || expert_table == nullptr) {
+    r.diagnostic = "MoE phase launch: invalid arguments";
+    return r;
+  }
+  if (sublayer && impl_->norm_weight.get() == nullptr) {
+    r.diagnostic = "MoE sublayer decode needs an RMSNorm weight";
+    return r;
+  }
+  const osmd_moe_args a = impl_->args(x, y, tokens, expert_table, sublayer);
+  int rc;
+  switch (phase) {
+    case 0: rc = osmd_moe_route(&a, context.stream()); break;
+    case 1: rc = osmd_moe_gate_up(&a, context.stream()); break;
+    case 2: rc = osmd_moe_down(&a, context.stream()); break;
+    default:
+      r.diagnostic = "MoE phase must be 0 (route), 1 (gate/up) or 2 (down)";
+      return r;
+  }
+  if (rc != 0) {
+    r.diagnostic = hip_error("MoE phase launch failed", rc);
+    return r;
+  }
+  r.executed = true;
+  return r;
+}
+
+bool HipMoeLayer::download_routing(HipComputeContext& context, std::uint32_t tokens, HipMoeRouting& out,
+                                   std::string* diagnostic) const noexcept {
+  try {
+    if (!valid() || tokens == 0 || tokens > impl_->max_tokens)
+      return set_diag(diagnostic, "routing download: invalid layer or token count"), false;
+    const std::size_t K = impl_->cfg.top_k, E = impl_->cfg.expert_count;
+    out.ids.resize(tokens * K);
+    out.weights.resize(tokens * K);
+    out.mass.resize(tokens);
+    out.shared_gate.resize(tokens);
+    out.logits.resize(tokens * E);
+    const osmd_stream st = context.stream();
+    int rc = osmd_memcpy_d2h(out.ids.data(), impl_->ids.get(), tokens * K * 4, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(out.weights.data(), impl_->weights.get(), tokens * K * 4, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(out.mass.data(), impl_->mass.get(), tokens * 4, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(out.shared_gate.data(), impl_->shared_gate.get(), tokens * 4, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(out.logits.data(), impl_->logits.get(), tokens * E * 4, st);
+    if (rc == 0) rc = osmd_stream_synchronize(st);
+    if (rc != 0) return set_diag(diagnostic, hip_error("routing download failed", rc)), false;
+    if (!impl_->cfg.has_shared_expert) std::fill(out.shared_gate.begin(), out.shared_gate.end(), 0.0F);
+    return true;
+  } catch (const std::exception& e) {
+    return set_diag(diagnostic, std::string("routing download exception: ") + e.what()), false;
+  }
+}
+
+HipMoeResult HipMoeLayer::run(HipComputeContext& context, std::span<const float> hidden,
+                              std::uint32_t tokens, const std::uint8_t* const* expert_table,
+                              bool sublayer) noexcept {
+  HipMoeResult r;
+  try {
+    if (!valid()) {
+      r.diagnostic = "MoE layer is not valid";
+      return r;
+    }
+    const std::size_t D = impl_->cfg.geometry.hidden;
+    if (tokens == 0 || hidden.size() != static_cast<std::size_t>(tokens) * D) {
+      r.diagnostic = "qwen router: hidden vector size mismatch";
+      return r;
+    }
+    if (!all_finite(hidden)) {
+      r.diagnostic = "qwen router: hidden vector contains non-finite value";
+      return r;
+    }
+    if (tokens > impl_->max_tokens) {
+      r.diagnostic = "MoE decode token count exceeds max_tokens";
+      return r;
+    }
+    if (!context.activate(&r.diagnostic)) return r;
+    const osmd_stream st = context.stream();
+    int rc = osmd_memcpy_h2d(impl_->x_in.get(), hidden.data(), hidden.size_bytes(), st);
+    if (rc != 0) {
+      r.diagnostic = hip_error("MoE input upload failed", rc);
+      return r;
+    }
+    auto d = decode_device(context, impl_->x_in.as<const float>(), impl_->y_out.as<float>(), tokens,
+                           expert_table, sublayer);
+    if (!d.executed) {
+      r.diagnostic = d.diagnostic;
+      return r;
+    }
+    r.values.resize(hidden.size());
+    rc = osmd_memcpy_d2h(r.values.data(), impl_->y_out.get(), hidden.size_bytes(), st);
+    if (rc == 0 && sublayer) {
+      r.normalized.resize(hidden.size());
+      rc = osmd_memcpy_d2h(r.normalized.data(), impl_->x_norm.get(), hidden.size_bytes(), st);
+    }
+    if (rc != 0) {
+      r.values.clear();
+      r.diagnostic = hip_error("MoE output download failed", rc);
+      return r;
+    }
+    if (!download_routing(context, tokens, r.routing, &r.diagnostic)) {
+      r.values.clear();
+      return r;
+    }
+    for (float v : r.values)
+      if (!std::isfinite(v)) {
+        r.values.clear();
+        r.diagnostic = "routed MoE produced non-finite output";
+        return r;
+      }
+    r.executed = true;
+    r.diagnostic = "HIP routed MoE decode executed";
+  } catch (const std::exception& e) {
+    r.values.clear();
+    r.diagnostic = std::string("MoE decode exception: ") + e.what();
+  }
+  return r;
+}
+
+// Internal access for the cache-driven path.
+struct MoeLayerAccess {
+  static HipMoeLayer::Impl* impl(HipMoeLayer& l) { return l.impl_.get(); }
+};
+
+HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpertCache& expert_cache,
+                                     HipMoeLayer& layer_state, std::uint32_t layer,
+                                     std::span<const float> hidden, bool sublayer) noexcept {
+  HipMoeResult r;
+  try {
+    auto* m = MoeLayerAccess::impl(layer_state);
+    if (m == nullptr || !layer_state.valid()) {
+      r.diagnostic = "MoE layer is not valid";
+      return r;
+    }
+    const std::size_t D = m->cfg.geometry.hidden, K = m->cfg.top_k;
+    const std::uint32_t tokens = static_cast<std::uint32_t>(hidden.size() / (D ? D : 1));
+    if (tokens == 0 || hidden.size() != tokens * D || tokens > m->max_tokens) {
+      r.diagnostic = "qwen router: hidden vector size mismatch";
+      return r;
+    }
+    if (!all_finite(hidden)) {
+      r.diagnostic = "qwen router: hidden vector contains non-finite value";
+      return r;
+    }
+    if (sublayer && m->norm_weight.get() == nullptr) {
+      r.diagnostic = "MoE sublayer decode needs an RMSNorm weight";
+      return r;
+    }
+    if (!context.activate(&r.diagnostic)) return r;
+    const osmd_stream st = context.stream();
+    // 1. route on the device
+    int rc = osmd_memcpy_h2d(m->x_in.get(), hidden.data(), hidden.size_bytes(), st);
+    osmd_moe_args a = m->args(m->x_in.as<const float>(), m->y_out.as<float>(), tokens, nullptr, sublayer);
+    if (rc == 0) rc = osmd_moe_route(&a, st);
+    std::vector<std::uint32_t> ids(tokens * K);
+    if (rc == 0) rc = osmd_memcpy_d2h(ids.data(), m->ids.get(), ids.size() * 4, st);
+    if (rc == 0) rc = osmd_stream_synchronize(st);
+    if (rc != 0) {
+      r.diagnostic = hip_error("Qwen sparse MoE routing failed", rc);
+      return r;
+    }
+    // 2. make every pick resident (in pick order, as the reference does)
+    const std::uint32_t nslot = m->nslot();
+    auto* host_ptrs = static_cast<const std::uint8_t**>(m->host_ptrs.get());
+    std::unordered_set<std::uint64_t> needed;
+    for (std::uint32_t t = 0; t < tokens; ++t) {
+      for (std::size_t j = 0; j < K; ++j) {
+        const std::uint32_t id = ids[t * K + j];
+        std::string d;
+        HipResidentExpert* e = expert_cache.get(layer, id, &d);
+        if (e == nullptr) {
+          r.diagnostic = "Qwen sparse MoE routed expert " + std::to_string(id) + " load failed: " + d;
+          return r;
+        }
+        if (e->input_dim() != D || e->output_dim() != D ||
+            e->intermediate_dim() != m->cfg.geometry.inter) {
+          r.diagnostic = "Qwen sparse MoE routed expert geometry mismatch";
+          return r;
+        }
+        host_ptrs[t * nslot + j] = e->device_blob();
+        needed.insert(LfuRecencyPolicy::make_key(layer, id));
+      }
+      if (nslot > K) host_ptrs[t * nslot + K] = m->shared_blob.as<const std::uint8_t>();
+    }
+    for (const std::uint64_t key : needed)
+      if (!expert_cache.contains(layer, static_cast<std::uint32_t>(key & 0xFFFFFFFFU))) {
+        r.diagnostic = "Qwen sparse MoE: the cache budget cannot hold every expert of this batch at once";
+        return r;
+      }
+    // 3. expert kernels over the resident slots
+    rc = osmd_memcpy_h2d(m->slot_ptrs.get(), host_ptrs, tokens * nslot * sizeof(void*), st);
+    if (rc == 0) rc = osmd_moe_experts(&a, st);
+    r.values.resize(hidden.size());
+    if (rc == 0) rc = osmd_memcpy_d2h(r.values.data(), m->y_out.get(), hidden.size_bytes(), st);
+    if (rc == 0 && sublayer) {
+      r.normalized.resize(hidden.size());
+      rc = osmd_memcpy_d2h(r.normalized.data(), m->x_norm.get(), hidden.size_bytes(), st);
+    }
+    if (rc != 0) {
+      r.values.clear();
+      r.diagnostic = hip_error("Qwen sparse MoE expert phase failed", rc);
+      return r;
+    }
+    if (!layer_state.download_routing(context, tokens, r.routing, &r.diagnostic)) {
+      r.values.clear();
+      return r;
+    }
+    r.executed = true;
+    r.diagnostic = "Qwen sparse MoE combined routed and shared experts on the device.";
+  } catch (const std::exception& e) {
+    r.values.clear();
+    r.diagnostic = std::string("Qwen sparse MoE exception: ") + e.what();
+  }
+  return r;
+}
+
+}  // namespace osm

@@ -1,0 +1,655 @@
+// osm_hip.hpp -- C++20 host facade of the MI355X q4 routed-MoE path.
+//
+// Mirrors the reference's backend operator surface (include/orbi/streammoe/
+// backend/vulkan_*.hpp, model/routed_moe.hpp, cache/expert_cache.hpp) with
+// HIP-backed classes of the same shape: factories return std::optional and
+// fill a diagnostic, operations are noexcept and return {executed,
+// diagnostic}, invalid geometry is rejected before any launch. Everything
+// below talks to the device only through the thin C ABI in
+// csrc/device/osm_device.h.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <memory>
+#include <optional>
+#include <span>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <vector>
+
+#include "../device/osm_device.h"
+
+namespace osm {
+
+// ---- results (vulkan_float_buffer.hpp:15-18, vulkan_q4_gemv.hpp:15-19) ----
+struct HipDispatchResult {
+  bool executed{};
+  std::string diagnostic;
+};
+
+struct HipValuesResult {
+  bool executed{};
+  std::vector<float> values;
+  std::string diagnostic;
+};
+
+// ---- device memory (RAII over osmd_malloc) ---------------------------------
+class DeviceBytes {
+ public:
+  DeviceBytes() = default;
+  ~DeviceBytes();
+  DeviceBytes(const DeviceBytes&) = delete;
+  DeviceBytes& operator=(const DeviceBytes&) = delete;
+  DeviceBytes(DeviceBytes&& o) noexcept;
+  DeviceBytes& operator=(DeviceBytes&& o) noexcept;
+  // Returns a HIP error code (0 on success).
+  int allocate(std::size_t bytes);
+  void reset() noexcept;
+  void* get() const noexcept { return ptr_; }
+  std::size_t size() const noexcept { return bytes_; }
+  template <typename T>
+  T* as() const noexcept { return static_cast<T*>(ptr_); }
+
+ private:
+  void* ptr_ = nullptr;
+  std::size_t bytes_ = 0;
+};
+
+class PinnedBytes {
+ public:
+  PinnedBytes() = default;
+  ~PinnedBytes();
+  PinnedBytes(const PinnedBytes&) = delete;
+  PinnedBytes& operator=(const PinnedBytes&) = delete;
+  PinnedBytes(PinnedBytes&& o) noexcept;
+  PinnedBytes& operator=(PinnedBytes&& o) noexcept;
+  int allocate(std::size_t bytes);
+  void reset() noexcept;
+  void* get() const noexcept { return ptr_; }
+  std::size_t size() const noexcept { return bytes_; }
+
+ private:
+  void* ptr_ = nullptr;
+  std::size_t bytes_ = 0;
+};
+
+// ---- context (vulkan_compute_context.hpp:19-49) ---------------------------
+// One device, one compute stream and one side stream for cache fills.
+class HipComputeContext {
+ public:
+  HipComputeContext();
+  ~HipComputeContext();
+  HipComputeContext(const HipComputeContext&) = delete;
+  HipComputeContext& operator=(const HipComputeContext&) = delete;
+  HipComputeContext(HipComputeContext&&) noexcept;
+  HipComputeContext& operator=(HipComputeContext&&) noexcept;
+
+  [[nodiscard]] static std::optional<HipComputeContext> create(
+      int device = 0, std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] int device() const noexcept;
+  [[nodiscard]] const std::string& device_name() const noexcept;
+  [[nodiscard]] osmd_stream stream() const noexcept;
+  [[nodiscard]] osmd_stream copy_stream() const noexcept;
+  // Makes this context's device current on the calling thread.
+  [[nodiscard]] bool activate(std::string* diagnostic = nullptr) const noexcept;
+  [[nodiscard]] bool synchronize(std::string* diagnostic = nullptr) const noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- float buffer (vulkan_float_buffer.hpp:23-58) -------------------------
+class HipFloatBuffer {
+ public:
+  HipFloatBuffer();
+  ~HipFloatBuffer();
+  HipFloatBuffer(const HipFloatBuffer&) = delete;
+  HipFloatBuffer& operator=(const HipFloatBuffer&) = delete;
+  HipFloatBuffer(HipFloatBuffer&&) noexcept;
+  HipFloatBuffer& operator=(HipFloatBuffer&&) noexcept;
+
+  [[nodiscard]] static std::optional<HipFloatBuffer> create(
+      HipComputeContext& context, std::size_t element_count,
+      std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] std::size_t size() const noexcept;
+  [[nodiscard]] std::size_t size_bytes() const noexcept;
+  [[nodiscard]] int device() const noexcept;
+  [[nodiscard]] float* data() const noexcept;
+
+  // Stream-ordered on the context's compute stream; both wait for completion.
+  [[nodiscard]] bool upload(std::span<const float> values,
+                            std::string* diagnostic = nullptr) noexcept;
+  [[nodiscard]] std::optional<std::vector<float>> download(
+      std::string* diagnostic = nullptr) const noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- q4 projection weights (vulkan_q4_weights.hpp:19-55) ------------------
+class HipQ4ProjectionWeights {
+ public:
+  HipQ4ProjectionWeights();
+  ~HipQ4ProjectionWeights();
+  HipQ4ProjectionWeights(const HipQ4ProjectionWeights&) = delete;
+  HipQ4ProjectionWeights& operator=(const HipQ4ProjectionWeights&) = delete;
+  HipQ4ProjectionWeights(HipQ4ProjectionWeights&&) noexcept;
+  HipQ4ProjectionWeights& operator=(HipQ4ProjectionWeights&&) noexcept;
+
+  // The reference's signature: fp32 scales and biases.
+  [[nodiscard]] static std::optional<HipQ4ProjectionWeights> create(
+      HipComputeContext& context, std::span<const std::uint32_t> packed,
+      std::size_t out_dim, std::size_t packed_cols,
+      std::span<const float> scales, std::span<const float> biases,
+      std::size_t group_size, std::string* diagnostic = nullptr) noexcept;
+
+  // Metadata kept in its stored dtype (bf16/f16/f32); meta_count entries each.
+  [[nodiscard]] static std::optional<HipQ4ProjectionWeights> create_raw(
+      HipComputeContext& context, std::span<const std::uint32_t> packed,
+      std::size_t out_dim, std::size_t packed_cols, const void* scales,
+      const void* biases, std::uint32_t meta_dtype, std::size_t group_size,
+      std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] std::size_t out_dim() const noexcept;
+  [[nodiscard]] std::size_t packed_cols() const noexcept;
+  [[nodiscard]] std::size_t in_dim() const noexcept;
+  [[nodiscard]] std::size_t group_size() const noexcept;
+  [[nodiscard]] std::uint32_t meta_dtype() const noexcept;
+  [[nodiscard]] std::size_t packed_size_bytes() const noexcept;
+  [[nodiscard]] std::size_t meta_size_bytes() const noexcept;  // scales + biases
+  [[nodiscard]] int device() const noexcept;
+  [[nodiscard]] osmd_q4_proj view() const noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- single operators ------------------------------------------------------
+// vulkan_q4_dequant.hpp:23-30
+[[nodiscard]] HipValuesResult run_hip_q4_dequant(
+    HipComputeContext& context, std::span<const std::uint32_t> packed,
+    std::size_t rows, std::size_t packed_cols, std::span<const float> scales,
+    std::span<const float> biases, std::size_t group_size) noexcept;
+// vulkan_q4_gemv.hpp:25-33
+[[nodiscard]] HipValuesResult run_hip_q4_gemv(
+    HipComputeContext& context, std::span<const std::uint32_t> packed,
+    std::size_t out_dim, std::size_t packed_cols, std::span<const float> scales,
+    std::span<const float> biases, std::size_t group_size,
+    std::span<const float> x) noexcept;
+// vulkan_q4_gemv.hpp:39-48
+[[nodiscard]] HipDispatchResult run_hip_q4_gemv_buffers(
+    HipComputeContext& context, std::span<const std::uint32_t> packed,
+    std::size_t out_dim, std::size_t packed_cols, std::span<const float> scales,
+    std::span<const float> biases, std::size_t group_size,
+    const HipFloatBuffer& x, HipFloatBuffer& y) noexcept;
+// vulkan_q4_gemv.hpp:53-57
+[[nodiscard]] HipDispatchResult run_hip_q4_gemv_preloaded(
+    HipComputeContext& context, const HipQ4ProjectionWeights& weights,
+    const HipFloatBuffer& x, HipFloatBuffer& y) noexcept;
+// vulkan_swiglu.hpp:19-30
+[[nodiscard]] HipValuesResult run_hip_swiglu(HipComputeContext& context,
+                                             std::span<const float> gate,
+                                             std::span<const float> up) noexcept;
+[[nodiscard]] HipDispatchResult run_hip_swiglu_buffers(
+    HipComputeContext& context, const HipFloatBuffer& gate,
+    const HipFloatBuffer& up, HipFloatBuffer& output) noexcept;
+// vulkan_weighted_accumulate.hpp:12-16
+[[nodiscard]] HipDispatchResult run_hip_weighted_accumulate(
+    HipComputeContext& context, const HipFloatBuffer& source, float weight,
+    HipFloatBuffer& accumulator) noexcept;
+// vulkan_rmsnorm.hpp:25-31
+[[nodiscard]] HipValuesResult run_hip_rms_norm(
+    HipComputeContext& context, std::span<const float> input, std::size_t rows,
+    std::size_t dim, std::span<const float> weight, float eps) noexcept;
+// Nibble unpack (integer-exact check of the packed layout): out[8*w + j] is
+// nibble j (low first) of word w.
+[[nodiscard]] bool run_hip_unpack_nibbles(HipComputeContext& context,
+                                          std::span<const std::uint32_t> packed,
+                                          std::span<std::uint8_t> out,
+                                          std::string* diagnostic = nullptr) noexcept;
+
+// ---- experts (vulkan_resident_expert.hpp:41-69) ----------------------------
+// Validates an expert geometry for the fused kernels.
+[[nodiscard]] bool check_expert_geometry(const osm_expert_geometry& g,
+                                         std::string* diagnostic) noexcept;
+[[nodiscard]] std::size_t expert_blob_bytes(const osm_expert_geometry& g) noexcept;
+
+class HipResidentExpert {
+ public:
+  HipResidentExpert();
+  ~HipResidentExpert();
+  HipResidentExpert(const HipResidentExpert&) = delete;
+  HipResidentExpert& operator=(const HipResidentExpert&) = delete;
+  HipResidentExpert(HipResidentExpert&&) noexcept;
+  HipResidentExpert& operator=(HipResidentExpert&&) noexcept;
+
+  // Copies the blob (qpack section order) into its own device allocation.
+  [[nodiscard]] static std::optional<HipResidentExpert> create(
+      HipComputeContext& context, std::span<const std::byte> blob,
+      const osm_expert_geometry& geometry, std::string* diagnostic = nullptr) noexcept;
+  // Non-owning view of a blob already in device memory (a cache slot).
+  [[nodiscard]] static std::optional<HipResidentExpert> view(
+      HipComputeContext& context, const std::uint8_t* device_blob,
+      const osm_expert_geometry& geometry, std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] std::size_t input_dim() const noexcept;
+  [[nodiscard]] std::size_t intermediate_dim() const noexcept;
+  [[nodiscard]] std::size_t output_dim() const noexcept;
+  [[nodiscard]] std::size_t packed_weight_bytes() const noexcept;
+  // Bytes of HBM the expert's weights occupy (the blob; one cache slot).
+  [[nodiscard]] std::size_t accounted_bytes() const noexcept;
+  [[nodiscard]] const std::uint8_t* device_blob() const noexcept;
+  [[nodiscard]] const osm_expert_geometry& geometry() const noexcept;
+
+  [[nodiscard]] HipValuesResult run(HipComputeContext& context,
+                                    std::span<const float> x) noexcept;
+  [[nodiscard]] HipDispatchResult run_from_buffer(HipComputeContext& context,
+                                                  const HipFloatBuffer& x) noexcept;
+  // Valid until this expert is moved/destroyed or run again.
+  [[nodiscard]] const HipFloatBuffer* output_buffer() const noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- shared expert (vulkan_resident_shared_expert.hpp:49-69) --------------
+class HipResidentSharedExpert {
+ public:
+  HipResidentSharedExpert();
+  ~HipResidentSharedExpert();
+  HipResidentSharedExpert(const HipResidentSharedExpert&) = delete;
+  HipResidentSharedExpert& operator=(const HipResidentSharedExpert&) = delete;
+  HipResidentSharedExpert(HipResidentSharedExpert&&) noexcept;
+  HipResidentSharedExpert& operator=(HipResidentSharedExpert&&) noexcept;
+
+  [[nodiscard]] static std::optional<HipResidentSharedExpert> create(
+      HipComputeContext& context, std::span<const std::byte> blob,
+      const osm_expert_geometry& geometry, std::span<const float> scalar_gate,
+      std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] std::size_t input_dim() const noexcept;
+  [[nodiscard]] std::size_t intermediate_dim() const noexcept;
+  [[nodiscard]] std::size_t output_dim() const noexcept;
+  [[nodiscard]] std::size_t accounted_bytes() const noexcept;
+  [[nodiscard]] const std::uint8_t* device_blob() const noexcept;
+  [[nodiscard]] const float* device_scalar_gate() const noexcept;
+  [[nodiscard]] std::span<const float> scalar_gate() const noexcept;
+
+  // sigmoid(scalar_gate . hidden), summed in index order on the host like
+  // vulkan_resident_shared_expert.cpp:292-317.
+  [[nodiscard]] std::optional<float> scalar_scale(
+      std::span<const float> hidden, std::string* diagnostic = nullptr) const noexcept;
+  [[nodiscard]] HipDispatchResult run_from_buffer(HipComputeContext& context,
+                                                  const HipFloatBuffer& hidden) noexcept;
+  [[nodiscard]] const HipFloatBuffer* output_buffer() const noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- host L1 expert cache (cache/expert_cache.hpp:30-87) ------------------
+struct ExpertId {
+  std::uint32_t layer{};
+  std::uint32_t expert{};
+};
+
+struct ExpertReadRequest {
+  ExpertId id{};
+  std::span<std::byte> destination{};
+};
+
+// storage/expert_storage.hpp:20-29: every destination is fully populated or
+// the call throws.
+class ExpertStorage {
+ public:
+  virtual ~ExpertStorage() = default;
+  [[nodiscard]] virtual std::size_t expert_stride_bytes() const noexcept = 0;
+  virtual void read_experts(std::span<ExpertReadRequest> requests) = 0;
+};
+
+struct ExpertCacheEntry {
+  ExpertId id{};
+  std::size_t slot{};
+  std::span<const std::byte> bytes{};
+};
+
+struct ExpertCacheStats {
+  std::size_t hits{};
+  std::size_t misses{};
+  std::size_t allocated_slots{};
+  std::size_t capacity_slots{};
+  std::size_t logical_bytes{};
+  std::size_t budget_bytes{};
+};
+
+// Fixed-stride slots in pinned host memory (so a GPU fill from a slot is an
+// asynchronous DMA), lazily grown up to budget/stride; LFU+recency victims;
+// members of the current batch protected; rollback when the storage throws.
+class HostExpertCache {
+ public:
+  HostExpertCache(ExpertStorage& storage, std::size_t budget_bytes,
+                  std::size_t minimum_slots = 1, bool pinned = true);
+  ~HostExpertCache();
+  HostExpertCache(const HostExpertCache&) = delete;
+  HostExpertCache& operator=(const HostExpertCache&) = delete;
+
+  [[nodiscard]] std::vector<ExpertCacheEntry> fetch(
+      std::uint32_t layer, std::span<const std::uint32_t> experts);
+  [[nodiscard]] std::optional<std::size_t> resident_slot(
+      std::uint32_t layer, std::uint32_t expert) const noexcept;
+  [[nodiscard]] ExpertCacheStats stats() const noexcept;
+  [[nodiscard]] std::size_t stride_bytes() const noexcept { return stride_; }
+
+ private:
+  struct SlotMeta {
+    std::optional<std::uint64_t> key{};
+    std::size_t frequency{};
+    std::uint64_t last_use{};
+  };
+  std::byte* slot_data(std::size_t slot) const noexcept;
+  std::size_t pick_fill_slot(const std::unordered_set<std::size_t>& in_batch);
+
+  ExpertStorage& storage_;
+  std::size_t stride_{};
+  std::size_t budget_bytes_{};
+  std::size_t max_slots_{};
+  bool pinned_{};
+  std::vector<std::byte*> slots_;
+  std::vector<PinnedBytes> pinned_slots_;
+  std::vector<std::vector<std::byte>> pageable_slots_;
+  std::vector<SlotMeta> meta_;
+  std::unordered_map<std::uint64_t, std::size_t> key_to_slot_;
+  std::unordered_map<std::uint64_t, std::size_t> frequency_;
+  std::uint64_t tick_{};
+  std::size_t hits_{};
+  std::size_t misses_{};
+};
+
+// ---- GPU resident cache policy (vulkan_resident_expert_cache.cpp:44-188) --
+// The LFU+recency decision logic alone, separable so host tests can drive it
+// without a device: key (layer<<32)|expert, one tick per get, per-key
+// frequency history that survives eviction, victims by min (frequency,
+// last_use, key) while resident + incoming > budget.
+class LfuRecencyPolicy {
+ public:
+  explicit LfuRecencyPolicy(std::size_t budget_bytes);
+
+  struct Outcome {
+    bool hit{};
+    std::vector<std::uint64_t> evicted;  // keys, in eviction order
+  };
+  // First half of a get: one tick, frequency history, and on a hit the
+  // entry's (frequency, last_use) refresh. Returns true on a hit.
+  [[nodiscard]] bool touch(std::uint32_t layer, std::uint32_t expert);
+  // Second half of a miss, once the expert's bytes are in hand: evict until
+  // it fits, then insert. Throws std::invalid_argument for zero or
+  // over-budget sizes (the reference's "accounting is zero" / "exceeds the
+  // configured budget"). Returns the evicted keys in eviction order.
+  [[nodiscard]] std::vector<std::uint64_t> admit(std::uint32_t layer, std::uint32_t expert,
+                                                 std::size_t accounted_bytes);
+  // touch + admit on a miss.
+  [[nodiscard]] Outcome access(std::uint32_t layer, std::uint32_t expert,
+                               std::size_t accounted_bytes);
+  // Undo the insertion of a key whose fill failed.
+  void forget(std::uint64_t key) noexcept;
+  [[nodiscard]] bool contains(std::uint32_t layer, std::uint32_t expert) const noexcept;
+  [[nodiscard]] static std::uint64_t make_key(std::uint32_t layer,
+                                              std::uint32_t expert) noexcept {
+    return (static_cast<std::uint64_t>(layer) << 32U) | expert;
+  }
+
+  std::size_t hits{};
+  std::size_t misses{};
+  std::size_t loads{};
+  std::size_t evictions{};
+  [[nodiscard]] std::size_t resident_entries() const noexcept { return entries_.size(); }
+  [[nodiscard]] std::size_t resident_bytes() const noexcept { return resident_bytes_; }
+  [[nodiscard]] std::size_t budget_bytes() const noexcept { return budget_bytes_; }
+
+ private:
+  struct Node {
+    std::size_t bytes{};
+    std::size_t frequency{};
+    std::uint64_t last_use{};
+  };
+  [[nodiscard]] std::uint64_t victim() const;
+  std::size_t budget_bytes_{};
+  std::size_t resident_bytes_{};
+  std::unordered_map<std::uint64_t, Node> entries_;
+  std::unordered_map<std::uint64_t, std::size_t> history_;
+  std::uint64_t tick_{};
+};
+
+// ---- expert sources for cache fills ---------------------------------------
+// Where a resident-cache miss copies its blob from: a host pointer to the
+// expert's bytes (pinned memory makes the copy an asynchronous DMA).
+class ExpertBlobSource {
+ public:
+  virtual ~ExpertBlobSource() = default;
+  [[nodiscard]] virtual const osm_expert_geometry& geometry() const noexcept = 0;
+  // Throws on failure; the pointer stays valid until the next call.
+  [[nodiscard]] virtual const std::byte* host_blob(std::uint32_t layer,
+                                                   std::uint32_t expert) = 0;
+  // True when returned pointers stay valid after later calls, so a fill
+  // may still be in flight when the next one starts.
+  [[nodiscard]] virtual bool stable_pointers() const noexcept { return false; }
+};
+
+// Whole model (layers x experts blobs) in one pinned host allocation.
+class PinnedExpertStore final : public ExpertBlobSource {
+ public:
+  PinnedExpertStore(const osm_expert_geometry& geometry, std::uint32_t layers,
+                    std::uint32_t experts);
+  [[nodiscard]] const osm_expert_geometry& geometry() const noexcept override { return geom_; }
+  [[nodiscard]] const std::byte* host_blob(std::uint32_t layer, std::uint32_t expert) override;
+  [[nodiscard]] bool stable_pointers() const noexcept override { return true; }
+  [[nodiscard]] std::byte* mutable_blob(std::uint32_t layer, std::uint32_t expert);
+  [[nodiscard]] std::size_t stride() const noexcept { return stride_; }
+  [[nodiscard]] std::uint32_t layers() const noexcept { return layers_; }
+  [[nodiscard]] std::uint32_t experts() const noexcept { return experts_; }
+  [[nodiscard]] std::byte* data() const noexcept { return static_cast<std::byte*>(mem_.get()); }
+
+ private:
+  osm_expert_geometry geom_{};
+  std::uint32_t layers_{}, experts_{};
+  std::size_t stride_{};
+  PinnedBytes mem_;
+};
+
+// The reference's miss path: host L1 cache over an ExpertStorage
+// (vulkan_resident_expert_cache.cpp:98-107).
+class HostCacheSource final : public ExpertBlobSource {
+ public:
+  HostCacheSource(HostExpertCache& cache, const osm_expert_geometry& geometry);
+  [[nodiscard]] const osm_expert_geometry& geometry() const noexcept override { return geom_; }
+  [[nodiscard]] const std::byte* host_blob(std::uint32_t layer, std::uint32_t expert) override;
+
+ private:
+  HostExpertCache& cache_;
+  osm_expert_geometry geom_{};
+};
+
+// ---- GPU resident expert cache (vulkan_resident_expert_cache.hpp:27-83) ----
+struct HipResidentExpertCacheStats {
+  std::size_t hits{};
+  std::size_t misses{};
+  std::size_t loads{};
+  std::size_t evictions{};
+  std::size_t resident_entries{};
+  std::size_t resident_bytes{};
+  std::size_t budget_bytes{};
+};
+
+// One HBM slab of budget/stride slots. A miss copies the blob from the source
+// into a free or evicted slot on the context's side stream; the compute
+// stream waits for that copy, so work enqueued after get() sees the expert,
+// and the side stream waits for work enqueued before get(), so a slot is
+// never overwritten while an earlier kernel may still read it.
+class HipResidentExpertCache {
+ public:
+  // Throws std::invalid_argument for an invalid context or a zero budget
+  // (vulkan_resident_expert_cache.cpp:18-35).
+  HipResidentExpertCache(HipComputeContext& context, ExpertBlobSource& source,
+                         std::size_t budget_bytes);
+  ~HipResidentExpertCache();
+  HipResidentExpertCache(const HipResidentExpertCache&) = delete;
+  HipResidentExpertCache& operator=(const HipResidentExpertCache&) = delete;
+
+  [[nodiscard]] HipResidentExpert* get(std::uint32_t layer, std::uint32_t expert,
+                                       std::string* diagnostic = nullptr) noexcept;
+  [[nodiscard]] HipValuesResult run(std::uint32_t layer, std::uint32_t expert,
+                                    std::span<const float> x) noexcept;
+  [[nodiscard]] bool contains(std::uint32_t layer, std::uint32_t expert) const noexcept;
+  [[nodiscard]] HipResidentExpertCacheStats stats() const noexcept;
+
+  [[nodiscard]] std::size_t slot_count() const noexcept;
+  [[nodiscard]] std::size_t stride() const noexcept;
+  [[nodiscard]] std::uint64_t bytes_filled() const noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- HBM-resident expert stack (all experts of several layers) -------------
+class HipExpertSlab {
+ public:
+  HipExpertSlab();
+  ~HipExpertSlab();
+  HipExpertSlab(const HipExpertSlab&) = delete;
+  HipExpertSlab& operator=(const HipExpertSlab&) = delete;
+  HipExpertSlab(HipExpertSlab&&) noexcept;
+  HipExpertSlab& operator=(HipExpertSlab&&) noexcept;
+
+  [[nodiscard]] static std::optional<HipExpertSlab> create(
+      HipComputeContext& context, const osm_expert_geometry& geometry,
+      std::uint32_t layers, std::uint32_t experts,
+      std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] std::uint32_t layers() const noexcept;
+  [[nodiscard]] std::uint32_t experts() const noexcept;
+  [[nodiscard]] std::size_t stride() const noexcept;
+  [[nodiscard]] std::size_t bytes() const noexcept;
+  [[nodiscard]] const osm_expert_geometry& geometry() const noexcept;
+  [[nodiscard]] std::uint8_t* blob(std::uint32_t layer, std::uint32_t expert) const noexcept;
+  [[nodiscard]] const std::uint8_t* const* device_table(std::uint32_t layer) const noexcept;
+  [[nodiscard]] bool upload(std::uint32_t layer, std::uint32_t expert,
+                            std::span<const std::byte> blob,
+                            std::string* diagnostic = nullptr) noexcept;
+  // Fills every expert with the seeded synthetic generator, on the device.
+  [[nodiscard]] bool synthesize(std::uint64_t seed, std::string* diagnostic = nullptr) noexcept;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// ---- routed-MoE layer (checkpoint_sparse_moe.hpp + checkpoint_moe_sublayer.hpp)
+struct HipMoeLayerConfig {
+  osm_expert_geometry geometry{};
+  std::uint32_t expert_count{};
+  std::uint32_t top_k{};
+  bool norm_topk_prob{true};
+  bool has_shared_expert{true};
+  float rms_eps{1e-6F};
+};
+
+struct HipMoeRouting {
+  std::vector<std::uint32_t> ids;   // [tokens, top_k], picks by descending probability
+  std::vector<float> weights;       // [tokens, top_k]
+  std::vector<float> mass;          // [tokens] selected probability mass
+  std::vector<float> shared_gate;   // [tokens]
+  std::vector<float> logits;        // [tokens, expert_count]
+};
+
+struct HipMoeResult {
+  bool executed{};
+  HipMoeRouting routing;
+  std::vector<float> normalized;  // [tokens, hidden] RMSNorm output (sublayer only)
+  std::vector<float> values;      // [tokens, hidden]
+  std::string diagnostic;
+};
+
+// Per-layer state that stays resident: router [E, D] and shared-expert gate
+// vector [D] (bf16 or f32), optional RMSNorm weight, the shared expert, and
+// scratch for up to max_tokens tokens.
+class HipMoeLayer {
+ public:
+  HipMoeLayer();
+  ~HipMoeLayer();
+  HipMoeLayer(const HipMoeLayer&) = delete;
+  HipMoeLayer& operator=(const HipMoeLayer&) = delete;
+  HipMoeLayer(HipMoeLayer&&) noexcept;
+  HipMoeLayer& operator=(HipMoeLayer&&) noexcept;
+
+  // router / shared_gate_vec are in router_dtype (OSM_META_F32 or BF16/F16
+  // bits); norm_weight may be empty (no RMSNorm); shared_blob may be empty
+  // when config.has_shared_expert is false.
+  [[nodiscard]] static std::optional<HipMoeLayer> create(
+      HipComputeContext& context, const HipMoeLayerConfig& config,
+      const void* router, std::uint32_t router_dtype, const void* shared_gate_vec,
+      std::span<const float> norm_weight, std::span<const std::byte> shared_blob,
+      std::uint32_t max_tokens, std::string* diagnostic = nullptr) noexcept;
+
+  [[nodiscard]] bool valid() const noexcept;
+  [[nodiscard]] const HipMoeLayerConfig& config() const noexcept;
+  [[nodiscard]] std::uint32_t max_tokens() const noexcept;
+  [[nodiscard]] const std::uint8_t* shared_blob() const noexcept;
+
+  // Stream-ordered decode of `tokens` rows of device x into device y with
+  // every routed expert resolved through `expert_table` (device, [E]).
+  // sublayer=true: y = x + MoE(RMSNorm(x)); false: y = MoE(x).
+  [[nodiscard]] HipDispatchResult decode_device(HipComputeContext& context,
+                                                const float* x, float* y,
+                                                std::uint32_t tokens,
+                                                const std::uint8_t* const* expert_table,
+                                                bool sublayer) noexcept;
+  // One phase of a decode whose routing already ran (0 route, 1 gate/up,
+  // 2 down), for per-kernel timing.
+  [[nodiscard]] HipDispatchResult launch_phase(HipComputeContext& context, const float* x,
+                                               float* y, std::uint32_t tokens,
+                                               const std::uint8_t* const* expert_table,
+                                               bool sublayer, int phase) noexcept;
+  // Host in/out variant that also returns the routing of every token.
+  [[nodiscard]] HipMoeResult run(HipComputeContext& context,
+                                 std::span<const float> hidden, std::uint32_t tokens,
+                                 const std::uint8_t* const* expert_table,
+                                 bool sublayer) noexcept;
+  // Routing outputs of the last decode (device pointers).
+  [[nodiscard]] const std::uint32_t* device_ids() const noexcept;
+  [[nodiscard]] bool download_routing(HipComputeContext& context, std::uint32_t tokens,
+                                      HipMoeRouting& out,
+                                      std::string* diagnostic = nullptr) const noexcept;
+
+ private:
+  friend struct MoeLayerAccess;
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+// routed_moe.hpp:58-65 -- one token through the resident cache: route on the
+// device, make every pick resident (misses filled on the side stream), then
+// the fused expert kernels. The cache decides residency on the host from the
+// routed ids, as the reference's cache does.
+[[nodiscard]] HipMoeResult run_qwen_sparse_moe_hip(
+    HipComputeContext& context, HipResidentExpertCache& expert_cache,
+    HipMoeLayer& layer_state, std::uint32_t layer, std::span<const float> hidden,
+    bool sublayer) noexcept;
+
+}  // namespace osm

@@ -1,0 +1,139 @@
+"""Fixture builders and metrics shared by the tests."""
+
+from __future__ import annotations
+
+import numpy as np
+
+META_F32, META_F16, META_BF16 = 0, 1, 2
+
+
+def pack_q4(q: np.ndarray) -> np.ndarray:
+    """[rows, cols] nibbles 0..15 -> [rows, cols/8] uint32, low nibble first."""
+    q = np.asarray(q, np.uint32)
+    rows, cols = q.shape
+    q = q.reshape(rows, cols // 8, 8)
+    words = np.zeros((rows, cols // 8), np.uint32)
+    for lane in range(8):
+        words |= q[:, :, lane] << np.uint32(4 * lane)
+    return words
+
+
+def unpack_q4(words: np.ndarray) -> np.ndarray:
+    w = np.asarray(words, np.uint32)
+    lanes = [(w >> np.uint32(4 * j)) & np.uint32(0xF) for j in range(8)]
+    return np.stack(lanes, axis=-1).reshape(*w.shape[:-1], w.shape[-1] * 8).astype(np.uint8)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32)
+
+
+def meta_encode(values: np.ndarray, meta: int) -> np.ndarray:
+    v = np.ascontiguousarray(values, np.float32)
+    if meta == META_F32:
+        return v.view(np.uint8).ravel()
+    if meta == META_F16:
+        return v.astype(np.float16).view(np.uint8).ravel()
+    return bf16_bits(v).view(np.uint8).ravel()
+
+
+def meta_decode(values: np.ndarray, meta: int) -> np.ndarray:
+    """The fp32 the device sees for metadata stored as `meta`."""
+    v = np.ascontiguousarray(values, np.float32)
+    if meta == META_F32:
+        return v
+    if meta == META_F16:
+        return v.astype(np.float16).astype(np.float32)
+    return bf16_to_f32(bf16_bits(v))
+
+
+def make_blob(projections, meta: int) -> np.ndarray:
+    """projections: three (packed u32 [out, in/8], scales [out, g], biases [out, g])
+    in gate, up, down order -> the qpack-ordered expert blob."""
+    parts = []
+    for packed, s, b in projections:
+        parts.append(np.ascontiguousarray(packed, np.uint32).view(np.uint8).ravel())
+        parts.append(meta_encode(s, meta))
+        parts.append(meta_encode(b, meta))
+    return np.concatenate(parts)
+
+
+def rel_l2(actual, expected) -> float:
+    a = np.asarray(actual, np.float64).ravel()
+    e = np.asarray(expected, np.float64).ravel()
+    return float(np.linalg.norm(a - e) / max(np.linalg.norm(e), 1e-30))
+
+
+def max_abs(actual, expected) -> float:
+    return float(np.max(np.abs(np.asarray(actual, np.float64) - np.asarray(expected, np.float64))))
+
+
+# ---- fixtures restated from the reference's own tests --------------------------------
+def gemv_fixture():
+    """tests/vulkan_q4_gemv_test.cpp:27-115 (7 rows x 128 columns, group 64)."""
+    out_dim, packed_cols, group = 7, 16, 64
+    in_dim = packed_cols * 8
+    q = np.zeros((out_dim, in_dim), np.uint32)
+    for row in range(out_dim):
+        for word in range(packed_cols):
+            for lane in range(8):
+                q[row, word * 8 + lane] = (row * 7 + word * 3 + lane * (word % 5 + 1)) & 0xF
+    gpr = in_dim // group
+    scales = np.zeros((out_dim, gpr), np.float32)
+    biases = np.zeros((out_dim, gpr), np.float32)
+    for row in range(out_dim):
+        for g in range(gpr):
+            scales[row, g] = np.float32(0.125) + np.float32(0.075) * np.float32(row + 2 * g + 1)
+            biases[row, g] = (np.float32(-0.45) if g == 0 else np.float32(0.30)) + np.float32(0.035) * np.float32(row)
+    x = np.array([np.float32((i % 17) - 8) * np.float32(0.0625) + np.float32((i * 7) % 5) * np.float32(0.0175)
+                  for i in range(in_dim)], np.float32)
+    return pack_q4(q), out_dim, packed_cols, scales, biases, group, x
+
+
+def cache_fixture_expert(expert: int, meta: int = META_BF16):
+    """The three-expert qpack of tests/vulkan_resident_expert_cache_test.cpp:51-132:
+    hidden 128, intermediate 64, group 64, BF16 metadata."""
+    def proj(seed, out_dim, packed_cols):
+        in_dim = packed_cols * 8
+        q = np.zeros((out_dim, in_dim), np.uint32)
+        for row in range(out_dim):
+            for word in range(packed_cols):
+                for lane in range(8):
+                    q[row, word * 8 + lane] = (seed * 3 + expert * 5 + row * 7 + word * 2 + lane) & 0xF
+        gpr = in_dim // 64
+        s = np.zeros((out_dim, gpr), np.float32)
+        b = np.zeros((out_dim, gpr), np.float32)
+        for row in range(out_dim):
+            for g in range(gpr):
+                s[row, g] = np.float32(((seed + expert + row + g) % 6) + 1) * np.float32(0.125)
+                b[row, g] = np.float32(((seed * 2 + expert + row + g) % 7) - 3) * np.float32(0.125)
+        return pack_q4(q), s, b
+
+    return make_blob([proj(1, 64, 16), proj(2, 64, 16), proj(3, 128, 8)], meta)
+
+
+def cache_fixture_token(seed: int) -> np.ndarray:
+    """token() of tests/vulkan_resident_expert_cache_test.cpp:270-279."""
+    return np.array([np.float32(((i * (seed + 5)) % 31) - 15) * np.float32(0.03125) for i in range(128)], np.float32)
+
+
+def random_projection(rng, out_dim, in_dim, group, meta):
+    """Seeded random q4 projection in the BASELINE distribution."""
+    q = rng.integers(0, 16, size=(out_dim, in_dim), dtype=np.uint32)
+    s = np.abs(rng.normal(0, 0.02, size=(out_dim, in_dim // group))).astype(np.float32)
+    b = (-8.0 * meta_decode(s, meta) + rng.normal(0, 0.002, size=s.shape)).astype(np.float32)
+    return pack_q4(q), meta_decode(s, meta), meta_decode(b, meta)
+
+
+def random_blob(rng, hidden, inter, group, meta):
+    projs = [random_projection(rng, inter, hidden, group, meta),
+             random_projection(rng, inter, hidden, group, meta),
+             random_projection(rng, hidden, inter, group, meta)]
+    return make_blob(projs, meta), projs

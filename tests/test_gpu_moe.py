@@ -1,0 +1,217 @@
+"""Resident experts and the routed-MoE layer on the device against the oracle.
+
+Bars: routed expert ids bit-exact (order included: descending probability,
+ties to the lower id); routing weights and the shared gate within 1e-6
+absolute (tests/checkpoint_moe_sublayer_test.cpp:690-699); outputs within
+1e-3 relative L2 of the fp32 CPU oracle, and within the reference's absolute
+tolerances on its own small fixtures."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import osm_hip
+from helpers import cache_fixture_expert, cache_fixture_token, max_abs, random_blob, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+QWEN = dict(hidden=2048, inter=512, group=64, experts=512, top_k=10)
+
+
+def test_synth_device_matches_host(ctx):
+    g = osm_hip.geometry(2048, 512, 64, osm_hip.BF16)
+    for layer, expert in [(0, 0), (3, 511), (47, 0xFFFFFFFF)]:
+        assert np.array_equal(osm_hip.synth_expert_blob(ctx, 9, layer, expert, g), O.synth_expert_blob(9, layer, expert, 2048, 512))
+    g32 = osm_hip.geometry(256, 64, 32, osm_hip.F32)
+    assert np.array_equal(osm_hip.synth_expert_blob(ctx, 2, 1, 5, g32), O.synth_expert_blob(2, 1, 5, 256, 64, 32, O.META_F32))
+    assert np.array_equal(osm_hip.synth_router_bf16(ctx, 9, 4, 512, 2048), O.synth_router_bf16(9, 4, 512, 2048))
+    assert np.array_equal(osm_hip.synth_shared_gate_bf16(ctx, 9, 4, 2048), O.synth_shared_gate_bf16(9, 4, 2048))
+    assert np.array_equal(osm_hip.synth_norm_weight(ctx, 9, 4, 2048).view(np.uint32), O.synth_norm_weight(9, 4, 2048).view(np.uint32))
+    assert np.array_equal(osm_hip.synth_tokens(ctx, 9, 100, 5, 2048).view(np.uint32), O.synth_tokens(9, 100, 5, 2048).view(np.uint32))
+
+
+# ---- single experts --------------------------------------------------------------------
+def test_resident_expert_reference_fixture(ctx):
+    # The 128 -> 64 -> 128 experts of tests/vulkan_resident_expert_cache_test.cpp (tolerance 0.01).
+    g = osm_hip.geometry(128, 64, 64, osm_hip.BF16)
+    for e in range(3):
+        blob = cache_fixture_expert(e)
+        ex = osm_hip.ResidentExpert(ctx, blob, g)
+        assert ex.accounted_bytes == blob.size
+        x = cache_fixture_token(e)
+        gpu = ex.run(x)
+        ora = O.expert_forward(blob, 128, 64, 64, O.META_BF16, x)
+        assert max_abs(gpu, ora) <= 0.01 and rel_l2(gpu, ora) <= 1e-3
+
+
+@pytest.mark.parametrize("meta", [osm_hip.BF16, osm_hip.F32, osm_hip.F16])
+def test_resident_expert_qwen_shape(ctx, meta):
+    # One expert, one token at the Qwen3-Next shape (2048 -> 512 -> 2048).
+    g = osm_hip.geometry(2048, 512, 64, meta)
+    rng = np.random.default_rng(20 + meta)
+    blob, _ = random_blob(rng, 2048, 512, 64, meta)
+    x = rng.normal(0, 1, 2048).astype(np.float32)
+    ex = osm_hip.ResidentExpert(ctx, blob, g)
+    gpu = ex.run(x)
+    ora = O.expert_forward(blob, 2048, 512, 64, meta, x)
+    assert rel_l2(gpu, ora) <= 1e-3
+    xb = osm_hip.FloatBuffer(ctx, 2048)
+    xb.upload(x)
+    ex.run_from_buffer(xb)
+    assert np.array_equal(ex.output(), gpu)
+
+
+def test_resident_expert_rejects_bad_geometry(ctx):
+    with pytest.raises(osm_hip.OsmError):
+        osm_hip.ResidentExpert(ctx, np.zeros(100, np.uint8), osm_hip.geometry(100, 64, 64, osm_hip.BF16))
+    with pytest.raises(osm_hip.OsmError):
+        osm_hip.ResidentExpert(ctx, np.zeros(100, np.uint8), osm_hip.geometry(128, 64, 64, osm_hip.BF16))
+
+
+def test_shared_expert(ctx):
+    seed = 31
+    g = osm_hip.geometry(2048, 512, 64, osm_hip.BF16)
+    blob = O.synth_expert_blob(seed, 0, O.SHARED_EXPERT_ID, 2048, 512)
+    sg = O.bf16_bits_to_f32(O.synth_shared_gate_bf16(seed, 0, 2048))
+    x = O.synth_tokens(seed, 0, 1, 2048)[0]
+    se = osm_hip.SharedExpert(ctx, blob, g, sg)
+    logit = np.float32(0)
+    for i in range(2048):
+        logit = np.float32(logit + np.float32(sg[i] * x[i]))
+    assert se.scalar_scale(x) == O.sigmoid(float(logit))
+    xb = osm_hip.FloatBuffer(ctx, 2048)
+    xb.upload(x)
+    se.run_from_buffer(xb)
+    assert rel_l2(se.output(), O.expert_forward(blob, 2048, 512, 64, O.META_BF16, x)) <= 1e-3
+
+
+# ---- MoE layer ---------------------------------------------------------------------------
+class QwenLayer:
+    """One synthetic Qwen3-Next-shaped MoE layer: device slab + layer state, and
+    the oracle's view of the same weights (experts regenerated on the host)."""
+
+    def __init__(self, ctx, seed, layer=0, max_tokens=16, norm=False, **shape):
+        sh = dict(QWEN, **shape)
+        self.seed, self.layer = seed, layer
+        self.D, self.I, self.G, self.E, self.k = sh["hidden"], sh["inter"], sh["group"], sh["experts"], sh["top_k"]
+        self.g = osm_hip.geometry(self.D, self.I, self.G, osm_hip.BF16)
+        self.slab = osm_hip.ExpertSlab(ctx, self.g, 1, self.E)
+        self._synth_slab()
+        self.router_bits = O.synth_router_bf16(seed, layer, self.E, self.D)
+        self.sg_bits = O.synth_shared_gate_bf16(seed, layer, self.D)
+        self.norm_w = O.synth_norm_weight(seed, layer, self.D) if norm else None
+        self.shared = O.synth_expert_blob(seed, layer, O.SHARED_EXPERT_ID, self.D, self.I, self.G)
+        self.moe = osm_hip.MoeLayer(ctx, self.g, self.E, self.k, self.router_bits, osm_hip.BF16, self.sg_bits,
+                                    self.norm_w, self.shared, max_tokens=max_tokens)
+        self._blobs = {}
+
+    def _synth_slab(self):
+        # The slab holds layer `self.layer` of the seeded model at slab layer 0.
+        if self.layer == 0:
+            self.slab.synthesize(self.seed)
+        else:
+            for e in range(self.E):
+                self.slab.upload(0, e, O.synth_expert_blob(self.seed, self.layer, e, self.D, self.I, self.G))
+
+    def blob(self, e):
+        if e not in self._blobs:
+            self._blobs[e] = O.synth_expert_blob(self.seed, self.layer, e, self.D, self.I, self.G)
+        return self._blobs[e]
+
+    def oracle_token(self, x, sublayer=False):
+        router = O.bf16_bits_to_f32(self.router_bits)
+        sg = O.bf16_bits_to_f32(self.sg_bits)
+        xin = O.rms_norm(x, 1, self.D, self.norm_w, 1e-6) if sublayer else x
+        picks = O.route_qwen_top_k(xin, router, self.D, self.E, self.k, True)
+        dummy = self.blob(int(picks["ids"][0]))
+        table = [self.blob(e) if e in set(int(i) for i in picks["ids"]) else dummy for e in range(self.E)]
+        if sublayer:
+            r = O.moe_sublayer(x, self.norm_w, 1e-6, router, table, self.shared, sg, self.D, self.I, self.G, O.META_BF16, self.k)
+        else:
+            r = O.qwen_sparse_moe(x, router, table, self.shared, sg, self.D, self.I, self.G, O.META_BF16, self.k)
+        r["logits"] = picks["logits"]
+        r["mass"] = picks["mass"]
+        return r
+
+
+def assert_token_parity(gpu, t, ora, sublayer=False):
+    ids_g, ids_o = gpu["ids"][t], ora["ids"]
+    if not np.array_equal(ids_g, ids_o):
+        lg = np.sort(ora["logits"])[::-1]
+        pytest.fail(f"routed ids differ: gpu {list(ids_g)} oracle {list(ids_o)}; "
+                    f"oracle logit gap k/k+1 = {lg[len(ids_o) - 1] - lg[len(ids_o)]:.3e}")
+    assert max_abs(gpu["weights"][t], ora["weights"]) <= 1e-6
+    assert abs(gpu["shared_gate"][t] - ora["shared_gate"]) <= 1e-6
+    assert rel_l2(gpu["logits"][t], ora["logits"]) <= 1e-5
+    assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
+    if sublayer:
+        assert max_abs(gpu["normalized"][t], ora["normalized"]) <= 1e-5
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_moe_decode_qwen_b1(ctx, seed):
+    # One routed-MoE sublayer decode, batch 1: top-10 of 512 + gated shared expert.
+    L = QwenLayer(ctx, seed)
+    x = O.synth_tokens(seed, 0, 1, L.D)
+    gpu = L.moe.run_slab(L.slab, 0, x)
+    assert_token_parity(gpu, 0, L.oracle_token(x[0]))
+
+
+def test_moe_sublayer_rmsnorm_residual(ctx):
+    seed = 4
+    L = QwenLayer(ctx, seed, norm=True)
+    x = O.synth_tokens(seed, 0, 1, L.D) * np.float32(2.5)
+    gpu = L.moe.run_slab(L.slab, 0, x, sublayer=True)
+    assert_token_parity(gpu, 0, L.oracle_token(x[0], sublayer=True), sublayer=True)
+
+
+@pytest.mark.parametrize("tokens", [4, 16])
+def test_moe_decode_batched(ctx, tokens):
+    # Decode batch sizes: each token routed independently (oracle: per-token loop,
+    # as src/session/greedy_token_session.cpp:170-192 runs prefill).
+    seed = 5
+    L = QwenLayer(ctx, seed, max_tokens=16)
+    x = O.synth_tokens(seed, 1000, tokens, L.D)
+    gpu = L.moe.run_slab(L.slab, 0, x)
+    for t in range(tokens):
+        assert_token_parity(gpu, t, L.oracle_token(x[t]), sublayer=False)
+
+
+def test_moe_small_reference_shapes_f32_router(ctx):
+    # The reference's routed-MoE fixture sizes: hidden 128, intermediate 64,
+    # 3 experts, top-2 (tests/weighted_routed_moe_test.cpp); fp32 router and
+    # fp32 metadata, no shared expert.
+    rng = np.random.default_rng(6)
+    D, I, E, k = 128, 64, 3, 2
+    g = osm_hip.geometry(D, I, 64, osm_hip.F32)
+    blobs = [random_blob(rng, D, I, 64, O.META_F32)[0] for _ in range(E)]
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blobs[e])
+    router = rng.normal(0, 0.3, (E, D)).astype(np.float32)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, router, osm_hip.F32, max_tokens=2)
+    x = rng.normal(0, 1, (2, D)).astype(np.float32)
+    gpu = moe.run_slab(slab, 0, x)
+    for t in range(2):
+        ora = O.qwen_sparse_moe(x[t], router, blobs, None, None, D, I, 64, O.META_F32, k)
+        assert np.array_equal(gpu["ids"][t], ora["ids"])
+        assert max_abs(gpu["weights"][t], ora["weights"]) <= 1e-6
+        assert abs(gpu["weights"][t].sum() - 1) <= 1e-6
+        assert max_abs(gpu["out"][t], ora["out"]) <= 0.02 and rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
+
+
+def test_moe_rejects_invalid(ctx):
+    g = osm_hip.geometry(2048, 512, 64, osm_hip.BF16)
+    r = np.zeros(16 * 2048, np.uint16)
+    with pytest.raises(osm_hip.OsmError):
+        osm_hip.MoeLayer(ctx, g, 16, 17, r)  # top_k > experts
+    bad = r.copy()
+    bad[5] = 0x7F80  # +inf
+    with pytest.raises(osm_hip.OsmError):
+        osm_hip.MoeLayer(ctx, g, 16, 2, bad)
+    moe = osm_hip.MoeLayer(ctx, g, 16, 2, r, max_tokens=1)
+    slab = osm_hip.ExpertSlab(ctx, g, 1, 16)
+    with pytest.raises(osm_hip.OsmError):
+        moe.run_slab(slab, 0, np.full((1, 2048), np.nan, np.float32))
+    with pytest.raises(osm_hip.OsmError):
+        moe.run_slab(slab, 0, np.zeros((2, 2048), np.float32))  # more tokens than max_tokens
