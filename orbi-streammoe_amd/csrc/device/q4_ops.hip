@@ -19,6 +19,7 @@ __global__ void q4_dequant_kernel(const uint32_t* __restrict__ packed,
                                   const void* __restrict__ biases, uint32_t rows,
                                   uint32_t packed_cols, uint32_t group,
                                   float* __restrict__ out) {
+#pragma clang fp contract(off)
   const size_t total = static_cast<size_t>(rows) * packed_cols;
   const uint32_t groups = packed_cols * 8u / group;
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
@@ -33,7 +34,8 @@ __global__ void q4_dequant_kernel(const uint32_t* __restrict__ packed,
       const uint32_t col = wc * 8u + j;
       const size_t gi = static_cast<size_t>(r) * groups + col / group;
       const float q = static_cast<float>((w >> (4 * j)) & 0xFu);
-      v[j] = __fadd_rn(__fmul_rn(meta_at<META>(scales, gi), q), meta_at<META>(biases, gi));
+      const float prod = meta_at<META>(scales, gi) * q;
+      v[j] = prod + meta_at<META>(biases, gi);
     }
     float4* o = reinterpret_cast<float4*>(out + wi * 8u);
     o[0] = make_float4(v[0], v[1], v[2], v[3]);
@@ -110,9 +112,10 @@ __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restri
 // acc[i] += weight * src[i], rounded as the reference's scalar loop rounds.
 __global__ void weighted_accumulate_kernel(const float* __restrict__ src, float weight,
                                            float* __restrict__ acc, size_t n) {
+#pragma clang fp contract(off)
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
-    acc[i] = __fadd_rn(acc[i], __fmul_rn(weight, src[i]));
+    acc[i] = acc[i] + weight * src[i];
 }
 
 // One workgroup per row: block-wide sum of squares, then

@@ -5,8 +5,9 @@
 // is a pure function of (seed, a, b, tensor, index): a SplitMix64-style
 // finaliser over a counter, an Irwin-Hall(4) normal from four 16-bit draws
 // scaled to unit variance, and round-to-nearest-even to bf16. Only exact
-// integer steps and single IEEE roundings (__fmul_rn / __fadd_rn) are used,
-// so the same element computed on the host is bit-identical.
+// integer steps and separately rounded IEEE multiplies and adds are used
+// (contraction is off for this file), so the same element computed on the
+// host is bit-identical.
 //
 // Distributions (per expert projection): nibbles uniform on 0..15 (the low
 // 32 bits of the hash); scale = bf16(|N(0,1)| * 0.02); bias =
@@ -14,6 +15,10 @@
 // bf16(N(0,1) * 0.02). RMSNorm weight: 1 + N(0,1) * 0.02 (fp32). Tokens:
 // N(0,1) (fp32).
 #include "device_common.hpp"
+
+// Every multiply and add below rounds on its own, as on the host: no fused
+// multiply-add contraction anywhere in this file.
+#pragma clang fp contract(off)
 
 namespace {
 
@@ -43,7 +48,7 @@ __device__ __forceinline__ float normal_at(uint64_t stream, uint64_t i) {
   const uint64_t h = mix64(stream + i);
   const int32_t s = static_cast<int32_t>((h & 0xFFFFu) + ((h >> 16) & 0xFFFFu) +
                                          ((h >> 32) & 0xFFFFu) + (h >> 48));
-  return __fmul_rn(static_cast<float>(s - 131070), 0x1.bb67aep-16f);
+  return static_cast<float>(s - 131070) * 0x1.bb67aep-16f;
 }
 
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
@@ -78,10 +83,10 @@ __global__ void synth_meta_kernel(uint64_t seed, uint32_t layer, uint32_t first_
   uint8_t* base = dst + blockIdx.y * stride;
   const size_t step = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < ps.groups; i += step) {
-    const uint16_t sbits = bf16_rne(__fmul_rn(fabsf(normal_at(ss, i)), 0.02f));
+    const uint16_t sbits = bf16_rne(fabsf(normal_at(ss, i)) * 0.02f);
     const float sval = bf16_to_f32(sbits);
-    const float noise = __fmul_rn(normal_at(sb, i), 0.002f);
-    const uint16_t bbits = bf16_rne(__fadd_rn(__fmul_rn(-8.0f, sval), noise));
+    const float noise = normal_at(sb, i) * 0.002f;
+    const uint16_t bbits = bf16_rne(-8.0f * sval + noise);
     if (meta_dtype == OSM_META_F32) {
       reinterpret_cast<float*>(base + ps.s_off)[i] = sval;
       reinterpret_cast<float*>(base + ps.b_off)[i] = bf16_to_f32(bbits);
@@ -95,12 +100,12 @@ __global__ void synth_meta_kernel(uint64_t seed, uint32_t layer, uint32_t first_
 __global__ void synth_bf16_kernel(uint64_t stream, size_t n, float sigma, uint16_t* out) {
   const size_t step = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += step)
-    out[i] = bf16_rne(__fmul_rn(normal_at(stream, i), sigma));
+    out[i] = bf16_rne(normal_at(stream, i) * sigma);
 }
 
 __global__ void synth_norm_kernel(uint64_t stream, uint32_t n, float* out) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = __fadd_rn(1.0f, __fmul_rn(normal_at(stream, i), 0.02f));
+  if (i < n) out[i] = 1.0f + normal_at(stream, i) * 0.02f;
 }
 
 __global__ void synth_tokens_kernel(uint64_t seed, uint32_t first_token, uint32_t hidden,
