@@ -55,6 +55,7 @@ typedef struct osm_expert_cache_s* osm_expert_cache;
 typedef struct osm_cache_policy_s* osm_cache_policy;
 typedef struct osm_moe_layer_s* osm_moe_layer;
 typedef struct osm_event_s* osm_event;
+typedef struct osm_graph_s* osm_graph;
 
 /* Diagnostic of the last failed call on this thread (empty string if none). */
 const char* osm_last_error(void);
@@ -80,6 +81,10 @@ int osm_device_alloc(osm_context ctx, size_t bytes, void** out);
 int osm_device_free(osm_context ctx, void* ptr);
 int osm_memcpy_h2d(osm_context ctx, void* dst, const void* src, size_t bytes);
 int osm_memcpy_d2h(osm_context ctx, void* dst, const void* src, size_t bytes);
+/* Device-to-device copy enqueued on the context's compute stream; returns
+ * before it runs (no synchronisation), so it may be captured into a graph or
+ * refresh a graph's input between launches. */
+int osm_memcpy_d2d_async(osm_context ctx, void* dst, const void* src, size_t bytes);
 
 /* ---- float buffer: VulkanFloatBuffer (vulkan_float_buffer.hpp:23-58) ------- */
 int osm_buffer_create(osm_context ctx, size_t element_count, osm_buffer* out);
@@ -217,17 +222,37 @@ int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache 
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,
                                 uint32_t tokens, int sublayer);
-/* Enqueues n_layers decodes back to back. chained != 0: sublayer form,
- * layer i reads the output of layer i-1 (x_dev [tokens, D] in, y_dev
- * [tokens, D] out, scratch_dev [tokens, D] ping-pong). chained == 0: layer i
- * reads x_dev + i*tokens*D and writes y_dev + i*tokens*D (MoE form). Layer i
- * uses layers[i] and slab layer slab_layers[i]. */
+/* Enqueues n_layers decodes back to back, as the reference's decoder stack
+ * runs its layers in order (src/model/checkpoint_decoder_stack.cpp:191-204).
+ * chained != 0: sublayer form, layer i reads the output of layer i-1 (x_dev
+ * [tokens, D] in, y_dev [tokens, D] out, scratch_dev [tokens, D] ping-pong).
+ * chained == 0: layer i reads x_dev + i*tokens*D and writes y_dev +
+ * i*tokens*D (MoE form). Layer i uses layers[i] and slab layer
+ * slab_layers[i]. */
 int osm_moe_decode_layers(osm_context ctx, const osm_moe_layer* layers,
                           const uint32_t* slab_layers, uint32_t n_layers, osm_expert_slab slab,
                           const float* x_dev, float* y_dev, float* scratch_dev, uint32_t tokens,
                           int chained);
-/* Launches one phase of a decode whose routing already ran for this layer
- * (phase 0 route, 1 gate/up + SwiGLU, 2 down + accumulate); for per-kernel
+/* ---- graphs (no counterpart in the reference, whose decoder stack
+ * dispatches every operator from the host) ------------------------------------
+ * A decode step, or any sequence of enqueue-only calls on the context,
+ * recorded once into a HIP graph: each launch replays every kernel on the
+ * same buffers with one submission. Callers refresh input contents between
+ * launches; layers, slabs and buffers must outlive the graph. Between
+ * capture_begin and capture_end only enqueue-only calls may be made on the
+ * context (decode_layers, moe_layer_decode_device, moe_layer_launch_phase,
+ * memcpy_d2d_async); capture_end always ends the capture. */
+int osm_decode_graph_create(osm_context ctx, const osm_moe_layer* layers,
+                            const uint32_t* slab_layers, uint32_t n_layers, osm_expert_slab slab,
+                            const float* x_dev, float* y_dev, float* scratch_dev, uint32_t tokens,
+                            int chained, osm_graph* out);
+int osm_graph_capture_begin(osm_context ctx);
+int osm_graph_capture_end(osm_context ctx, osm_graph* out);
+int osm_graph_launch(osm_context ctx, osm_graph g);
+void osm_graph_destroy(osm_graph g);
+/* Launches one kernel of a decode (phase 0 router GEMV, 1 expert selection +
+ * gate/up + SwiGLU, 2 down + weighted accumulate); phases 1 and 2 read what
+ * the previous phases of this layer left in its workspace. For per-kernel
  * timing. */
 int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                uint32_t slab_layer, const float* x_dev, float* y_dev,

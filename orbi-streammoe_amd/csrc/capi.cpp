@@ -37,6 +37,9 @@ struct osm_expert_slab_s {
 struct osm_expert_store_s {
   std::unique_ptr<osm::PinnedExpertStore> store;
 };
+struct osm_graph_s {
+  osm::HipGraph graph;
+};
 struct osm_event_s {
   osmd_event ev = nullptr;
   osm_context ctx = nullptr;
@@ -224,6 +227,14 @@ int osm_memcpy_d2h(osm_context ctx, void* dst, const void* src, size_t bytes) {
   int rc = osmd_memcpy_d2h(dst, src, bytes, ctx->ctx.stream());
   if (rc == 0) rc = osmd_stream_synchronize(ctx->ctx.stream());
   return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipMemcpy D2H", rc));
+}
+
+int osm_memcpy_d2d_async(osm_context ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(OSM_E_INVALID, "invalid arguments");
+  std::string d;
+  if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
+  const int rc = bytes ? osmd_memcpy_d2d(dst, src, bytes, ctx->ctx.stream()) : 0;
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipMemcpyAsync D2D", rc));
 }
 
 // ---- float buffer -----------------------------------------------------------
@@ -570,38 +581,92 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
   return from_diag(r.executed, r.diagnostic);
 }
 
-int osm_moe_decode_layers(osm_context ctx, const osm_moe_layer* layers, const uint32_t* slab_layers,
+// Builds the facade's decode step from C handles, checking each layer
+// against the slab.
+static int decode_step_of(osm_context ctx, const osm_moe_layer* layers, const uint32_t* slab_layers,
                           uint32_t n_layers, osm_expert_slab slab, const float* x_dev, float* y_dev,
-                          float* scratch_dev, uint32_t tokens, int chained) {
+                          float* scratch_dev, uint32_t tokens, int chained, osm::HipDecodeStep& step) {
   if (!ctx || !layers || !slab_layers || !slab || !x_dev || !y_dev || n_layers == 0)
     return fail(OSM_E_INVALID, "invalid arguments");
   if (chained && !scratch_dev) return fail(OSM_E_INVALID, "chained decode needs a scratch buffer");
   for (uint32_t i = 0; i < n_layers; ++i) {
     if (!layers[i]) return fail(OSM_E_INVALID, "null layer");
-    if (!slab->slab.device_table(slab_layers[i])) return fail(OSM_E_INVALID, "slab layer out of range");
+    const auto* table = slab->slab.device_table(slab_layers[i]);
+    if (!table) return fail(OSM_E_INVALID, "slab layer out of range");
     if (slab->slab.experts() != layers[i]->layer.config().expert_count)
       return fail(OSM_E_INVALID, "slab expert count does not match a layer's router");
+    step.layers.push_back(&layers[i]->layer);
+    step.tables.push_back(table);
   }
-  const std::size_t D = layers[0]->layer.config().geometry.hidden;
-  const std::size_t step = static_cast<std::size_t>(tokens) * D;
-  for (uint32_t i = 0; i < n_layers; ++i) {
-    const float* x;
-    float* y;
-    if (chained) {
-      // Ping-pong so the last layer lands in y_dev.
-      const bool last_to_y = ((n_layers - 1 - i) % 2) == 0;
-      x = (i == 0) ? x_dev : (last_to_y ? scratch_dev : y_dev);
-      y = last_to_y ? y_dev : scratch_dev;
-    } else {
-      x = x_dev + i * step;
-      y = y_dev + i * step;
-    }
-    auto r = layers[i]->layer.decode_device(ctx->ctx, x, y, tokens, slab->slab.device_table(slab_layers[i]),
-                                            chained != 0);
-    if (!r.executed) return fail(OSM_E_INVALID, r.diagnostic);
-  }
+  step.x = x_dev;
+  step.y = y_dev;
+  step.scratch = scratch_dev;
+  step.tokens = tokens;
+  step.chained = chained != 0;
   return ok();
 }
+
+int osm_moe_decode_layers(osm_context ctx, const osm_moe_layer* layers, const uint32_t* slab_layers,
+                          uint32_t n_layers, osm_expert_slab slab, const float* x_dev, float* y_dev,
+                          float* scratch_dev, uint32_t tokens, int chained) {
+  OSM_GUARD_BEGIN
+  osm::HipDecodeStep step;
+  const int rc = decode_step_of(ctx, layers, slab_layers, n_layers, slab, x_dev, y_dev, scratch_dev, tokens,
+                                chained, step);
+  if (rc != OSM_OK) return rc;
+  auto r = osm::enqueue_decode_step(ctx->ctx, step);
+  return from_diag(r.executed, r.diagnostic);
+  OSM_GUARD_END
+}
+
+int osm_decode_graph_create(osm_context ctx, const osm_moe_layer* layers, const uint32_t* slab_layers,
+                            uint32_t n_layers, osm_expert_slab slab, const float* x_dev, float* y_dev,
+                            float* scratch_dev, uint32_t tokens, int chained, osm_graph* out) {
+  OSM_GUARD_BEGIN
+  if (!out) return fail(OSM_E_INVALID, "null output handle");
+  *out = nullptr;
+  osm::HipDecodeStep step;
+  const int rc = decode_step_of(ctx, layers, slab_layers, n_layers, slab, x_dev, y_dev, scratch_dev, tokens,
+                                chained, step);
+  if (rc != OSM_OK) return rc;
+  std::string diag;
+  auto g = osm::HipGraph::capture_decode_step(ctx->ctx, step, &diag);
+  if (!g) return fail(OSM_E_INVALID, diag);
+  *out = new osm_graph_s{std::move(*g)};
+  return ok();
+  OSM_GUARD_END
+}
+
+int osm_graph_capture_begin(osm_context ctx) {
+  OSM_GUARD_BEGIN
+  if (!ctx) return fail(OSM_E_INVALID, "null context");
+  std::string diag;
+  if (!osm::HipGraph::begin_capture(ctx->ctx, &diag)) return fail(OSM_E_DEVICE, diag);
+  return ok();
+  OSM_GUARD_END
+}
+
+int osm_graph_capture_end(osm_context ctx, osm_graph* out) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !out) return fail(OSM_E_INVALID, "null argument");
+  *out = nullptr;
+  std::string diag;
+  auto g = osm::HipGraph::end_capture(ctx->ctx, &diag);
+  if (!g) return fail(OSM_E_DEVICE, diag);
+  *out = new osm_graph_s{std::move(*g)};
+  return ok();
+  OSM_GUARD_END
+}
+
+int osm_graph_launch(osm_context ctx, osm_graph g) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !g) return fail(OSM_E_INVALID, "null argument");
+  auto r = g->graph.launch(ctx->ctx);
+  return from_diag(r.executed, r.diagnostic);
+  OSM_GUARD_END
+}
+
+void osm_graph_destroy(osm_graph g) { delete g; }
 
 }  // extern "C"
 

@@ -30,16 +30,73 @@ __device__ __forceinline__ float meta_at(const void* p, size_t i) {
 }
 
 // ---- wavefront reductions (64 lanes) --------------------------------------
+// Within a 16-lane row the steps are DPP moves (VALU latency, no LDS
+// round trip): quad_perm [1,0,3,2] (xor 1), quad_perm [2,3,0,1] (xor 2),
+// row_half_mirror (lane i <-> 7-i) and row_mirror (lane i <-> 15-i). Across
+// rows, row_bcast:15 / row_bcast:31 fold rows into lane 63, which readlane
+// then broadcasts as a wave-uniform value.
+enum : int {
+  kDppXor1 = 0xB1,
+  kDppXor2 = 0x4E,
+  kDppRowHalfMirror = 0x141,
+  kDppRowMirror = 0x140,
+  kDppRowBcast15 = 0x142,
+  kDppRowBcast31 = 0x143,
+};
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                               __builtin_bit_cast(int, v), CTRL,
+                                                               ROW_MASK, 0xF, false));
+}
+
+// Sum over each aligned group of WIDTH lanes (WIDTH in {1,2,4,8,16}); every
+// lane of the group holds the result.
+template <int WIDTH>
+__device__ __forceinline__ float row_sum(float v) {
+  if constexpr (WIDTH >= 2) v += dpp<kDppXor1>(0.0f, v);
+  if constexpr (WIDTH >= 4) v += dpp<kDppXor2>(0.0f, v);
+  if constexpr (WIDTH >= 8) v += dpp<kDppRowHalfMirror>(0.0f, v);
+  if constexpr (WIDTH >= 16) v += dpp<kDppRowMirror>(0.0f, v);
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  v = row_sum<16>(v);
+  v += dpp<kDppRowBcast15, 0xA>(0.0f, v);
+  v += dpp<kDppRowBcast31, 0xC>(0.0f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
+  v = fmaxf(v, dpp<kDppXor1>(v, v));
+  v = fmaxf(v, dpp<kDppXor2>(v, v));
+  v = fmaxf(v, dpp<kDppRowHalfMirror>(v, v));
+  v = fmaxf(v, dpp<kDppRowMirror>(v, v));
+  v = fmaxf(v, dpp<kDppRowBcast15, 0xA>(v, v));
+  v = fmaxf(v, dpp<kDppRowBcast31, 0xC>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t old, uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v),
+                                                           CTRL, ROW_MASK, 0xF, false));
+}
+
+// Unsigned max over the wavefront. 0 is the identity of the max, so each
+// step can issue as a single v_max_u32 with a DPP source.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(0u, v));
+  v = max(v, dpp_u32<kDppXor2>(0u, v));
+  v = max(v, dpp_u32<kDppRowHalfMirror>(0u, v));
+  v = max(v, dpp_u32<kDppRowMirror>(0u, v));
+  v = max(v, dpp_u32<kDppRowBcast15, 0xA>(0u, v));
+  v = max(v, dpp_u32<kDppRowBcast31, 0xC>(0u, v));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_sum(float v, int width) {
   for (int m = width >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
@@ -47,30 +104,64 @@ __device__ __forceinline__ float group_sum(float v, int width) {
 }
 
 // ---- nibble dot products ---------------------------------------------------
-// Sum over the 8 nibbles of `w` (low nibble first) times x[0..7]. The even
-// and odd nibbles are split into bytes so each value converts with one
-// byte-to-float instruction.
-__device__ __forceinline__ float nib_dot8(uint32_t w, const float* x) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
-  float d = static_cast<float>(lo & 0xFFu) * x[0];
-  d = fmaf(static_cast<float>(hi & 0xFFu), x[1], d);
-  d = fmaf(static_cast<float>((lo >> 8) & 0xFFu), x[2], d);
-  d = fmaf(static_cast<float>((hi >> 8) & 0xFFu), x[3], d);
-  d = fmaf(static_cast<float>((lo >> 16) & 0xFFu), x[4], d);
-  d = fmaf(static_cast<float>((hi >> 16) & 0xFFu), x[5], d);
-  d = fmaf(static_cast<float>(lo >> 24), x[6], d);
-  d = fmaf(static_cast<float>(hi >> 24), x[7], d);
+// A nibble q masked into the low bits of a 16-bit lane is the f16 subnormal
+// q * 2^-24, exactly. `w & 0x000F000F` therefore holds nibbles 0 and 4 of
+// `w` as an f16 pair, `(w >> 4) & 0x000F000F` nibbles 1 and 5, and so on, and
+// v_fma_mix_f32 multiplies either half by an fp32 x and accumulates in fp32.
+// Every product and partial sum is the plain fp32 one times 2^-24 (a power of
+// two, with fp32 and f16 denormals preserved), so scaling the sum by 2^24
+// gives the same bits as converting each nibble to float whenever no product
+// falls below 2^-102: about 14 VALU instructions per 8 nibbles instead of 21.
+__device__ __forceinline__ float f16_lo(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
+}
+__device__ __forceinline__ float f16_hi(uint32_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v >> 16)));
+}
+
+// A zero the compiler cannot see through: seeding a chain with it keeps the
+// first product a v_fma_mix_f32 instead of a convert and a multiply. The
+// seeded chain differs from one started with the product only in the sign of
+// an exactly-zero result.
+__device__ __forceinline__ float opaque_zero() {
+  float z = 0.0f;
+  asm("" : "+v"(z));
+  return z;
+}
+
+// z + 2^-24 * sum over the 8 nibbles of `w` (low nibble first) times
+// x[0..7], accumulated in nibble order.
+__device__ __forceinline__ float nib_dot8_s24(uint32_t w, const float* x, float z) {
+  const uint32_t p0 = w & 0x000F000Fu;
+  const uint32_t p1 = (w >> 4) & 0x000F000Fu;
+  const uint32_t p2 = (w >> 8) & 0x000F000Fu;
+  const uint32_t p3 = (w >> 12) & 0x000F000Fu;
+  float d = fmaf(f16_lo(p0), x[0], z);
+  d = fmaf(f16_lo(p1), x[1], d);
+  d = fmaf(f16_lo(p2), x[2], d);
+  d = fmaf(f16_lo(p3), x[3], d);
+  d = fmaf(f16_hi(p0), x[4], d);
+  d = fmaf(f16_hi(p1), x[5], d);
+  d = fmaf(f16_hi(p2), x[6], d);
+  d = fmaf(f16_hi(p3), x[7], d);
   return d;
 }
 
-// 32 columns held by one 16-byte chunk.
+constexpr float kTwo24 = 16777216.0f;
+
+// Sum over the 8 nibbles of `w` times x[0..7].
+__device__ __forceinline__ float nib_dot8(uint32_t w, const float* x) {
+  return nib_dot8_s24(w, x, opaque_zero()) * kTwo24;
+}
+
+// 32 columns held by one 16-byte chunk: four independent chains of eight.
 __device__ __forceinline__ float nib_dot32(uint4 q, const float* x) {
-  float d = nib_dot8(q.x, x);
-  d += nib_dot8(q.y, x + 8);
-  d += nib_dot8(q.z, x + 16);
-  d += nib_dot8(q.w, x + 24);
-  return d;
+  const float z = opaque_zero();
+  float d = nib_dot8_s24(q.x, x, z);
+  d += nib_dot8_s24(q.y, x + 8, z);
+  d += nib_dot8_s24(q.z, x + 16, z);
+  d += nib_dot8_s24(q.w, x + 24, z);
+  return d * kTwo24;
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {

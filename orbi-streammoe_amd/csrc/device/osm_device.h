@@ -22,6 +22,7 @@ extern "C" {
 
 typedef void* osmd_stream;
 typedef void* osmd_event;
+typedef void* osmd_graph; /* an instantiated, replayable graph */
 
 const char* osmd_error_string(int code);
 
@@ -49,6 +50,14 @@ int osmd_event_synchronize(osmd_event e);
 int osmd_stream_wait_event(osmd_stream s, osmd_event e);
 int osmd_event_elapsed_ms(osmd_event start, osmd_event stop, float* ms);
 int osmd_device_synchronize(void);
+/* Records what is enqueued on s between begin and end (nothing runs), then
+ * instantiates it. A failed launch inside still needs the end call, which
+ * then returns its error and no graph. Capture must not record memset nodes:
+ * buffers are cleared with osmd_zero. */
+int osmd_capture_begin(osmd_stream s);
+int osmd_capture_end(osmd_stream s, osmd_graph* out);
+int osmd_graph_launch(osmd_graph g, osmd_stream s);
+int osmd_graph_destroy(osmd_graph g);
 
 /* ---- elementwise / projection kernels ----------------------------------- */
 typedef struct osmd_q4_proj {
@@ -98,7 +107,8 @@ typedef struct osmd_moe_args {
   const void* shared_gate_vec;        /* [D] */
   const float* norm_weight;           /* [D] */
   const uint8_t* shared_expert;       /* blob */
-  const uint8_t* const* expert_table; /* [E] device pointers to blobs */
+  const uint8_t* const* expert_table; /* [E] device pointers to blobs, or null */
+  const uint8_t* fallback_blob;       /* any valid blob, read in place of a null pointer */
   float* logits;      /* [B, E]   out */
   uint32_t* ids;      /* [B, k]   out */
   float* weights;     /* [B, k]   out */
@@ -114,17 +124,27 @@ typedef struct osmd_moe_args {
 #define OSMD_MAX_TOP_K 16u
 #define OSMD_MAX_EXPERTS 1024u
 
-/* route: RMSNorm + router + shared gate + top-k; writes ids/weights/mass/
- * shared_gate and slot_ptrs (from expert_table; an absent expert gives a
- * null pointer, which the expert phase skips). experts: gate/up + SwiGLU and
- * down + weighted accumulate over slot_ptrs. decode = route then experts. */
+/* decode (every expert resident, expert_table set): three kernels --
+ *   route:   RMSNorm (optional) + router GEMV + shared-gate dot -> logits
+ *   gate_up: top-k selection from the logits (recomputed by one wavefront
+ *            of every routed workgroup; one publishes ids/weights/mass/
+ *            slot_ptrs), then the gate/up GEMVs with fused SwiGLU -> h
+ *   down:    down GEMVs + weighted accumulate (+ residual) -> y
+ * Host-driven residency (expert_table null): osmd_moe_route runs route and a
+ * one-wavefront select kernel, so the host can read ids and write slot_ptrs
+ * before osmd_moe_experts (gate_up then reads slot_ptrs). */
 int osmd_moe_route(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_experts(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s);
-/* The two halves of the expert phase, for per-kernel timing. */
+/* Single kernels, for per-kernel timing: the router GEMV alone, gate/up
+ * (with its selection when expert_table is set), and down. */
+int osmd_moe_router(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_down(const osmd_moe_args* a, osmd_stream s);
 
+/* Bytes of LDS the down kernel stages for `nslot` slots of width `inter`
+ * (the host rejects layers whose staging exceeds 64 KiB). */
+size_t osmd_moe_down_lds_bytes(uint32_t inter, uint32_t nslot);
 /* ---- seeded synthetic inputs (bit-identical to the host generator) ------ */
 int osmd_synth_expert_blobs(uint64_t seed, uint32_t layer, uint32_t first_expert,
                             uint32_t count, osm_expert_geometry g, uint8_t* dst,

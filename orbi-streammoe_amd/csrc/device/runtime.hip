@@ -115,4 +115,31 @@ int osmd_event_elapsed_ms(osmd_event start, osmd_event stop, float* ms) {
 }
 int osmd_device_synchronize(void) { return rc(hipDeviceSynchronize()); }
 
+// Graph capture of one stream: what is enqueued between begin and end is
+// recorded instead of run, then instantiated once and replayed with a single
+// submission per launch. Thread-local mode: other threads keep using HIP.
+int osmd_capture_begin(osmd_stream s) {
+  return rc(hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeThreadLocal));
+}
+int osmd_capture_end(osmd_stream s, osmd_graph* out) {
+  *out = nullptr;
+  hipGraph_t graph = nullptr;
+  int r = rc(hipStreamEndCapture(static_cast<hipStream_t>(s), &graph));
+  if (r != 0) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return r;
+  }
+  hipGraphExec_t exec = nullptr;
+  r = rc(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+  (void)hipGraphDestroy(graph);
+  if (r == 0) *out = exec;
+  return r;
+}
+int osmd_graph_launch(osmd_graph g, osmd_stream s) {
+  return rc(hipGraphLaunch(static_cast<hipGraphExec_t>(g), static_cast<hipStream_t>(s)));
+}
+int osmd_graph_destroy(osmd_graph g) {
+  return g ? rc(hipGraphExecDestroy(static_cast<hipGraphExec_t>(g))) : 0;
+}
+
 }  // extern "C"

@@ -31,6 +31,7 @@ struct HipMoeLayer::Impl {
   std::uint32_t max_tokens = 0;
   int device = -1;
   DeviceBytes router, shared_gate_vec, norm_weight, shared_blob;
+  DeviceBytes zero_blob;  // fallback blob when there is no shared expert
   // workspace
   DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs, counter;
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
@@ -56,6 +57,7 @@ struct HipMoeLayer::Impl {
     a.norm_weight = norm_weight.as<const float>();
     a.shared_expert = shared_blob.as<const std::uint8_t>();
     a.expert_table = table;
+    a.fallback_blob = shared_blob.get() ? shared_blob.as<const std::uint8_t>() : zero_blob.as<const std::uint8_t>();
     a.logits = logits.as<float>();
     a.ids = ids.as<std::uint32_t>();
     a.weights = weights.as<float>();
@@ -98,7 +100,7 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
       return std::nullopt;
     }
     const std::size_t nslot = config.top_k + (config.has_shared_expert ? 1U : 0U);
-    if (nslot * (g.inter + g.inter / 32U) * sizeof(float) > 65536U) {
+    if (osmd_moe_down_lds_bytes(g.inter, static_cast<std::uint32_t>(nslot)) > 65536U) {
       set_diag(diagnostic, "MoE layer: (top_k + shared) * intermediate exceeds the 64 KiB LDS staging");
       return std::nullopt;
     }
@@ -146,6 +148,10 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
     if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_gate_vec, shared_gate_vec, D * esz);
     if (rc == 0 && !norm_weight.empty()) rc = up(impl->norm_weight, norm_weight.data(), norm_weight.size_bytes());
     if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_blob, shared_blob.data(), shared_blob.size());
+    if (rc == 0 && !config.has_shared_expert) {
+      rc = impl->zero_blob.allocate(expert_blob_bytes(g));
+      if (rc == 0) rc = osmd_zero(impl->zero_blob.get(), impl->zero_blob.size(), st);
+    }
     if (rc == 0) rc = impl->x_in.allocate(T * D * sizeof(float));
     if (rc == 0) rc = impl->y_out.allocate(T * D * sizeof(float));
     if (rc == 0) rc = impl->logits.allocate(T * E * sizeof(float));
@@ -245,7 +251,7 @@ HipDispatchResult HipMoeLayer::launch_phase(HipComputeContext& context, const fl
   const osmd_moe_args a = impl_->args(x, y, tokens, expert_table, sublayer);
   int rc;
   switch (phase) {
-    case 0: rc = osmd_moe_route(&a, context.stream()); break;
+    case 0: rc = osmd_moe_router(&a, context.stream()); break;
     case 1: rc = osmd_moe_gate_up(&a, context.stream()); break;
     case 2: rc = osmd_moe_down(&a, context.stream()); break;
     default:

@@ -620,8 +620,9 @@ class HipMoeLayer {
                                                 std::uint32_t tokens,
                                                 const std::uint8_t* const* expert_table,
                                                 bool sublayer) noexcept;
-  // One phase of a decode whose routing already ran (0 route, 1 gate/up,
-  // 2 down), for per-kernel timing.
+  // One kernel of a decode (0 router GEMV, 1 selection + gate/up + SwiGLU,
+  // 2 down + weighted accumulate), for per-kernel timing; 1 and 2 read the
+  // workspace the previous kernels of this layer left.
   [[nodiscard]] HipDispatchResult launch_phase(HipComputeContext& context, const float* x,
                                                float* y, std::uint32_t tokens,
                                                const std::uint8_t* const* expert_table,
@@ -641,6 +642,57 @@ class HipMoeLayer {
   friend struct MoeLayerAccess;
   struct Impl;
   std::unique_ptr<Impl> impl_;
+};
+
+// One decode step through a stack of MoE layers, each with its device expert
+// table (checkpoint_decoder_stack.cpp:191-204 runs the layers in order).
+// chained: layer i + 1 reads what layer i wrote, each layer a sublayer
+// y = x + MoE(RMSNorm(x)), ping-ponging through scratch so the last layer
+// lands in y. Otherwise every layer decodes its own `tokens` rows:
+// x + i * tokens * D into y + i * tokens * D.
+struct HipDecodeStep {
+  std::vector<HipMoeLayer*> layers;
+  std::vector<const std::uint8_t* const*> tables;
+  const float* x = nullptr;
+  float* y = nullptr;
+  float* scratch = nullptr;
+  std::uint32_t tokens = 1;
+  bool chained = false;
+};
+
+[[nodiscard]] HipDispatchResult enqueue_decode_step(HipComputeContext& context,
+                                                    const HipDecodeStep& step) noexcept;
+
+// Work recorded once from the context's compute stream into a HIP graph and
+// replayed with one submission: the same kernels on the same buffers every
+// launch, without the per-launch host and queue overhead. Only enqueue-only
+// operations may run between begin_capture and end_capture (no
+// synchronisation, no host copies, no memsets).
+class HipGraph {
+ public:
+  HipGraph() = default;
+  ~HipGraph();
+  HipGraph(const HipGraph&) = delete;
+  HipGraph& operator=(const HipGraph&) = delete;
+  HipGraph(HipGraph&& o) noexcept;
+  HipGraph& operator=(HipGraph&& o) noexcept;
+
+  [[nodiscard]] static bool begin_capture(HipComputeContext& context,
+                                          std::string* diagnostic = nullptr) noexcept;
+  // Ends the capture begun on this context's stream (always) and
+  // instantiates what was recorded.
+  [[nodiscard]] static std::optional<HipGraph> end_capture(HipComputeContext& context,
+                                                           std::string* diagnostic = nullptr) noexcept;
+  // One decode step, captured.
+  [[nodiscard]] static std::optional<HipGraph> capture_decode_step(HipComputeContext& context,
+                                                                   const HipDecodeStep& step,
+                                                                   std::string* diagnostic = nullptr) noexcept;
+  [[nodiscard]] bool valid() const noexcept { return exec_ != nullptr; }
+  [[nodiscard]] HipDispatchResult launch(HipComputeContext& context) noexcept;
+
+ private:
+  osmd_graph exec_ = nullptr;
+  int device_ = -1;
 };
 
 // routed_moe.hpp:58-65 -- one token through the resident cache: route on the

@@ -128,6 +128,12 @@ _PROTOTYPES = {
     "osm_moe_layer_decode_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_decode_layers": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_layer_launch_phase": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int, c_int]),
+    "osm_decode_graph_create": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int, POINTER(_H)]),
+    "osm_graph_capture_begin": (c_int, [_H]),
+    "osm_graph_capture_end": (c_int, [_H, POINTER(_H)]),
+    "osm_graph_launch": (c_int, [_H, _H]),
+    "osm_graph_destroy": (None, [_H]),
+    "osm_memcpy_d2d_async": (c_int, [_H, c_void_p, c_void_p, c_size_t]),
     "osm_expert_store_create": (c_int, [POINTER(Geometry), c_uint32, c_uint32, POINTER(_H)]),
     "osm_expert_store_destroy": (None, [_H]),
     "osm_expert_store_blob": (c_void_p, [_H, c_uint32, c_uint32]),
@@ -258,6 +264,13 @@ class Context(_Handle):
 
     def alloc(self, nbytes: int) -> "DeviceArray":
         return DeviceArray(self, nbytes)
+
+    def copy_d2d(self, dst_ptr, src_ptr, nbytes: int):
+        """Enqueued device-to-device copy on the compute stream (no sync)."""
+        check(load().osm_memcpy_d2d_async(self.h, dst_ptr, src_ptr, nbytes))
+
+    def capture(self) -> "_Capture":
+        return _Capture(self)
 
     def event(self) -> "Event":
         return Event(self)
@@ -545,6 +558,55 @@ def decode_layers(ctx, layers, slab_layers, slab, x_ptr, y_ptr, scratch_ptr, tok
     arr = (c_void_p * n)(*[l.h for l in layers])
     sl = (c_uint32 * n)(*slab_layers)
     check(load().osm_moe_decode_layers(ctx.h, arr, sl, n, slab.h, x_ptr, y_ptr, scratch_ptr, tokens, 1 if chained else 0))
+
+
+class Graph(_Handle):
+    """Work recorded once from a context's compute stream into a HIP graph;
+    launch() replays it. Whatever it reads and writes must outlive it."""
+
+    _destroy = "osm_graph_destroy"
+
+    def __init__(self, ctx, h, keep=()):
+        super().__init__(h)
+        self.ctx = ctx
+        self._keep = keep
+
+    def launch(self):
+        check(load().osm_graph_launch(self.ctx.h, self.h))
+
+
+def decode_graph(ctx, layers, slab_layers, slab, x_ptr, y_ptr, scratch_ptr, tokens, chained) -> Graph:
+    """decode_layers(...) with these exact arguments, captured into a graph."""
+    n = len(layers)
+    arr = (c_void_p * n)(*[l.h for l in layers])
+    sl = (c_uint32 * n)(*slab_layers)
+    h = c_void_p()
+    check(load().osm_decode_graph_create(ctx.h, arr, sl, n, slab.h, x_ptr, y_ptr, scratch_ptr, tokens,
+                                         1 if chained else 0, ctypes.byref(h)))
+    return Graph(ctx, h, (layers, slab))
+
+
+class _Capture:
+    """`with ctx.capture() as cap:` records the enqueue-only calls made inside
+    on ctx; cap.graph is the instantiated graph afterwards."""
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        self.graph = None
+
+    def __enter__(self):
+        check(load().osm_graph_capture_begin(self.ctx.h))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = c_void_p()
+        rc = load().osm_graph_capture_end(self.ctx.h, ctypes.byref(h))  # always ends the capture
+        if exc_type is None:
+            check(rc)
+            self.graph = Graph(self.ctx, h)
+        elif rc == 0:
+            load().osm_graph_destroy(h)
+        return False
 
 
 # ---- sources and caches -------------------------------------------------------------

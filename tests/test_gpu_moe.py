@@ -200,6 +200,46 @@ def test_moe_small_reference_shapes_f32_router(ctx):
         assert max_abs(gpu["out"][t], ora["out"]) <= 0.02 and rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
 
 
+@pytest.mark.parametrize("E,k,mode", [(100, 7, "random"), (1024, 10, "random"), (200, 16, "ties"),
+                                      (64, 1, "ties"), (700, 16, "underflow"), (33, 16, "underflow")])
+def test_moe_routing_edges(ctx, E, k, mode):
+    # Selection corners against the oracle's router (reference_ops.cpp:130-212):
+    # expert counts that leave lanes partly or wholly empty, exact ties (three
+    # distinct router rows, so equal logits and probabilities: lower id first),
+    # and logits hundreds apart, where exp underflows to 0 for all but a few
+    # experts and the remaining picks are the lowest ids with probability 0.
+    rng = np.random.default_rng(E * 31 + k)
+    D, I, G = 128, 64, 64
+    g = osm_hip.geometry(D, I, G, osm_hip.F32)
+    blob = random_blob(rng, D, I, G, O.META_F32)[0]  # one blob everywhere: routing is under test
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blob)
+    if mode == "ties":
+        rows = rng.normal(0, 0.3, (3, D)).astype(np.float32)
+        router = rows[rng.integers(0, 3, E)]
+    elif mode == "underflow":
+        router = rng.normal(0, 30.0, (E, D)).astype(np.float32)
+    else:
+        router = rng.normal(0, 0.3, (E, D)).astype(np.float32)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, router, osm_hip.F32, max_tokens=2)
+    x = rng.normal(0, 1, (2, D)).astype(np.float32)
+    gpu = moe.run_slab(slab, 0, x)
+    for t in range(2):
+        ora = O.route_qwen_top_k(x[t], router, D, E, k, True)
+        if mode == "underflow":
+            assert np.count_nonzero(O.softmax(ora["logits"])) < k  # the corner is exercised
+        assert np.array_equal(gpu["ids"][t], ora["ids"]), (list(gpu["ids"][t]), list(ora["ids"]))
+        assert rel_l2(gpu["logits"][t], ora["logits"]) <= 1e-5
+        # Logits of magnitude ~1e3 move the weights by the GEMV's rounding, so
+        # the selection is also checked on the device's own logits, exactly.
+        ids_own, w_own = O.route_top_k(gpu["logits"][t], k, True)
+        assert np.array_equal(gpu["ids"][t], ids_own)
+        assert max_abs(gpu["weights"][t], w_own) <= 1e-6
+        if mode != "underflow":
+            assert max_abs(gpu["weights"][t], ora["weights"]) <= 1e-6
+
+
 def test_moe_rejects_invalid(ctx):
     g = osm_hip.geometry(2048, 512, 64, osm_hip.BF16)
     r = np.zeros(16 * 2048, np.uint16)
@@ -215,3 +255,56 @@ def test_moe_rejects_invalid(ctx):
         moe.run_slab(slab, 0, np.full((1, 2048), np.nan, np.float32))
     with pytest.raises(osm_hip.OsmError):
         moe.run_slab(slab, 0, np.zeros((2, 2048), np.float32))  # more tokens than max_tokens
+
+
+@pytest.mark.parametrize("chained", [False, True])
+def test_decode_graph_replays_match_eager(ctx, chained):
+    # A decode step over three layers captured into a HIP graph: every replay,
+    # with fresh input contents and eager work and synchronisation in between,
+    # must give the bits of the same step enqueued eagerly (the kernels are
+    # deterministic: no atomics, fixed reduction orders).
+    seed, D, I, G, E, k, L, B = 11, 256, 128, 64, 64, 4, 3, 2
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    slab = osm_hip.ExpertSlab(ctx, g, L, E)
+    slab.synthesize(seed)
+    layers = [osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, l, E, D), osm_hip.BF16,
+                               O.synth_shared_gate_bf16(seed, l, D), O.synth_norm_weight(seed, l, D),
+                               O.synth_expert_blob(seed, l, O.SHARED_EXPERT_ID, D, I, G), max_tokens=B)
+              for l in range(L)]
+    n = (1 if chained else L) * B * D
+    x, y, scratch, x_ref, y_ref = (ctx.alloc(L * B * D * 4) for _ in range(5))
+    graph = osm_hip.decode_graph(ctx, layers, list(range(L)), slab, x.ptr, y.ptr, scratch.ptr, B, chained)
+    rng = np.random.default_rng(seed)
+    for _ in range(3):
+        xin = rng.normal(0, 1, n).astype(np.float32)
+        x.upload(xin)
+        graph.launch()
+        got = y.download(np.float32, n)
+        x_ref.upload(xin)
+        osm_hip.decode_layers(ctx, layers, list(range(L)), slab, x_ref.ptr, y_ref.ptr, scratch.ptr, B, chained)
+        ref = y_ref.download(np.float32, n)
+        assert np.all(np.isfinite(ref))
+        assert np.array_equal(got, ref)
+
+
+def test_captured_phases_match_decode(ctx):
+    # The three kernels of one decode, launched one by one inside a capture
+    # and replayed, give the bits of decode_device.
+    seed, D, I, G, E, k = 12, 256, 128, 64, 64, 4
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    slab.synthesize(seed)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, 0, E, D), osm_hip.BF16,
+                           O.synth_shared_gate_bf16(seed, 0, D), None,
+                           O.synth_expert_blob(seed, 0, O.SHARED_EXPERT_ID, D, I, G), max_tokens=1)
+    x, y, y_ref = (ctx.alloc(D * 4) for _ in range(3))
+    with ctx.capture() as cap:
+        for phase in (0, 1, 2):
+            moe.launch_phase(slab, 0, x.ptr, y.ptr, 1, False, phase)
+    rng = np.random.default_rng(seed)
+    for _ in range(2):
+        x.upload(rng.normal(0, 1, D).astype(np.float32))
+        cap.graph.launch()
+        got = y.download(np.float32, D)
+        moe.decode_device(slab, 0, x.ptr, y_ref.ptr, 1)
+        assert np.array_equal(got, y_ref.download(np.float32, D))
