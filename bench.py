@@ -49,6 +49,12 @@ def parse():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--phase-rounds", type=int, default=20)
     ap.add_argument("--cpu-tokens", type=int, default=64, help="token-layers in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no benchmark: summarise two rocprofv3 --pmc counter_collection.csv files "
+                         "(FETCH_SIZE, WRITE_SIZE) of a run with --copy-probe-mb into HBM bytes per dispatch")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="after the run, one device-to-device copy of this many MiB: the known-size "
+                         "reference for scaling HBM traffic counters")
     return ap.parse_args()
 
 
@@ -91,6 +97,47 @@ def traffic_from_profiles(kernel):
         return data["kernels"][kernel]["hbm_bytes_per_dispatch"]
     except Exception:
         return None
+
+
+def summarize_counters(fetch_csv, write_csv, probe_mb):
+    """HBM bytes per dispatch of the decode kernels from FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch), each scaled by what the same counter
+    reads for the copy probe -- a copy kernel of known size whose loads are
+    16 bytes per lane, like the decode kernels' weight streams."""
+    import csv
+    from collections import defaultdict
+
+    def per_kernel(path):
+        vals = defaultdict(list)
+        for r in csv.DictReader(open(path)):
+            vals[(r["Kernel_Name"], int(r["Grid_Size"]))].append(float(r["Counter_Value"]))
+        return vals
+
+    fetch, write = per_kernel(fetch_csv), per_kernel(write_csv)
+    probe_kib = probe_mb * 1024.0
+
+    def probe(vals):
+        cands = [(g, v) for (n, g), v in vals.items() if "copy16_kernel" in n]
+        g, v = max(cands)  # the probe is the largest copy
+        return sum(v) / len(v)
+
+    f_probe, w_probe = probe(fetch), probe(write)
+    ff, fw = probe_kib / f_probe, probe_kib / w_probe
+    out = {"probe_bytes": probe_mb << 20, "probe_fetch_kib": f_probe, "probe_write_kib": w_probe,
+           "fetch_scale": round(ff, 4), "write_scale": round(fw, 4), "kernels": {}}
+    for short in ("route_kernel", "gate_up_kernel", "down_kernel"):
+        keys = [k for k in fetch if short in k[0]]
+        if not keys:
+            continue
+        key = max(keys, key=lambda k: len(fetch[k]))  # the instantiation the decode runs
+        f = sum(fetch[key]) / len(fetch[key])
+        w = sum(write[key]) / len(write[key]) if key in write else 0.0
+        out["kernels"][short] = {
+            "instantiation": key[0], "dispatches": len(fetch[key]),
+            "fetch_kib": round(f, 3), "write_kib": round(w, 3),
+            "hbm_bytes_per_dispatch": int(round((f * ff + w * fw) * 1024)),
+        }
+    return out
 
 
 def cpu_baseline(seed, tokens):
@@ -154,6 +201,9 @@ def cpu_baseline(seed, tokens):
 
 def main():
     args = parse()
+    if args.counters:
+        print(json.dumps(summarize_counters(args.counters[0], args.counters[1], args.copy_probe_mb), indent=1))
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU; multi-GPU runs are not part of this build "
                                    f"(asked for --gpus {args.gpus})"}))
@@ -291,6 +341,13 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+    if args.copy_probe_mb > 0:
+        n = args.copy_probe_mb << 20
+        src, dst = ctx.alloc(n), ctx.alloc(n)
+        ctx.copy_d2d(dst.ptr, src.ptr, n)
+        ctx.synchronize()
+        log(f"[bench] copy probe: {n} bytes device to device")
 
 
 if __name__ == "__main__":

@@ -83,7 +83,8 @@ int osm_memcpy_h2d(osm_context ctx, void* dst, const void* src, size_t bytes);
 int osm_memcpy_d2h(osm_context ctx, void* dst, const void* src, size_t bytes);
 /* Device-to-device copy enqueued on the context's compute stream; returns
  * before it runs (no synchronisation), so it may be captured into a graph or
- * refresh a graph's input between launches. */
+ * refresh a graph's input between launches. 16-byte aligned copies run as a
+ * kernel (1 KB per wavefront load), others as an async memcpy. */
 int osm_memcpy_d2d_async(osm_context ctx, void* dst, const void* src, size_t bytes);
 
 /* ---- float buffer: VulkanFloatBuffer (vulkan_float_buffer.hpp:23-58) ------- */

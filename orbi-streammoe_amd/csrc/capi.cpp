@@ -233,8 +233,8 @@ int osm_memcpy_d2d_async(osm_context ctx, void* dst, const void* src, size_t byt
   if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(OSM_E_INVALID, "invalid arguments");
   std::string d;
   if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
-  const int rc = bytes ? osmd_memcpy_d2d(dst, src, bytes, ctx->ctx.stream()) : 0;
-  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipMemcpyAsync D2D", rc));
+  const int rc = osmd_copy_d2d(dst, src, bytes, ctx->ctx.stream());
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("device copy", rc));
 }
 
 // ---- float buffer -----------------------------------------------------------

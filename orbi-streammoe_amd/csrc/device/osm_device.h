@@ -38,6 +38,9 @@ int osmd_host_free(void* ptr);
 int osmd_memcpy_h2d(void* dst, const void* src, size_t bytes, osmd_stream s);
 int osmd_memcpy_d2h(void* dst, const void* src, size_t bytes, osmd_stream s);
 int osmd_memcpy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s);
+/* Device-to-device copy with a kernel when dst, src and bytes are 16-byte
+ * aligned (a kernel node when captured), else hipMemcpyAsync. */
+int osmd_copy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s);
 /* Zero-fill with a kernel (safe inside captured graphs). */
 int osmd_zero(void* dst, size_t bytes, osmd_stream s);
 int osmd_stream_create(osmd_stream* s);

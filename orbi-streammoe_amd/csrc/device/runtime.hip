@@ -18,6 +18,14 @@ __global__ void zero_kernel(uint4* __restrict__ dst16, size_t n16,
     for (size_t i = threadIdx.x; i < ntail; i += blockDim.x) tail[i] = 0;
 }
 
+// Grid-stride copy: each lane moves 16 bytes per step, so a wavefront
+// instruction moves 1 KB of contiguous memory.
+__global__ void copy16_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+    dst[i] = src[i];
+}
+
 }  // namespace
 
 extern "C" {
@@ -34,7 +42,10 @@ int osmd_device_name(int device, char* buf, size_t n) {
   const int r = rc(hipGetDeviceProperties(&prop, device));
   if (r != 0) return r;
   if (n > 0) {
-    std::strncpy(buf, prop.name, n - 1);
+    // Some drivers leave the marketing name empty; the ISA name then says
+    // what the device is.
+    const char* name = prop.name[0] != '\0' ? prop.name : prop.gcnArchName;
+    std::strncpy(buf, name, n - 1);
     buf[n - 1] = '\0';
   }
   return 0;
@@ -76,6 +87,18 @@ int osmd_zero(void* dst, size_t bytes, osmd_stream s) {
   if (blocks > 4096) blocks = 4096;
   zero_kernel<<<static_cast<unsigned>(blocks), 256, 0, static_cast<hipStream_t>(s)>>>(
       static_cast<uint4*>(dst), n16, static_cast<uint8_t*>(dst) + n16 * 16, ntail);
+  return osmk::launch_status();
+}
+
+int osmd_copy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s) {
+  if (bytes == 0) return 0;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes;
+  if (a % 16 != 0) return osmd_memcpy_d2d(dst, src, bytes, s);
+  const size_t n16 = bytes / 16;
+  size_t blocks = (n16 + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  copy16_kernel<<<static_cast<unsigned>(blocks), 256, 0, static_cast<hipStream_t>(s)>>>(
+      static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
   return osmk::launch_status();
 }
 

@@ -1,0 +1,91 @@
+"""The HBM-resident expert cache on the device.
+
+The reference's own scenario (tests/vulkan_resident_expert_cache_test.cpp:
+316-382) with its fixture experts and tolerance, and the cached routed-MoE
+decode (capped budget, misses filled from pinned host memory) against the
+all-resident decode and the restated cache policy."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import osm_hip
+from helpers import cache_fixture_expert, cache_fixture_token, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def test_resident_cache_reference_scenario(ctx):
+    # Budget of two experts; E0, E1 miss; E0 hits without touching the host
+    # cache; E2 misses and evicts E1 (frequency 1 < E0's 2).
+    g = osm_hip.geometry(128, 64, 64, osm_hip.BF16)
+    blobs = [cache_fixture_expert(e) for e in range(3)]
+    stride = blobs[0].size
+
+    def read(layers, experts, dests):
+        for l, e, d in zip(layers, experts, dests):
+            d[:] = blobs[e]
+        return 0
+
+    host = osm_hip.HostExpertCache(stride, stride, read, minimum_slots=1)
+    cache = osm_hip.ExpertCache(ctx, 2 * stride, host_cache=host, g=g)
+    cache.get(0, 0)
+    cache.get(0, 1)
+    st = cache.stats()
+    assert (st["hits"], st["misses"], st["loads"], st["evictions"]) == (0, 2, 2, 0)
+    assert st["resident_entries"] == 2 and st["resident_bytes"] == 2 * stride
+
+    before = host.stats()
+    cache.get(0, 0)
+    after = host.stats()
+    assert (after["hits"], after["misses"]) == (before["hits"], before["misses"])  # a GPU hit bypasses L1
+
+    cache.get(0, 2)
+    st = cache.stats()
+    assert (st["hits"], st["misses"], st["loads"], st["evictions"]) == (1, 3, 3, 1)
+    assert st["resident_entries"] == 2 and st["resident_bytes"] <= st["budget_bytes"]
+    assert cache.contains(0, 0) and not cache.contains(0, 1) and cache.contains(0, 2)
+
+    for e in (0, 2):
+        x = cache_fixture_token(e)
+        got = cache.run(0, e, x)
+        assert max_abs(got, O.expert_forward(blobs[e], 128, 64, 64, O.META_BF16, x)) <= 0.01
+    st = cache.stats()
+    assert (st["hits"], st["misses"], st["loads"], st["evictions"]) == (3, 3, 3, 1)
+
+
+def test_cached_decode_matches_resident_decode(ctx):
+    # A capped cache (12 of 2 x 64 experts) filled from pinned host memory on
+    # the side stream: every token's output and routing must be the bits of
+    # the all-resident decode, and the hit/miss/eviction counts those of the
+    # restated policy replayed over the same picks (routed_moe.cpp:320-404
+    # fetches the picks in order).
+    seed, D, I, G, E, k, layers = 21, 256, 128, 64, 64, 4, 2
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    store = osm_hip.ExpertStore(g, layers, E)
+    store.synthesize(ctx, seed)
+    slab = osm_hip.ExpertSlab(ctx, g, layers, E)
+    slab.synthesize(seed)
+    stride = store.stride
+    cache = osm_hip.ExpertCache(ctx, 12 * stride, store=store)
+    policy = O.DeviceCachePolicy(12 * stride)
+    moes = [osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, l, E, D), osm_hip.BF16,
+                             O.synth_shared_gate_bf16(seed, l, D), O.synth_norm_weight(seed, l, D),
+                             O.synth_expert_blob(seed, l, O.SHARED_EXPERT_ID, D, I, G), max_tokens=1)
+            for l in range(layers)]
+    x = O.synth_tokens(seed, 0, 12, D)
+    for t in range(12):
+        l = t % layers
+        sub = t % 3 == 0
+        got = moes[l].run_cached(cache, l, x[t], sublayer=sub)
+        ref = moes[l].run_slab(slab, l, x[t], sublayer=sub)
+        assert np.array_equal(got["ids"], ref["ids"])
+        assert np.array_equal(got["weights"], ref["weights"])
+        assert np.array_equal(got["out"], ref["out"])
+        for e in got["ids"][0]:
+            policy.get(l, int(e), stride)
+    st, po = cache.stats(), policy.stats()
+    for key in ("hits", "misses", "loads", "evictions", "resident_entries", "resident_bytes"):
+        assert st[key] == po[key], (key, st, po)
+    assert po["evictions"] > 0  # the cap was exercised
+    assert cache.bytes_filled == st["loads"] * stride
