@@ -205,6 +205,31 @@ def _shared_fixture():
     return hidden, inter, x, gate, up, down, scalar
 
 
+# ---- reference_ops.cpp: sigmoid / silu / swiglu -------------------------------------------
+def test_swiglu_kat_and_closed_form():
+    # tests/cpu_reference_test.cpp:138-147, and the closed forms in fp64:
+    # sigmoid(v) = 1 / (1 + e^-v), silu(v) = v * sigmoid(v).
+    out = O.swiglu([-1.0, 0.0, 1.0], [2.0, 3.0, 4.0])
+    assert abs(out[0] - O.silu(-1.0) * 2.0) <= 1e-6 and out[1] == 0.0 and abs(out[2] - O.silu(1.0) * 4.0) <= 1e-6
+    assert O.sigmoid(0.0) == 0.5
+    for v in np.linspace(-30, 30, 241):
+        v = float(np.float32(v))
+        sig = 1.0 / (1.0 + math.exp(-v))
+        assert abs(O.sigmoid(v) - sig) <= 2 * np.spacing(np.float32(sig))
+        assert abs(O.silu(v) - v * sig) <= 4 * np.spacing(np.float32(abs(v * sig))) + 1e-45
+    rng = np.random.default_rng(7)
+    g, u = rng.normal(0, 3, 257).astype(np.float32), rng.normal(0, 1, 257).astype(np.float32)
+    ref = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    assert np.max(np.abs(O.swiglu(g, u) - ref)) <= 1e-6
+
+
+@needs_ref
+def test_swiglu_matches_reference_build():
+    rng = np.random.default_rng(8)
+    g, u = rng.normal(0, 3, 1000).astype(np.float32), rng.normal(0, 1, 1000).astype(np.float32)
+    assert np.array_equal(O.swiglu(g, u), O.swiglu(g, u, impl="ref"))
+
+
 def test_shared_expert_closed_form():
     hidden, inter, x, gate, up, down, scalar = _shared_fixture()
     out, sg = O.run_shared_expert(x, gate, up, down, scalar, hidden, inter)
