@@ -110,6 +110,15 @@ int osm_swiglu(osm_context ctx, const float* gate, size_t gate_len, const float*
 /* run_vulkan_rms_norm (vulkan_rmsnorm.hpp:25-31): out has rows*dim floats. */
 int osm_rms_norm(osm_context ctx, const float* input, size_t input_len, size_t rows, size_t dim,
                  const float* weight, size_t weight_len, float eps, float* out);
+/* quantize_affine_q4_rows (src/conversion/single_expert_pilot.cpp:276-358)
+ * on the device: values [rows, cols] fp32 (host) -> packed [rows, cols/8],
+ * scales and biases [rows, cols/group] (host), and the largest and mean
+ * absolute reconstruction error. OSM_E_INVALID for bad geometry (the
+ * reference's std::invalid_argument), OSM_E_RUNTIME for a non-finite weight
+ * or an error above the group bound (its std::runtime_error). */
+int osm_q4_quantize(osm_context ctx, const float* values, size_t rows, size_t cols, size_t group,
+                    uint32_t* packed, float* scales, float* biases, float* max_abs_error,
+                    double* mean_abs_error);
 /* Integer-exact nibble unpack of the packed layout: out[8*w + j] = nibble j
  * (low first) of word w (the lane order of reference_ops.cpp:48-63). */
 int osm_unpack_nibbles(osm_context ctx, const uint32_t* packed, size_t words, uint8_t* out);

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_uint16, c_uint32, c_uint64, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int64, c_size_t, c_uint16, c_uint32, c_uint64, c_void_p
 
 import numpy as np
 
@@ -32,6 +32,7 @@ _P = c_void_p
 _ORACLE_PROTOS = {
     "oracle_last_error": (c_char_p, []),
     "oracle_dequantize_affine_rows": (c_int, [_P, c_size_t, c_size_t, c_size_t, _P, c_size_t, _P, c_size_t, c_uint32, c_uint32, _P]),
+    "oracle_quantize_affine_q4_rows": (c_int, [_P, c_size_t, c_size_t, c_size_t, c_size_t, _P, _P, _P, POINTER(c_float), POINTER(c_double)]),
     "oracle_matvec_row_major": (c_int, [_P, c_size_t, c_size_t, c_size_t, _P, c_size_t, _P]),
     "oracle_rms_norm_inplace": (c_int, [_P, c_size_t, c_size_t, c_size_t, _P, c_size_t, c_float]),
     "oracle_softmax_inplace": (c_int, [_P, c_size_t]),
@@ -148,6 +149,20 @@ def dequantize_affine_rows(packed, rows, packed_cols, scales, biases, bits=4, gr
     fn = lib().oracle_dequantize_affine_rows if impl == "oracle" else ref().ref_dequantize_affine_rows
     _check(fn(p(pk), pk.size, rows, packed_cols, p(s), s.size, p(b), b.size, bits, group_size, p(out)), impl)
     return out
+
+
+def quantize_affine_q4_rows(values, rows, cols, group):
+    """single_expert_pilot.cpp:276-358: (packed, scales, biases, max_err, mean_err)."""
+    v = f32(values).reshape(-1)
+    packed = np.zeros(rows * (cols // 8) if cols % 8 == 0 else 1, np.uint32)
+    groups = cols // group if group and cols % group == 0 else 1
+    scales = np.zeros(max(rows * groups, 1), np.float32)
+    biases = np.zeros_like(scales)
+    mx = c_float(0)
+    mean = c_double(0)
+    _check(lib().oracle_quantize_affine_q4_rows(p(v), v.size, rows, cols, group, p(packed), p(scales), p(biases),
+                                                ctypes.byref(mx), ctypes.byref(mean)))
+    return packed, scales, biases, mx.value, mean.value
 
 
 def matvec_row_major(weight, out_dim, in_dim, x, impl="oracle"):

@@ -607,6 +607,59 @@ int oracle_dequantize_affine_rows(const uint32_t* packed, size_t packed_len,
                       biases, biases_len, bits, group_size, out);
 }
 
+// src/conversion/single_expert_pilot.cpp:276-358 -- affine q4 quantizer. The
+// reference's source needs nlohmann/json to compile, so it is not part of the
+// reference build; this restatement is pinned by the reference's own test
+// (a round trip through the pinned dequant) and by the argmin and grid
+// properties in tests/test_oracle_pinning.py.
+int oracle_quantize_affine_q4_rows(const float* values, size_t values_len, size_t rows,
+                                   size_t cols, size_t group, uint32_t* packed,
+                                   float* scales, float* biases, float* max_abs_error,
+                                   double* mean_abs_error) {
+  if (rows == 0U || cols == 0U || group == 0U || cols % 8U != 0U || cols % group != 0U ||
+      rows > std::numeric_limits<size_t>::max() / cols || values_len != rows * cols)
+    return fail_invalid("affine q4 quantizer: invalid matrix geometry");
+  const size_t words = cols / 8U;
+  const size_t groups = cols / group;
+  std::fill(packed, packed + rows * words, 0U);
+  float worst = 0.0F;
+  double total = 0.0;
+  for (size_t r = 0; r < rows; ++r) {
+    for (size_t gi = 0; gi < groups; ++gi) {
+      const float* v = values + r * cols + gi * group;
+      float lo = std::numeric_limits<float>::infinity();
+      float hi = -std::numeric_limits<float>::infinity();
+      for (size_t i = 0; i < group; ++i) {
+        if (!std::isfinite(v[i])) return fail_runtime("affine q4 quantizer: non-finite source weight");
+        lo = std::min(lo, v[i]);
+        hi = std::max(hi, v[i]);
+      }
+      const float range = hi - lo;
+      const float scale = range > 0.0F ? range / 15.0F : 1.0F;
+      const float bias = lo;
+      scales[r * groups + gi] = scale;
+      biases[r * groups + gi] = bias;
+      const float allowed = range > 0.0F ? scale * 0.5001F + 1e-6F : 1e-6F;
+      for (size_t i = 0; i < group; ++i) {
+        const size_t col = gi * group + i;
+        const float t = (v[i] - bias) / scale;
+        // std::lround rounds halves away from zero; NaN (an overflowed range)
+        // maps to 0 here rather than to an implementation-defined integer.
+        const long n = std::isnan(t) ? 0L : std::lround(t);
+        const uint32_t q = static_cast<uint32_t>(std::clamp(n, 0L, 15L));
+        packed[r * words + col / 8U] |= q << (4U * (col % 8U));
+        const float err = std::fabs(scale * static_cast<float>(q) + bias - v[i]);
+        if (err > allowed) return fail_runtime("affine q4 quantizer: error above the group bound");
+        worst = std::max(worst, err);
+        total += static_cast<double>(err);
+      }
+    }
+  }
+  *max_abs_error = worst;
+  *mean_abs_error = total / static_cast<double>(rows * cols);
+  return 0;
+}
+
 int oracle_matvec_row_major(const float* weight, size_t weight_len,
                             size_t out_dim, size_t in_dim, const float* x,
                             size_t x_len, float* out) {

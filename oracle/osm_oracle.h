@@ -25,6 +25,17 @@ enum { ORACLE_META_F32 = 0, ORACLE_META_F16 = 1, ORACLE_META_BF16 = 2 };
 
 const char* oracle_last_error(void);
 
+/* ---- single_expert_pilot.cpp:276-358 restatement -------------------------
+ * quantize_affine_q4_rows: per (row, group) scale = range/15 (1 when flat),
+ * bias = min, q = clamp(round-half-away((v - bias) / scale), 0, 15), low
+ * nibble first. Outputs packed [rows, cols/8], scales/biases [rows, cols/g],
+ * the largest and mean reconstruction error. Returns 1 for bad geometry, 2
+ * for a non-finite weight or an error above the group bound. */
+int oracle_quantize_affine_q4_rows(const float* values, size_t values_len, size_t rows,
+                                   size_t cols, size_t group, uint32_t* packed,
+                                   float* scales, float* biases, float* max_abs_error,
+                                   double* mean_abs_error);
+
 /* ---- reference_ops.cpp restatement ------------------------------------ */
 int oracle_dequantize_affine_rows(const uint32_t* packed, size_t packed_len,
                                   size_t rows, size_t packed_cols,

@@ -6,6 +6,7 @@
 #include <memory>
 #include <new>
 #include <stdexcept>
+#include <limits>
 #include <string>
 #include <vector>
 
@@ -313,6 +314,27 @@ int osm_rms_norm(osm_context ctx, const float* input, size_t input_len, size_t r
   auto r = osm::run_hip_rms_norm(ctx->ctx, {input, input_len}, rows, dim, {weight, weight_len}, eps);
   if (!r.executed) return fail(OSM_E_INVALID, r.diagnostic);
   std::memcpy(out, r.values.data(), r.values.size() * sizeof(float));
+  return ok();
+  OSM_GUARD_END
+}
+
+int osm_q4_quantize(osm_context ctx, const float* values, size_t rows, size_t cols, size_t group,
+                    uint32_t* packed, float* scales, float* biases, float* max_abs_error,
+                    double* mean_abs_error) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !values || !packed || !scales || !biases || !max_abs_error || !mean_abs_error)
+    return fail(OSM_E_INVALID, "null argument");
+  if (rows != 0 && cols > std::numeric_limits<size_t>::max() / rows)
+    return fail(OSM_E_INVALID, "affine q4 quantizer: invalid matrix geometry");
+  auto r = osm::quantize_affine_q4_rows_hip(ctx->ctx, {values, rows * cols}, rows, cols, group);
+  if (r.invalid_argument) return fail(OSM_E_INVALID, r.diagnostic);
+  if (!r.executed) return fail(OSM_E_RUNTIME, r.diagnostic);
+  const auto& q = r.projection;
+  std::memcpy(packed, q.packed.data(), q.packed.size() * sizeof(uint32_t));
+  std::memcpy(scales, q.scales.data(), q.scales.size() * sizeof(float));
+  std::memcpy(biases, q.biases.data(), q.biases.size() * sizeof(float));
+  *max_abs_error = q.max_abs_error;
+  *mean_abs_error = q.mean_abs_error;
   return ok();
   OSM_GUARD_END
 }

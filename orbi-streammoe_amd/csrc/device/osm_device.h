@@ -83,6 +83,16 @@ int osmd_weighted_accumulate(const float* src, float weight, float* acc,
                              size_t n, osmd_stream s);
 int osmd_rms_norm(const float* in, const float* weight, float* out,
                   uint32_t rows, uint32_t dim, float eps, osmd_stream s);
+/* Affine q4 quantizer (single_expert_pilot.cpp:276-358) of values [rows,
+ * cols]: packed [rows, cols/8], scales/biases/bounds [rows, cols/group],
+ * per-block error maximum and sum ([osmd_q4_quantize_blocks()] each), and
+ * flags (zero on entry; bit 0 non-finite weight, bit 1 error above bound).
+ * Geometry is checked by the caller. */
+unsigned osmd_q4_quantize_blocks(size_t rows, size_t cols);
+int osmd_q4_quantize(const float* values, size_t rows, size_t cols, size_t group,
+                     uint32_t* packed, float* scales, float* biases, float* bounds,
+                     float* block_max, double* block_sum, uint32_t* flags,
+                     osmd_stream s);
 /* One expert MLP (gate/up GEMV with fused SwiGLU, then down GEMV) for one
  * token, used by the resident-expert operator. h is [inter] scratch. */
 int osmd_expert_forward(const uint8_t* blob, osm_expert_geometry g,

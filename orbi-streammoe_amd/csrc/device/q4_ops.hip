@@ -150,6 +150,96 @@ unsigned grid_for(size_t n, unsigned block) {
   return static_cast<unsigned>(g);
 }
 
+// ---- affine q4 quantizer (src/conversion/single_expert_pilot.cpp:276-358) --
+// Pass 1, one thread per (row, group): min, max, scale = range / 15 (1 when
+// flat), bias = min, the group's error bound (scale * 0.5001 + 1e-6, or 1e-6
+// when flat); flags bit 0 marks a non-finite weight. Pass 2, one
+// thread per packed word: q = clamp(round-half-away((v - bias) / scale), 0,
+// 15) per nibble (an overflowed range gives NaN, mapped to 0), the
+// reconstruction error against the group bound (flags bit 1), and per-block
+// error maximum and sum for the statistics. Every operation rounds on its
+// own, as the reference's scalar loop does.
+constexpr int kQuantThreads = 256;
+
+__global__ void quant_groups_kernel(const float* __restrict__ v, size_t rows, size_t cols, size_t group,
+                                    float* __restrict__ scales, float* __restrict__ biases,
+                                    float* __restrict__ bounds, uint32_t* __restrict__ flags) {
+#pragma clang fp contract(off)
+  const size_t groups = cols / group;
+  const size_t n = rows * groups;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float* g = v + (i / groups) * cols + (i % groups) * group;
+    float lo = INFINITY, hi = -INFINITY;
+    bool finite = true;
+    for (size_t j = 0; j < group; ++j) {
+      const float x = g[j];
+      finite = finite && isfinite(x);
+      lo = fminf(lo, x);
+      hi = fmaxf(hi, x);
+    }
+    if (!finite) atomicOr(flags, 1u);
+    const float range = hi - lo;
+    const float scale = range > 0.0f ? range / 15.0f : 1.0f;
+    scales[i] = scale;
+    biases[i] = lo;
+    bounds[i] = range > 0.0f ? scale * 0.5001f + 1e-6f : 1e-6f;
+  }
+}
+
+__global__ __launch_bounds__(kQuantThreads) void quant_pack_kernel(
+    const float* __restrict__ v, size_t rows, size_t cols, size_t group,
+    const float* __restrict__ scales, const float* __restrict__ biases,
+    const float* __restrict__ bounds, uint32_t* __restrict__ packed,
+    float* __restrict__ block_max, double* __restrict__ block_sum, uint32_t* __restrict__ flags) {
+#pragma clang fp contract(off)
+  __shared__ float smax[kQuantThreads];
+  __shared__ double ssum[kQuantThreads];
+  const size_t words_per_row = cols / 8u;
+  const size_t groups = cols / group;
+  const size_t n = rows * words_per_row;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  float worst = 0.0f;
+  double total = 0.0;
+  bool over = false;
+  for (size_t w = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; w < n; w += stride) {
+    const size_t row = w / words_per_row;
+    const size_t col0 = (w % words_per_row) * 8u;
+    uint32_t word = 0u;
+    for (uint32_t lane = 0; lane < 8u; ++lane) {
+      const size_t col = col0 + lane;
+      const size_t gi = row * groups + col / group;
+      const float scale = scales[gi];
+      const float bias = biases[gi];
+      const float x = v[row * cols + col];
+      const float t = (x - bias) / scale;
+      const int r = isnan(t) ? 0 : static_cast<int>(fminf(fmaxf(roundf(t), -1.0f), 16.0f));
+      const uint32_t q = static_cast<uint32_t>(r < 0 ? 0 : (r > 15 ? 15 : r));
+      word |= q << (4u * lane);
+      const float err = fabsf(scale * static_cast<float>(q) + bias - x);
+      over = over || err > bounds[gi];
+      worst = fmaxf(worst, err);
+      total += static_cast<double>(err);
+    }
+    packed[w] = word;
+  }
+  if (over) atomicOr(flags, 2u);
+  smax[threadIdx.x] = worst;
+  ssum[threadIdx.x] = total;
+  __syncthreads();
+  for (int h = kQuantThreads / 2; h > 0; h >>= 1) {
+    if (static_cast<int>(threadIdx.x) < h) {
+      smax[threadIdx.x] = fmaxf(smax[threadIdx.x], smax[threadIdx.x + h]);
+      ssum[threadIdx.x] += ssum[threadIdx.x + h];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    block_max[blockIdx.x] = smax[0];
+    block_sum[blockIdx.x] = ssum[0];
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -207,6 +297,28 @@ int osmd_weighted_accumulate(const float* src, float weight, float* acc, size_t 
 int osmd_rms_norm(const float* in, const float* weight, float* out, uint32_t rows, uint32_t dim,
                   float eps, osmd_stream s) {
   rms_norm_kernel<<<rows, 256, 0, static_cast<hipStream_t>(s)>>>(in, weight, out, dim, eps);
+  return launch_status();
+}
+
+unsigned osmd_q4_quantize_blocks(size_t rows, size_t cols) {
+  const size_t words = rows * (cols / 8u);
+  size_t b = (words + kQuantThreads - 1) / kQuantThreads;
+  if (b == 0) b = 1;
+  if (b > 2048) b = 2048;
+  return static_cast<unsigned>(b);
+}
+
+int osmd_q4_quantize(const float* values, size_t rows, size_t cols, size_t group, uint32_t* packed,
+                     float* scales, float* biases, float* bounds, float* block_max, double* block_sum,
+                     uint32_t* flags, osmd_stream s) {
+  const hipStream_t st = static_cast<hipStream_t>(s);
+  const size_t ngroups = rows * (cols / group);
+  size_t gb = (ngroups + 255) / 256;
+  if (gb > 4096) gb = 4096;
+  quant_groups_kernel<<<static_cast<unsigned>(gb), 256, 0, st>>>(values, rows, cols, group, scales, biases,
+                                                                 bounds, flags);
+  quant_pack_kernel<<<osmd_q4_quantize_blocks(rows, cols), kQuantThreads, 0, st>>>(
+      values, rows, cols, group, scales, biases, bounds, packed, block_max, block_sum, flags);
   return launch_status();
 }
 

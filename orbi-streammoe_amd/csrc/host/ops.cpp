@@ -183,6 +183,85 @@ HipValuesResult run_hip_q4_dequant(HipComputeContext& context, std::span<const s
   return r;
 }
 
+HipQuantizeResult quantize_affine_q4_rows_hip(HipComputeContext& context, std::span<const float> values,
+                                              std::size_t rows, std::size_t cols,
+                                              std::size_t group_size) noexcept {
+  HipQuantizeResult r;
+  try {
+    if (rows == 0U || cols == 0U || group_size == 0U || cols % 8U != 0U || cols % group_size != 0U ||
+        rows > std::numeric_limits<std::size_t>::max() / cols || values.size() != rows * cols) {
+      r.invalid_argument = true;
+      r.diagnostic = "affine q4 quantizer: invalid matrix geometry";
+      return r;
+    }
+    if (!context.activate(&r.diagnostic)) return r;
+    const std::size_t words = rows * (cols / 8U);
+    const std::size_t groups = rows * (cols / group_size);
+    const unsigned blocks = osmd_q4_quantize_blocks(rows, cols);
+    DeviceBytes v, packed, scales, biases, bounds, bmax, bsum, flags;
+    int rc = v.allocate(values.size_bytes());
+    if (rc == 0) rc = packed.allocate(words * 4U);
+    if (rc == 0) rc = scales.allocate(groups * 4U);
+    if (rc == 0) rc = biases.allocate(groups * 4U);
+    if (rc == 0) rc = bounds.allocate(groups * 4U);
+    if (rc == 0) rc = bmax.allocate(blocks * sizeof(float));
+    if (rc == 0) rc = bsum.allocate(blocks * sizeof(double));
+    if (rc == 0) rc = flags.allocate(sizeof(std::uint32_t));
+    const osmd_stream st = context.stream();
+    if (rc == 0) rc = osmd_memcpy_h2d(v.get(), values.data(), values.size_bytes(), st);
+    if (rc == 0) rc = osmd_zero(flags.get(), sizeof(std::uint32_t), st);
+    if (rc == 0)
+      rc = osmd_q4_quantize(v.as<const float>(), rows, cols, group_size, packed.as<std::uint32_t>(),
+                            scales.as<float>(), biases.as<float>(), bounds.as<float>(), bmax.as<float>(),
+                            bsum.as<double>(), flags.as<std::uint32_t>(), st);
+    HipAffineQ4Projection& q = r.projection;
+    q.rows = rows;
+    q.cols = cols;
+    q.packed_cols = cols / 8U;
+    q.groups_per_row = cols / group_size;
+    q.packed.resize(words);
+    q.scales.resize(groups);
+    q.biases.resize(groups);
+    std::vector<float> hmax(blocks);
+    std::vector<double> hsum(blocks);
+    std::uint32_t hflags = 0;
+    if (rc == 0) rc = osmd_memcpy_d2h(q.packed.data(), packed.get(), words * 4U, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(q.scales.data(), scales.get(), groups * 4U, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(q.biases.data(), biases.get(), groups * 4U, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(hmax.data(), bmax.get(), blocks * sizeof(float), st);
+    if (rc == 0) rc = osmd_memcpy_d2h(hsum.data(), bsum.get(), blocks * sizeof(double), st);
+    if (rc == 0) rc = osmd_memcpy_d2h(&hflags, flags.get(), sizeof(hflags), st);
+    if (rc == 0) rc = osmd_stream_synchronize(st);
+    if (rc != 0) {
+      r.projection = {};
+      r.diagnostic = hip_error("affine q4 quantizer failed", rc);
+      return r;
+    }
+    if (hflags & 1U) {
+      r.projection = {};
+      r.diagnostic = "affine q4 quantizer: non-finite source weight";
+      return r;
+    }
+    if (hflags & 2U) {
+      r.projection = {};
+      r.diagnostic = "affine q4 quantizer: error above the group bound";
+      return r;
+    }
+    double total = 0.0;
+    for (unsigned b = 0; b < blocks; ++b) {  // fixed order: deterministic
+      q.max_abs_error = std::max(q.max_abs_error, hmax[b]);
+      total += hsum[b];
+    }
+    q.mean_abs_error = total / static_cast<double>(rows * cols);
+    r.executed = true;
+    r.diagnostic = "HIP affine q4 quantizer executed.";
+  } catch (const std::exception& e) {
+    r.projection = {};
+    r.diagnostic = std::string("affine q4 quantizer exception: ") + e.what();
+  }
+  return r;
+}
+
 HipValuesResult run_hip_q4_gemv(HipComputeContext& context, std::span<const std::uint32_t> packed,
                                 std::size_t out_dim, std::size_t packed_cols,
                                 std::span<const float> scales, std::span<const float> biases,

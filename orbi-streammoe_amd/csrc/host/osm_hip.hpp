@@ -181,6 +181,27 @@ class HipQ4ProjectionWeights {
     HipComputeContext& context, std::span<const std::uint32_t> packed,
     std::size_t rows, std::size_t packed_cols, std::span<const float> scales,
     std::span<const float> biases, std::size_t group_size) noexcept;
+// AffineQ4Projection (conversion/single_expert_pilot.hpp:32-42).
+struct HipAffineQ4Projection {
+  std::size_t rows{}, cols{}, packed_cols{}, groups_per_row{};
+  std::vector<std::uint32_t> packed;
+  std::vector<float> scales, biases;
+  float max_abs_error{};
+  double mean_abs_error{};
+};
+struct HipQuantizeResult {
+  bool executed{};
+  bool invalid_argument{};  // where the reference throws std::invalid_argument
+  HipAffineQ4Projection projection;
+  std::string diagnostic;
+};
+// quantize_affine_q4_rows (single_expert_pilot.cpp:276-358) on the device:
+// bad geometry -> invalid_argument; a non-finite weight or an error above the
+// group bound -> executed = false (the reference's std::runtime_error).
+[[nodiscard]] HipQuantizeResult quantize_affine_q4_rows_hip(HipComputeContext& context,
+                                                            std::span<const float> values,
+                                                            std::size_t rows, std::size_t cols,
+                                                            std::size_t group_size) noexcept;
 // vulkan_q4_gemv.hpp:25-33
 [[nodiscard]] HipValuesResult run_hip_q4_gemv(
     HipComputeContext& context, std::span<const std::uint32_t> packed,

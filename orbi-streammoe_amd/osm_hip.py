@@ -97,6 +97,7 @@ _PROTOTYPES = {
     "osm_swiglu": (c_int, [_H, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
     "osm_rms_norm": (c_int, [_H, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_size_t, c_float, c_void_p]),
     "osm_unpack_nibbles": (c_int, [_H, c_void_p, c_size_t, c_void_p]),
+    "osm_q4_quantize": (c_int, [_H, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_void_p, c_void_p, POINTER(c_float), POINTER(ctypes.c_double)]),
     "osm_q4_gemv_buffers": (c_int, [_H, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t, c_size_t, _H, _H]),
     "osm_q4_projection_create": (c_int, [_H, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_void_p, c_uint32, c_size_t, POINTER(_H)]),
     "osm_q4_projection_destroy": (None, [_H]),
@@ -388,6 +389,22 @@ def unpack_nibbles(ctx, packed) -> np.ndarray:
     out = np.empty(pk.size * 8, np.uint8)
     check(load().osm_unpack_nibbles(ctx.h, _p(pk), pk.size, _p(out)))
     return out
+
+
+def q4_quantize(ctx, values, group):
+    """quantize_affine_q4_rows on the device: (packed, scales, biases, max_err, mean_err)."""
+    v = _c(values, np.float32)
+    if v.ndim != 2:
+        raise ValueError("values must be [rows, cols]")
+    rows, cols = v.shape
+    packed = np.empty(max(rows * (cols // 8), 1), np.uint32)
+    ng = rows * (cols // group) if group and cols % group == 0 else 1
+    scales = np.empty(max(ng, 1), np.float32)
+    biases = np.empty_like(scales)
+    mx, mean = c_float(0), ctypes.c_double(0)
+    check(load().osm_q4_quantize(ctx.h, _p(v), rows, cols, group, _p(packed), _p(scales), _p(biases),
+                                 ctypes.byref(mx), ctypes.byref(mean)))
+    return packed, scales, biases, mx.value, mean.value
 
 
 class Q4ProjectionWeights(_Handle):

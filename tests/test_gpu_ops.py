@@ -137,3 +137,40 @@ def test_rms_norm(ctx):
     assert max_abs(gpu, O.rms_norm(v, 3, 257, w, 1e-6)) <= 3e-5
     with pytest.raises(osm_hip.OsmError):
         osm_hip.run_rms_norm(ctx, v, 3, 257, w[:-1], 1e-6)
+
+
+# ---- affine q4 quantizer (single_expert_pilot.cpp:276-358) -------------------------------
+@pytest.mark.parametrize("rows,cols,group", [(2, 8, 4), (7, 64, 8), (512, 2048, 64), (2048, 512, 64),
+                                             (33, 256, 128), (5, 96, 32)])
+def test_quantizer_bit_exact(ctx, rows, cols, group):
+    rng = np.random.default_rng(rows * 131 + cols + group)
+    if (rows, cols) == (2, 8):  # tests/affine_q4_quantizer_test.cpp:21-52
+        v = np.array([-1.0, -0.5, 0.0, 0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 3.0, 3.0, 3.0, -2.0, -1.0, 0.0, 1.0],
+                     np.float32).reshape(2, 8)
+    else:
+        v = rng.normal(0, 0.05, (rows, cols)).astype(np.float32)
+        v[0, :group] = -0.75  # a flat group
+        v[-1, -group:] = np.round(v[-1, -group:] * 64) / 64  # values with exact half-way ratios
+    gpu = osm_hip.q4_quantize(ctx, v, group)
+    ora = O.quantize_affine_q4_rows(v, rows, cols, group)
+    for a, b in zip(gpu[:3], ora[:3]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert gpu[3] == ora[3]
+    assert abs(gpu[4] - ora[4]) <= 1e-12 * max(ora[4], 1e-30)
+    # Round trip through the device dequant stays within the group bound.
+    d = osm_hip.run_q4_dequant(ctx, gpu[0], rows, cols // 8, gpu[1], gpu[2], group)
+    assert float(np.max(np.abs(d.reshape(rows, cols) - v))) == gpu[3]
+
+
+def test_quantizer_rejections(ctx):
+    v = np.zeros((2, 64), np.float32)
+    with pytest.raises(osm_hip.OsmError) as e:
+        osm_hip.q4_quantize(ctx, v, 48)
+    assert e.value.status == osm_hip.OSM_E_INVALID
+    with pytest.raises(osm_hip.OsmError) as e:
+        osm_hip.q4_quantize(ctx, np.zeros((2, 60), np.float32), 4)
+    assert e.value.status == osm_hip.OSM_E_INVALID
+    v[1, 5] = np.nan
+    with pytest.raises(osm_hip.OsmError) as e:
+        osm_hip.q4_quantize(ctx, v, 64)
+    assert e.value.status == osm_hip.OSM_E_RUNTIME
