@@ -232,6 +232,20 @@ int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache 
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,
                                 uint32_t tokens, int sublayer);
+/* How decodes of several tokens run (no counterpart in the reference, which
+ * pushes tokens through the sublayer one at a time,
+ * src/session/greedy_token_session.cpp:170-192): OSM_PATH_AUTO takes the
+ * grouped GEMMs from 16 tokens on (group 32/64/128, 16-byte aligned input),
+ * OSM_PATH_PER_TOKEN always runs the per-token kernels, OSM_PATH_GROUPED
+ * always buckets (token, slot) pairs by expert and reads each expert once. */
+enum osm_moe_path { OSM_PATH_AUTO = 0, OSM_PATH_PER_TOKEN = 1, OSM_PATH_GROUPED = 2 };
+int osm_moe_layer_set_path(osm_moe_layer l, int path);
+/* A prefill chunk: bf16 x [tokens, D] (device, 16-byte aligned) through the
+ * grouped path, MoE form, y fp32 [tokens, D]; needs a bf16 router. Routing
+ * per token is that of run_qwen_sparse_moe_vulkan_accum on the widened x. */
+int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                                 uint32_t slab_layer, const uint16_t* x_bf16_dev, float* y_dev,
+                                 uint32_t tokens);
 /* Enqueues n_layers decodes back to back, as the reference's decoder stack
  * runs its layers in order (src/model/checkpoint_decoder_stack.cpp:191-204).
  * chained != 0: sublayer form, layer i reads the output of layer i-1 (x_dev

@@ -694,6 +694,26 @@ void osm_graph_destroy(osm_graph g) { delete g; }
 
 extern "C" {
 
+int osm_moe_layer_set_path(osm_moe_layer l, int path) {
+  if (!l) return fail(OSM_E_INVALID, "null layer");
+  if (path < OSM_PATH_AUTO || path > OSM_PATH_GROUPED) return fail(OSM_E_INVALID, "unknown MoE path");
+  l->layer.set_path(static_cast<osm::HipMoePath>(path));
+  return ok();
+}
+
+int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab, uint32_t slab_layer,
+                                 const uint16_t* x_bf16_dev, float* y_dev, uint32_t tokens) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !l || !slab) return fail(OSM_E_INVALID, "null argument");
+  const auto* table = slab->slab.device_table(slab_layer);
+  if (!table) return fail(OSM_E_INVALID, "slab layer out of range");
+  if (slab->slab.experts() != l->layer.config().expert_count)
+    return fail(OSM_E_INVALID, "slab expert count does not match the layer's router");
+  auto r = l->layer.prefill_device_bf16(ctx->ctx, x_bf16_dev, y_dev, tokens, table);
+  return from_diag(r.executed, r.diagnostic);
+  OSM_GUARD_END
+}
+
 int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                uint32_t slab_layer, const float* x_dev, float* y_dev, uint32_t tokens,
                                int sublayer, int phase) {

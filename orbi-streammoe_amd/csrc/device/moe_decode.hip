@@ -748,6 +748,10 @@ int osmd_moe_router(const osmd_moe_args* a, osmd_stream s) {
   }
 }
 
+int osmd_moe_select(const osmd_moe_args* a, osmd_stream s) {
+  return launch_select(*a, static_cast<hipStream_t>(s));
+}
+
 int osmd_moe_route(const osmd_moe_args* a, osmd_stream s) {
   const int r = osmd_moe_router(a, s);
   return r != 0 ? r : launch_select(*a, static_cast<hipStream_t>(s));

@@ -155,6 +155,41 @@ int osmd_moe_router(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_down(const osmd_moe_args* a, osmd_stream s);
 
+/* The selection kernel alone: top-k of a->logits for a->tokens tokens into
+ * ids / weights / mass (and slot_ptrs from expert_table when set). */
+int osmd_moe_select(const osmd_moe_args* a, osmd_stream s);
+
+/* ---- grouped (multi-token) MoE ------------------------------------------
+ * The routed-MoE sublayer for moe.tokens tokens with every (token, slot)
+ * pair bucketed by expert and each expert's gate/up/down run once as an
+ * MFMA grouped GEMM for all its pairs. moe.expert_table must be set; moe.x
+ * is fp32 [T, D], or bf16 [T, D] when x_bf16 (bf16 router, no RMSNorm form).
+ * Workspace sizes for T tokens, P = T * (k + shared) pairs:
+ *   x_terms  bf16 [T][3][D]    x_sums   f32 [T][D/G]
+ *   perm, pair_pos u32 [P]     pair_w   f32 [P]
+ *   tiles    16 B [osmd_moe_grouped_max_tiles()]   tile_count u32 [1]
+ *   h        f32 [P][I]        h_terms  bf16 [P][2][I]   h_sums f32 [P][I/G]
+ *   partial  f32 [P][D]
+ * plus the decode workspace of moe (logits, ids, weights, mass, shared_gate,
+ * x_norm). */
+typedef struct osmd_moe_grouped_args {
+  osmd_moe_args moe;
+  uint32_t x_bf16;
+  uint16_t* x_terms;
+  float* x_sums;
+  uint32_t* perm;
+  uint32_t* pair_pos;
+  float* pair_w;
+  void* tiles;
+  uint32_t* tile_count;
+  float* h;
+  uint16_t* h_terms;
+  float* h_sums;
+  float* partial;
+} osmd_moe_grouped_args;
+size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t experts);
+int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s);
+
 /* Bytes of LDS the down kernel stages for `nslot` slots of width `inter`
  * (the host rejects layers whose staging exceeds 64 KiB). */
 size_t osmd_moe_down_lds_bytes(uint32_t inter, uint32_t nslot);

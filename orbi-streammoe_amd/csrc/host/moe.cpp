@@ -35,6 +35,62 @@ struct HipMoeLayer::Impl {
   // workspace
   DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs, counter;
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
+  // grouped (multi-token) path: allocated on its first use
+  HipMoePath path = HipMoePath::automatic;
+  bool grouped_ready = false;
+  DeviceBytes g_x_terms, g_x_sums, g_perm, g_pair_pos, g_pair_w, g_tiles, g_tile_count, g_h, g_h_terms,
+      g_h_sums, g_partial;
+
+  int ensure_grouped(osmd_stream st) {
+    if (grouped_ready) return 0;
+    const osm_expert_geometry& g = cfg.geometry;
+    const std::size_t T = max_tokens, D = g.hidden, I = g.inter, G = g.group;
+    const std::size_t P = T * nslot();
+    const std::size_t tiles = osmd_moe_grouped_max_tiles(max_tokens, nslot(), cfg.expert_count);
+    int rc = g_x_terms.allocate(T * 3U * D * 2U);
+    if (rc == 0) rc = g_x_sums.allocate(T * (D / G) * 4U);
+    if (rc == 0) rc = g_perm.allocate(P * 4U);
+    if (rc == 0) rc = g_pair_pos.allocate(P * 4U);
+    if (rc == 0) rc = g_pair_w.allocate(P * 4U);
+    if (rc == 0) rc = g_tiles.allocate(tiles * 16U);
+    if (rc == 0) rc = g_tile_count.allocate(4U);
+    if (rc == 0) rc = g_h.allocate(P * I * 4U);
+    if (rc == 0) rc = g_h_terms.allocate(P * 2U * I * 2U);
+    if (rc == 0) rc = g_h_sums.allocate(P * (I / G) * 4U);
+    if (rc == 0) rc = g_partial.allocate(P * D * 4U);
+    if (rc == 0) rc = osmd_zero(g_tile_count.get(), 4U, st);
+    if (rc == 0) grouped_ready = true;
+    return rc;
+  }
+
+  // Whether a decode of `tokens` rows of x goes through the grouped GEMMs.
+  bool grouped_ok(const void* x) const {
+    const std::uint32_t G = cfg.geometry.group;
+    return (G == 32U || G == 64U || G == 128U) && reinterpret_cast<std::uintptr_t>(x) % 16U == 0U;
+  }
+  bool use_grouped(std::uint32_t tokens, const void* x) const {
+    if (path == HipMoePath::per_token) return false;
+    if (path == HipMoePath::grouped) return true;
+    return tokens >= kGroupedMinTokens && grouped_ok(x);
+  }
+
+  osmd_moe_grouped_args grouped_args(const osmd_moe_args& a, bool x_bf16) {
+    osmd_moe_grouped_args ga{};
+    ga.moe = a;
+    ga.x_bf16 = x_bf16 ? 1U : 0U;
+    ga.x_terms = g_x_terms.as<std::uint16_t>();
+    ga.x_sums = g_x_sums.as<float>();
+    ga.perm = g_perm.as<std::uint32_t>();
+    ga.pair_pos = g_pair_pos.as<std::uint32_t>();
+    ga.pair_w = g_pair_w.as<float>();
+    ga.tiles = g_tiles.get();
+    ga.tile_count = g_tile_count.as<std::uint32_t>();
+    ga.h = g_h.as<float>();
+    ga.h_terms = g_h_terms.as<std::uint16_t>();
+    ga.h_sums = g_h_sums.as<float>();
+    ga.partial = g_partial.as<float>();
+    return ga;
+  }
 
   std::uint32_t nslot() const { return cfg.top_k + (cfg.has_shared_expert ? 1U : 0U); }
 
@@ -221,13 +277,69 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
     return r;
   }
   const osmd_moe_args a = impl_->args(x, y, tokens, expert_table, sublayer);
-  const int rc = osmd_moe_decode(&a, context.stream());
+  int rc;
+  if (impl_->use_grouped(tokens, x)) {
+    if (!impl_->grouped_ok(x)) {
+      r.diagnostic = "grouped MoE needs group 32, 64 or 128 and a 16-byte aligned input";
+      return r;
+    }
+    rc = impl_->ensure_grouped(context.stream());
+    if (rc == 0) {
+      const osmd_moe_grouped_args ga = impl_->grouped_args(a, false);
+      rc = osmd_moe_grouped(&ga, context.stream());
+    }
+  } else {
+    rc = osmd_moe_decode(&a, context.stream());
+  }
   if (rc != 0) {
     r.diagnostic = hip_error("MoE decode launch failed", rc);
     return r;
   }
   r.executed = true;
   r.diagnostic = "HIP routed MoE decode enqueued";
+  return r;
+}
+
+void HipMoeLayer::set_path(HipMoePath path) noexcept {
+  if (impl_) impl_->path = path;
+}
+
+HipMoePath HipMoeLayer::path() const noexcept { return impl_ ? impl_->path : HipMoePath::automatic; }
+
+HipDispatchResult HipMoeLayer::prefill_device_bf16(HipComputeContext& context, const std::uint16_t* x_bf16,
+                                                   float* y, std::uint32_t tokens,
+                                                   const std::uint8_t* const* expert_table) noexcept {
+  HipDispatchResult r;
+  if (!valid()) {
+    r.diagnostic = "MoE layer is not valid";
+    return r;
+  }
+  if (!context.activate(&r.diagnostic)) return r;
+  if (tokens == 0 || tokens > impl_->max_tokens || x_bf16 == nullptr || y == nullptr || expert_table == nullptr) {
+    r.diagnostic = "MoE prefill: invalid arguments";
+    return r;
+  }
+  if (impl_->router_dtype != OSM_META_BF16) {
+    r.diagnostic = "MoE prefill from bf16 input needs a bf16 router";
+    return r;
+  }
+  if (!impl_->grouped_ok(x_bf16)) {
+    r.diagnostic = "grouped MoE needs group 32, 64 or 128 and a 16-byte aligned input";
+    return r;
+  }
+  int rc = impl_->ensure_grouped(context.stream());
+  if (rc == 0) {
+    osmd_moe_args a = impl_->args(nullptr, y, tokens, expert_table, false);
+    a.x = reinterpret_cast<const float*>(x_bf16);  // read as bf16 (x_bf16 = 1)
+    const osmd_moe_grouped_args ga = impl_->grouped_args(a, true);
+    rc = osmd_moe_grouped(&ga, context.stream());
+  }
+  if (rc != 0) {
+    r.diagnostic = hip_error("MoE prefill launch failed", rc);
+    return r;
+  }
+  r.executed = true;
+  r.diagnostic = "HIP grouped MoE prefill enqueued";
   return r;
 }
 

@@ -610,6 +610,13 @@ struct HipMoeResult {
 // Per-layer state that stays resident: router [E, D] and shared-expert gate
 // vector [D] (bf16 or f32), optional RMSNorm weight, the shared expert, and
 // scratch for up to max_tokens tokens.
+// How a decode of several tokens runs: the per-token kernels (every token
+// reads its picks' weights), or grouped GEMMs (tokens bucketed by expert,
+// each expert's weights read once for all its tokens). automatic takes the
+// grouped path from kGroupedMinTokens tokens on.
+enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2 };
+inline constexpr std::uint32_t kGroupedMinTokens = 16;
+
 class HipMoeLayer {
  public:
   HipMoeLayer();
@@ -641,6 +648,14 @@ class HipMoeLayer {
                                                 std::uint32_t tokens,
                                                 const std::uint8_t* const* expert_table,
                                                 bool sublayer) noexcept;
+  void set_path(HipMoePath path) noexcept;
+  [[nodiscard]] HipMoePath path() const noexcept;
+  // A prefill chunk in bf16 ([tokens, D], device) through the grouped path:
+  // bf16 router, MoE form (no RMSNorm / residual), y fp32 [tokens, D].
+  [[nodiscard]] HipDispatchResult prefill_device_bf16(HipComputeContext& context,
+                                                      const std::uint16_t* x_bf16, float* y,
+                                                      std::uint32_t tokens,
+                                                      const std::uint8_t* const* expert_table) noexcept;
   // One kernel of a decode (0 router GEMV, 1 selection + gate/up + SwiGLU,
   // 2 down + weighted accumulate), for per-kernel timing; 1 and 2 read the
   // workspace the previous kernels of this layer left.

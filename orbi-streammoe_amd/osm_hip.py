@@ -22,6 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libosm_hip.so")
 
 OSM_OK, OSM_E_INVALID, OSM_E_RUNTIME, OSM_E_DEVICE = 0, 1, 2, 3
+PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED = 0, 1, 2
 F32, F16, BF16 = 0, 1, 2
 
 
@@ -129,6 +130,8 @@ _PROTOTYPES = {
     "osm_moe_layer_decode_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_decode_layers": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_layer_launch_phase": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int, c_int]),
+    "osm_moe_layer_set_path": (c_int, [_H, c_int]),
+    "osm_moe_layer_prefill_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32]),
     "osm_decode_graph_create": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int, POINTER(_H)]),
     "osm_graph_capture_begin": (c_int, [_H]),
     "osm_graph_capture_end": (c_int, [_H, POINTER(_H)]),
@@ -565,6 +568,13 @@ class MoeLayer(_Handle):
 
     def decode_device(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer=False):
         check(load().osm_moe_layer_decode_device(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0))
+
+    def set_path(self, path):
+        """PATH_AUTO, PATH_PER_TOKEN or PATH_GROUPED."""
+        check(load().osm_moe_layer_set_path(self.h, path))
+
+    def prefill_device(self, slab, slab_layer, x_bf16_ptr, y_ptr, tokens):
+        check(load().osm_moe_layer_prefill_device(self.ctx.h, self.h, slab.h, slab_layer, x_bf16_ptr, y_ptr, tokens))
 
     def launch_phase(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer, phase):
         check(load().osm_moe_layer_launch_phase(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0, phase))

@@ -1,0 +1,92 @@
+"""The grouped (multi-token) MoE path: every (token, slot) pair bucketed by
+expert, each expert's gate/up/down run once as an MFMA grouped GEMM.
+
+The reference has no multi-token MoE; its oracle is the per-token loop
+(src/session/greedy_token_session.cpp:170-192 pushes tokens one at a time), so
+each token is checked against the per-token oracle at the decode bars: ids
+bit-exact, weights and shared gate within 1e-6, output within 1e-3 relative
+L2. The grouped GEMMs split activations into bf16 terms (3 for the router, 2
+for the experts), so they also agree with the per-token fp32 kernels to about
+1e-5."""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import osm_hip
+from helpers import max_abs, random_blob, rel_l2
+from test_gpu_moe import QwenLayer, assert_token_parity
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("tokens", [16, 48])
+def test_grouped_decode_qwen_shape(ctx, tokens):
+    seed = 41
+    L = QwenLayer(ctx, seed, max_tokens=64)
+    x = O.synth_tokens(seed, 3000, tokens, L.D)
+    L.moe.set_path(osm_hip.PATH_GROUPED)
+    gpu = L.moe.run_slab(L.slab, 0, x)
+    L.moe.set_path(osm_hip.PATH_PER_TOKEN)
+    per_token = L.moe.run_slab(L.slab, 0, x)
+    assert np.array_equal(gpu["ids"], per_token["ids"])
+    assert rel_l2(gpu["out"], per_token["out"]) <= 2e-5
+    for t in range(tokens):
+        assert_token_parity(gpu, t, L.oracle_token(x[t]))
+
+
+def test_grouped_sublayer(ctx):
+    seed = 42
+    L = QwenLayer(ctx, seed, max_tokens=16, norm=True)
+    x = O.synth_tokens(seed, 0, 16, L.D) * np.float32(2.0)
+    L.moe.set_path(osm_hip.PATH_GROUPED)
+    gpu = L.moe.run_slab(L.slab, 0, x, sublayer=True)
+    for t in range(16):
+        assert_token_parity(gpu, t, L.oracle_token(x[t], sublayer=True), sublayer=True)
+
+
+def test_grouped_small_f32_meta_f32_router_no_shared(ctx):
+    # f32 router (the per-token router kernel feeds the grouped experts),
+    # f32 metadata, group 32, no shared expert, 20 tokens over 64 experts.
+    rng = np.random.default_rng(43)
+    D, I, G, E, k, T = 256, 128, 32, 64, 6, 20
+    g = osm_hip.geometry(D, I, G, osm_hip.F32)
+    blobs = [random_blob(rng, D, I, G, O.META_F32)[0] for _ in range(E)]
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blobs[e])
+    # Router scale as in the reference's fixtures (logits of order 1), where
+    # the 1e-6 weight bar applies.
+    router = rng.normal(0, 0.1, (E, D)).astype(np.float32)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, router, osm_hip.F32, max_tokens=T)
+    moe.set_path(osm_hip.PATH_GROUPED)
+    x = rng.normal(0, 1, (T, D)).astype(np.float32)
+    gpu = moe.run_slab(slab, 0, x)
+    for t in range(T):
+        ora = O.qwen_sparse_moe(x[t], router, blobs, None, None, D, I, G, O.META_F32, k)
+        assert np.array_equal(gpu["ids"][t], ora["ids"])
+        assert max_abs(gpu["weights"][t], ora["weights"]) <= 1e-6
+        assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
+
+
+def test_prefill_bf16_chunk(ctx):
+    # A 256-token prefill chunk in bf16 at the Qwen3-Next shape: every token
+    # against the per-token kernels on the widened input, a sample of tokens
+    # against the oracle.
+    seed, T = 44, 256
+    L = QwenLayer(ctx, seed, max_tokens=T)
+    xf = O.synth_tokens(seed, 9000, T, L.D)
+    bits = ((xf.view(np.uint32) + 0x7FFF + ((xf.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    xw = (bits.astype(np.uint32) << 16).view(np.float32)  # the bf16 values, widened exactly
+    xb, y = ctx.alloc(T * L.D * 2), ctx.alloc(T * L.D * 4)
+    xb.upload(bits)
+    L.moe.prefill_device(L.slab, 0, xb.ptr, y.ptr, T)
+    got = y.download(np.float32, T * L.D).reshape(T, L.D)
+    L.moe.set_path(osm_hip.PATH_PER_TOKEN)
+    ref = L.moe.run_slab(L.slab, 0, xw)
+    for t in range(T):
+        assert rel_l2(got[t], ref["out"][t]) <= 2e-5, t
+    for t in range(0, T, 32):
+        ora = L.oracle_token(xw[t])
+        assert np.array_equal(ref["ids"][t], ora["ids"])
+        assert rel_l2(got[t], ora["out"]) <= 1e-3
