@@ -38,6 +38,8 @@ D, I, G, E, K = 2048, 512, 64, 512, 10
 EXPERT_BYTES = 1769472  # one expert: gate/up/down q4 + bf16 scale/bias
 ROUTER_BYTES = E * D * 2
 SHARED_GATE_BYTES = D * 2
+PREFILL_TOKENS = 512
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -49,6 +51,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--phase-rounds", type=int, default=20)
     ap.add_argument("--cpu-tokens", type=int, default=64, help="token-layers in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the decode-batch and prefill measurements")
     ap.add_argument("--counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no benchmark: summarise two rocprofv3 --pmc counter_collection.csv files "
                          "(FETCH_SIZE, WRITE_SIZE) of a run with --copy-probe-mb into HBM bytes per dispatch")
@@ -72,7 +76,7 @@ def build_model(ctx, layers, seed):
         sg = osm_hip.synth_shared_gate_bf16(ctx, seed, l, D)
         nw = osm_hip.synth_norm_weight(ctx, seed, l, D)
         shared = osm_hip.synth_expert_blob(ctx, seed, l, 0xFFFFFFFF, g)
-        moes.append(osm_hip.MoeLayer(ctx, g, E, K, router, osm_hip.BF16, sg, nw, shared, max_tokens=1))
+        moes.append(osm_hip.MoeLayer(ctx, g, E, K, router, osm_hip.BF16, sg, nw, shared, max_tokens=PREFILL_TOKENS))
     return g, slab, moes
 
 
@@ -138,6 +142,89 @@ def summarize_counters(fetch_csv, write_csv, probe_mb):
             "hbm_bytes_per_dispatch": int(round((f * ff + w * fw) * 1024)),
         }
     return out
+
+
+def unique_experts(ctx, moes, slab, seed, batch, first_token, layers=4):
+    """Mean distinct routed experts per layer-step for `batch` tokens, from
+    the routing the layers actually produce (host round trip, untimed)."""
+    n = []
+    for l in range(layers):
+        x = osm_hip.synth_tokens(ctx, seed, first_token + l * batch, batch, D)
+        n.append(len(set(int(e) for e in moes[l].run_slab(slab, l, x)["ids"].reshape(-1))))
+    return float(np.mean(n))
+
+
+def decode_batches(ctx, moes, slab, args):
+    """Config 2: decode batches of B tokens through each layer copy in turn,
+    with fresh tokens every step, on the per-token kernels and on the grouped
+    GEMMs. Bytes are counted from the actual routing: (distinct experts +
+    shared) x expert bytes + router + shared-gate vector + activations."""
+    L = len(moes)
+    out = {}
+    steps = max(3, args.steps // 20)
+    for B in (4, 16, 64):
+        n_tok = (steps + 1) * L * B
+        xs = ctx.alloc(n_tok * D * 4)
+        osm_hip.synth_tokens_device(ctx, args.seed, 200000, n_tok, D, xs.ptr)
+        ys = ctx.alloc(L * B * D * 4)
+        entry = {}
+        for name, path in (("per_token", osm_hip.PATH_PER_TOKEN), ("grouped", osm_hip.PATH_GROUPED)):
+            for m in moes:
+                m.set_path(path)
+
+            def step(i):
+                osm_hip.decode_layers(ctx, moes, list(range(L)), slab, xs.ptr.value + i * L * B * D * 4, ys.ptr, None, B,
+                                      chained=False)
+
+            step(steps)  # warm (and the grouped path's first-use workspace)
+            ms = time_steps(ctx, steps, step)
+            entry[name + "_us_per_layer_step"] = round(ms / steps * 1000.0 / L, 2)
+        for m in moes:
+            m.set_path(osm_hip.PATH_AUTO)
+        uniq = unique_experts(ctx, moes, slab, args.seed, B, 300000)
+        bytes_step = (uniq + 1) * EXPERT_BYTES + ROUTER_BYTES + SHARED_GATE_BYTES + 2 * B * D * 4
+        best = min(entry["per_token_us_per_layer_step"], entry["grouped_us_per_layer_step"])
+        entry.update({"distinct_experts": round(uniq, 1), "bytes_per_layer_step": int(bytes_step),
+                      "best_us_per_token": round(best / B, 3),
+                      "best_GBps": round(bytes_step / (best * 1e-6) / 1e9, 1)})
+        out[str(B)] = entry
+        log(f"[bench] decode batch {B}: {json.dumps(entry)}")
+        del xs, ys
+    return out
+
+
+def prefill(ctx, moes, slab, args, layers=8):
+    """Config 4: a 512-token bf16 prefill chunk through `layers` layer copies
+    (grouped GEMMs on the matrix cores), one fresh chunk per step."""
+    T = PREFILL_TOKENS
+    steps = max(3, args.steps // 20)
+    xs = []
+    for l in range(layers):
+        xf = osm_hip.synth_tokens(ctx, args.seed, 400000 + l * T, T, D)
+        u = xf.view(np.uint32)
+        bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        a = ctx.alloc(T * D * 2)
+        a.upload(bits)
+        xs.append(a)
+    y = ctx.alloc(T * D * 4)
+
+    def step(_i):
+        for l in range(layers):
+            moes[l].prefill_device(slab, l, xs[l].ptr, y.ptr, T)
+
+    step(0)
+    ms = time_steps(ctx, steps, step)
+    us = ms / steps * 1000.0 / layers
+    uniq = unique_experts(ctx, moes, slab, args.seed, T, 500000, layers=2)
+    bytes_chunk = (uniq + 1) * EXPERT_BYTES + ROUTER_BYTES + SHARED_GATE_BYTES + T * D * 2 + T * D * 4
+    flops = 2.0 * T * (K + 1) * 3 * D * I + 2.0 * T * D * (E + 1)
+    res = {"tokens": T, "layer_copies": layers, "us_per_chunk_layer": round(us, 1),
+           "us_per_token_layer": round(us / T, 4), "distinct_experts": round(uniq, 1),
+           "bytes_per_chunk_layer": int(bytes_chunk), "GBps": round(bytes_chunk / (us * 1e-6) / 1e9, 1),
+           "algorithmic_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
+           "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    log(f"[bench] prefill: {json.dumps(res)}")
+    return res
 
 
 def cpu_baseline(seed, tokens):
@@ -296,6 +383,11 @@ def main():
     dk = kernels[dominant]
     log(f"[bench] kernels: {json.dumps(kernels)}")
 
+    extras = {}
+    if not args.no_extras:
+        extras["decode_batches"] = decode_batches(ctx, moes, slab, args)
+        extras["prefill"] = prefill(ctx, moes, slab, args)
+
     cpu = None
     if args.cpu_tokens > 0:
         try:
@@ -340,6 +432,7 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    result.update(extras)
     print(json.dumps(result), flush=True)
 
     if args.copy_probe_mb > 0:

@@ -183,6 +183,11 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
   const u32x4 v = ldg<u32x4>(p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ldg8(const void* p) {
+  const u32x2 v = ldg<u32x2>(p);
+  return make_uint2(v.x, v.y);
+}
 
 // Raw metadata bits (bf16/f16 in the low 16 bits, or f32 bits) and their
 // widening, split so a load can be issued long before its value is needed.

@@ -50,6 +50,7 @@ constexpr uint32_t kGroupedThreads = kGroupedWaves * kWave;
 constexpr uint32_t kRowBlocksPerWave = 2;
 constexpr uint32_t kRowsPerWorkgroup = kGroupedWaves * kRowBlocksPerWave * kBlockRows;  // 128
 constexpr uint32_t kRouterSplit = 3;
+constexpr uint32_t kRouterGemmMinTokens = 64;
 constexpr uint32_t kActSplit = 2;
 
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
@@ -264,9 +265,16 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
 // Grouped q4 GEMM over the tile list. Workgroup = one tile (<= 16 pairs) x
 // 128 weight rows (4 waves x 2 blocks of 16). PROJ == 2: gate and up with
 // SwiGLU -> h[pair, row]; PROJ == 1: down, times the pair's weight ->
-// out[pair, row]. A rows: the pair's token (PROJ 2) or the pair itself
-// (PROJ 1). S = G / 32 MFMA steps per group; lane k-slot q reads words
-// S*q .. S*q+S-1 of each group, step s using word S*q + s.
+// out[pair, row]. A rows: the pair's token (PROJ 2) or the pair (PROJ 1).
+//
+// K runs in chunks of 32 * NSTEP columns. The A chunk (both bf16 terms of the
+// tile's 16 rows) and its group sums are staged in LDS, double-buffered, and
+// shared by the four waves; each wave keeps the next chunk's packed words and
+// metadata in flight in registers while it multiplies the current one, so a
+// chunk's memory latency hides behind the previous chunk's MFMAs.
+//
+// S = G / 32 MFMA steps per group; lane k-slot q uses words S*q .. S*q+S-1
+// of each group (step s: word S*q + s), so one lane load covers a group.
 struct GroupedParams {
   osm_expert_geometry g;
   const uint16_t* terms;  // A terms [rows][kActSplit][K]
@@ -282,35 +290,85 @@ struct GroupedParams {
   float* out;  // [P][N]
 };
 
-template <int META, int PROJ, int S>
+// Metadata of GPC consecutive groups of one row, kept as loaded: 16-bit
+// values two to a register (bf16 / f16), f32 one to a register.
+template <int META, int GPC>
+struct MetaRun {
+  static constexpr int kRegs = META == OSM_META_F32 ? GPC : (GPC + 1) / 2;
+  uint32_t r[kRegs];
+  __device__ __forceinline__ void load(const uint8_t* base, size_t idx) {
+    if constexpr (META != OSM_META_F32 && GPC == 4) {
+      const uint2 v = ldg8(base + idx * 2u);
+      r[0] = v.x;
+      r[1] = v.y;
+    } else if constexpr (META == OSM_META_F32 && GPC == 4) {
+      const uint4 v = ldg16(base + idx * 4u);
+      r[0] = v.x; r[1] = v.y; r[2] = v.z; r[3] = v.w;
+    } else if constexpr (META == OSM_META_F32) {
+#pragma unroll
+      for (int i = 0; i < GPC; ++i) r[i] = meta_bits<META>(base, idx + i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kRegs; ++i) {
+        const uint32_t lo = meta_bits<META>(base, idx + 2 * i);
+        const uint32_t hi = 2 * i + 1 < GPC ? meta_bits<META>(base, idx + 2 * i + 1) : 0u;
+        r[i] = lo | (hi << 16);
+      }
+    }
+  }
+  __device__ __forceinline__ float get(int i) const {
+    if constexpr (META == OSM_META_F32)
+      return __uint_as_float(r[i]);
+    else
+      return meta_widen<META>((r[i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
+  }
+};
+
+template <int S>
+__device__ __forceinline__ void word_run(const uint8_t* p, uint32_t* out) {
+  if constexpr (S == 4) {
+    const uint4 v = ldg16(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  } else if constexpr (S == 2) {
+    const uint2 v = ldg8(p);
+    out[0] = v.x; out[1] = v.y;
+  } else {
+    out[0] = ldg<uint32_t>(p);
+  }
+}
+
+template <int META, int PROJ, int S, int NSTEP>
 __global__ __launch_bounds__(kGroupedThreads) void grouped_kernel(GroupedParams p) {
+  constexpr int GPC = NSTEP / S;        // groups per chunk
+  constexpr uint32_t KC = 32u * NSTEP;  // columns per chunk
+  constexpr uint32_t RS = KC + 8u;      // LDS row stride (bf16), padded against bank conflicts
+  constexpr uint32_t kU4PerChunk = kActSplit * kTileTokens * KC / 8u;
+  __shared__ __align__(16) uint16_t a_lds[2][kActSplit][kTileTokens][RS];
+  __shared__ __align__(16) float xs_lds[2][GPC][kTileTokens];
+  __shared__ uint32_t arow_lds[kTileTokens];
+
   const uint32_t tile_idx = blockIdx.x;
   if (tile_idx >= *p.tile_count) return;  // uniform over the workgroup
   const Tile tl = p.tiles[tile_idx];
-  const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid % kWave, wave = tid / kWave;
   const uint32_t m = lane % 16u, q = lane / 16u;
   const uint32_t D = p.g.hidden, I = p.g.inter, G = p.g.group;
   const uint32_t K = PROJ == 2 ? D : I;
   const uint32_t N = PROJ == 2 ? I : D;
   const uint32_t ngroups = K / G;
+  const uint32_t nchunks = K / KC;
   const osm_expert_offsets off = osm_expert_layout(p.g);
 
   const uint8_t* blob = tl.expert < p.expert_count ? p.expert_table[tl.expert] : p.shared_expert;
   if (blob == nullptr) blob = p.fallback;
 
-  // A row of this lane (MFMA row m) and the pairs of its D rows (4q + j).
-  const uint32_t mm = m < tl.count ? m : tl.count - 1u;
-  const uint32_t pair_a = tl.start + mm;
-  const uint32_t arow = PROJ == 2 ? p.perm[pair_a] / p.nslot : pair_a;
-  const uint16_t* a_base = p.terms + static_cast<size_t>(arow) * kActSplit * K;
-  uint32_t drow[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t jj = 4u * q + j < tl.count ? 4u * q + j : tl.count - 1u;
-    drow[j] = PROJ == 2 ? p.perm[tl.start + jj] / p.nslot : tl.start + jj;
+  if (tid < kTileTokens) {  // A source row of each tile row (clamped into the tile)
+    const uint32_t pair = tl.start + (tid < tl.count ? tid : tl.count - 1u);
+    arow_lds[tid] = PROJ == 2 ? p.perm[pair] / p.nslot : pair;
   }
+  __syncthreads();
 
-  // This lane's weight rows (B column m of each row block).
   uint32_t wrow[kRowBlocksPerWave];
 #pragma unroll
   for (uint32_t nb = 0; nb < kRowBlocksPerWave; ++nb) {
@@ -320,7 +378,60 @@ __global__ __launch_bounds__(kGroupedThreads) void grouped_kernel(GroupedParams 
   const size_t q_off[2] = {PROJ == 2 ? off.gate_q : off.down_q, off.up_q};
   const size_t s_off[2] = {PROJ == 2 ? off.gate_s : off.down_s, off.up_s};
   const size_t b_off[2] = {PROJ == 2 ? off.gate_b : off.down_b, off.up_b};
-  const uint32_t words_per_row = K / 8u;
+  const size_t row_bytes = static_cast<size_t>(K) / 2u;
+
+  // Register sets: packed words and metadata of one chunk.
+  struct WSet {
+    uint32_t w[kRowBlocksPerWave][PROJ][NSTEP];
+    MetaRun<META, GPC> sb[kRowBlocksPerWave][PROJ], bb[kRowBlocksPerWave][PROJ];
+  };
+  auto load_w = [&](uint32_t c, WSet& W) {
+    const uint32_t g0 = c * GPC;
+#pragma unroll
+    for (uint32_t nb = 0; nb < kRowBlocksPerWave; ++nb)
+#pragma unroll
+      for (int pr = 0; pr < PROJ; ++pr) {
+        const uint8_t* qrow = blob + q_off[pr] + static_cast<size_t>(wrow[nb]) * row_bytes;
+#pragma unroll
+        for (int gg = 0; gg < GPC; ++gg)
+          word_run<S>(qrow + ((g0 + gg) * (G / 8u) + S * q) * 4u, &W.w[nb][pr][gg * S]);
+        const size_t mi = static_cast<size_t>(wrow[nb]) * ngroups + g0;
+        W.sb[nb][pr].load(blob + s_off[pr], mi);
+        W.bb[nb][pr].load(blob + b_off[pr], mi);
+      }
+  };
+  // A chunk: 16-byte units, thread tid takes units tid, tid + 256, ...
+  constexpr uint32_t kU4PerThread = (kU4PerChunk + kGroupedThreads - 1) / kGroupedThreads;
+  uint4 areg[kU4PerThread];
+  float xreg = 0.0f;
+  auto load_a = [&](uint32_t c) {
+    const uint32_t k0 = c * KC;
+#pragma unroll
+    for (uint32_t i = 0; i < kU4PerThread; ++i) {
+      const uint32_t u = tid + i * kGroupedThreads;
+      if (u < kU4PerChunk) {
+        const uint32_t term = u / (kTileTokens * KC / 8u);
+        const uint32_t rem = u % (kTileTokens * KC / 8u);
+        const uint32_t row = rem / (KC / 8u), cu = rem % (KC / 8u);
+        areg[i] = ldg16(p.terms + (static_cast<size_t>(arow_lds[row]) * kActSplit + term) * K + k0 + cu * 8u);
+      }
+    }
+    if (tid < GPC * kTileTokens)
+      xreg = p.sums[static_cast<size_t>(arow_lds[tid % kTileTokens]) * ngroups + c * GPC + tid / kTileTokens];
+  };
+  auto store_a = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t i = 0; i < kU4PerThread; ++i) {
+      const uint32_t u = tid + i * kGroupedThreads;
+      if (u < kU4PerChunk) {
+        const uint32_t term = u / (kTileTokens * KC / 8u);
+        const uint32_t rem = u % (kTileTokens * KC / 8u);
+        const uint32_t row = rem / (KC / 8u), cu = rem % (KC / 8u);
+        *reinterpret_cast<uint4*>(&a_lds[buf][term][row][cu * 8u]) = areg[i];
+      }
+    }
+    if (tid < GPC * kTileTokens) xs_lds[buf][tid / kTileTokens][tid % kTileTokens] = xreg;
+  };
 
   f32x4 total[kRowBlocksPerWave][PROJ];
 #pragma unroll
@@ -328,56 +439,49 @@ __global__ __launch_bounds__(kGroupedThreads) void grouped_kernel(GroupedParams 
 #pragma unroll
     for (int pr = 0; pr < PROJ; ++pr) total[nb][pr] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  struct Loads {
-    uint32_t w[kRowBlocksPerWave][PROJ][S];
-    uint32_t sb[kRowBlocksPerWave][PROJ], bb[kRowBlocksPerWave][PROJ];
-    uint4 a[S][kActSplit];
-    float xs[4];
-  };
-  auto load = [&](uint32_t gi) {
-    Loads L;
+  WSet cur, nxt;
+  load_w(0, cur);
+  load_a(0);
+  store_a(0);
+  __syncthreads();
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const uint32_t buf = c & 1u;
+    const bool more = c + 1u < nchunks;
+    if (more) {
+      load_w(c + 1u, nxt);
+      load_a(c + 1u);
+    }
 #pragma unroll
-    for (uint32_t nb = 0; nb < kRowBlocksPerWave; ++nb)
+    for (int gg = 0; gg < GPC; ++gg) {
+      bf16x8 a[S][kActSplit];
 #pragma unroll
-      for (int pr = 0; pr < PROJ; ++pr) {
-        const uint8_t* qrow = blob + q_off[pr] + static_cast<size_t>(wrow[nb]) * words_per_row * 4u;
-        const uint32_t w0 = gi * (G / 8u) + S * q;
+      for (int s2 = 0; s2 < S; ++s2)
 #pragma unroll
-        for (int s = 0; s < S; ++s) L.w[nb][pr][s] = ldg<uint32_t>(qrow + (w0 + s) * 4u);
-        const size_t mi = static_cast<size_t>(wrow[nb]) * ngroups + gi;
-        L.sb[nb][pr] = meta_bits<META>(blob + s_off[pr], mi);
-        L.bb[nb][pr] = meta_bits<META>(blob + b_off[pr], mi);
-      }
+        for (uint32_t t = 0; t < kActSplit; ++t)
+          a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&a_lds[buf][t][m][(gg * (G / 8u) + S * q + s2) * 8u]));
+      const float4 xs = *reinterpret_cast<const float4*>(&xs_lds[buf][gg][4u * q]);
 #pragma unroll
-    for (int s = 0; s < S; ++s)
+      for (uint32_t nb = 0; nb < kRowBlocksPerWave; ++nb)
 #pragma unroll
-      for (uint32_t t = 0; t < kActSplit; ++t)
-        L.a[s][t] = ldg16(a_base + static_cast<size_t>(t) * K + (gi * (G / 8u) + S * q + s) * 8u);
+        for (int pr = 0; pr < PROJ; ++pr) {
+          f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) L.xs[j] = p.sums[static_cast<size_t>(drow[j]) * ngroups + gi];
-    return L;
-  };
-
-  Loads cur = load(0);
-  for (uint32_t gi = 0; gi < ngroups; ++gi) {
-    const Loads nxt = load(gi + 1u < ngroups ? gi + 1u : gi);  // clamped: always in bounds
+          for (int s2 = 0; s2 < S; ++s2) {
+            const bf16x8 b = nibble_operand(cur.w[nb][pr][gg * S + s2]);
 #pragma unroll
-    for (uint32_t nb = 0; nb < kRowBlocksPerWave; ++nb)
-#pragma unroll
-      for (int pr = 0; pr < PROJ; ++pr) {
-        f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const bf16x8 b = nibble_operand(cur.w[nb][pr][s]);
-#pragma unroll
-          for (uint32_t t = 0; t < kActSplit; ++t) d = mfma(as_operand(cur.a[s][t]), b, d);
+            for (uint32_t t = 0; t < kActSplit; ++t) d = mfma(a[s2][t], b, d);
+          }
+          const float sc = cur.sb[nb][pr].get(gg);
+          const float cb = cur.bb[nb][pr].get(gg) - 128.0f * sc;
+          total[nb][pr][0] += sc * d[0] + cb * xs.x;
+          total[nb][pr][1] += sc * d[1] + cb * xs.y;
+          total[nb][pr][2] += sc * d[2] + cb * xs.z;
+          total[nb][pr][3] += sc * d[3] + cb * xs.w;
         }
-        const float sc = meta_widen<META>(cur.sb[nb][pr]);
-        const float c = meta_widen<META>(cur.bb[nb][pr]) - 128.0f * sc;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) total[nb][pr][j] += sc * d[j] + c * cur.xs[j];
-      }
-    cur = nxt;
+    }
+    if (more) store_a(buf ^ 1u);
+    __syncthreads();
+    if (more) cur = nxt;
   }
 
 #pragma unroll
@@ -414,12 +518,23 @@ __global__ void combine_kernel(const float* __restrict__ partial, const uint32_t
   }
 }
 
+template <int META, int PROJ, int S>
+void launch_grouped_s(const GroupedParams& gp, dim3 grid, hipStream_t st) {
+  // gate/up keep two projections' words in flight: 128-column chunks keep
+  // the registers under 256 (two waves per SIMD); down takes 256 columns.
+  const uint32_t K = PROJ == 2 ? gp.g.hidden : gp.g.inter;
+  if (PROJ == 1 && K % 256u == 0)
+    grouped_kernel<META, PROJ, S, 8><<<grid, kGroupedThreads, 0, st>>>(gp);
+  else
+    grouped_kernel<META, PROJ, S, 4><<<grid, kGroupedThreads, 0, st>>>(gp);  // K % 128 == 0
+}
+
 template <int META, int PROJ>
 void launch_grouped_meta(const GroupedParams& gp, dim3 grid, hipStream_t st) {
   switch (gp.g.group) {
-    case 32: grouped_kernel<META, PROJ, 1><<<grid, kGroupedThreads, 0, st>>>(gp); break;
-    case 64: grouped_kernel<META, PROJ, 2><<<grid, kGroupedThreads, 0, st>>>(gp); break;
-    default: grouped_kernel<META, PROJ, 4><<<grid, kGroupedThreads, 0, st>>>(gp); break;
+    case 32: launch_grouped_s<META, PROJ, 1>(gp, grid, st); break;
+    case 64: launch_grouped_s<META, PROJ, 2>(gp, grid, st); break;
+    default: launch_grouped_s<META, PROJ, 4>(gp, grid, st); break;
   }
 }
 
@@ -469,7 +584,9 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   }
   const size_t groups = static_cast<size_t>(T) * (D / G);
   int r = 0;
-  if (m.router_dtype == OSM_META_BF16) {
+  // Up to 64 tokens the per-token router kernel (one wavefront per router
+  // row and token) has the shorter latency; beyond, the MFMA router GEMM.
+  if (m.router_dtype == OSM_META_BF16 && (xbf16 || T > kRouterGemmMinTokens)) {
     if (xbf16)
       prepare_kernel<true, kRouterSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
     else
@@ -482,7 +599,7 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
         has_shared ? static_cast<const uint16_t*>(m.shared_gate_vec) : nullptr, m.expert_count, m.logits,
         m.shared_gate);
   } else {
-    // fp32 / f16 routers: the decode router kernel, one token per grid row.
+    // The decode router kernel, one token per grid row (fp32 input).
     osmd_moe_args ra = m;
     ra.flags &= ~static_cast<uint32_t>(OSMD_MOE_RMSNORM);  // x is normalised above
     ra.x = static_cast<const float*>(xin);

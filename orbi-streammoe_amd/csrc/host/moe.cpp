@@ -65,8 +65,9 @@ struct HipMoeLayer::Impl {
 
   // Whether a decode of `tokens` rows of x goes through the grouped GEMMs.
   bool grouped_ok(const void* x) const {
-    const std::uint32_t G = cfg.geometry.group;
-    return (G == 32U || G == 64U || G == 128U) && reinterpret_cast<std::uintptr_t>(x) % 16U == 0U;
+    const osm_expert_geometry& g = cfg.geometry;
+    return (g.group == 32U || g.group == 64U || g.group == 128U) && g.hidden % 128U == 0U &&
+           g.inter % 128U == 0U && reinterpret_cast<std::uintptr_t>(x) % 16U == 0U;
   }
   bool use_grouped(std::uint32_t tokens, const void* x) const {
     if (path == HipMoePath::per_token) return false;
@@ -280,7 +281,7 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
   int rc;
   if (impl_->use_grouped(tokens, x)) {
     if (!impl_->grouped_ok(x)) {
-      r.diagnostic = "grouped MoE needs group 32, 64 or 128 and a 16-byte aligned input";
+      r.diagnostic = "grouped MoE needs group 32, 64 or 128, hidden and intermediate multiples of 128, and a 16-byte aligned input";
       return r;
     }
     rc = impl_->ensure_grouped(context.stream());
@@ -324,7 +325,7 @@ HipDispatchResult HipMoeLayer::prefill_device_bf16(HipComputeContext& context, c
     return r;
   }
   if (!impl_->grouped_ok(x_bf16)) {
-    r.diagnostic = "grouped MoE needs group 32, 64 or 128 and a 16-byte aligned input";
+    r.diagnostic = "grouped MoE needs group 32, 64 or 128, hidden and intermediate multiples of 128, and a 16-byte aligned input";
     return r;
   }
   int rc = impl_->ensure_grouped(context.stream());
