@@ -235,7 +235,7 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
 /* How decodes of several tokens run (no counterpart in the reference, which
  * pushes tokens through the sublayer one at a time,
  * src/session/greedy_token_session.cpp:170-192): OSM_PATH_AUTO takes the
- * grouped GEMMs from 128 tokens on (group 32/64/128, hidden and intermediate
+ * grouped GEMMs from 32 tokens on (group 32/64/128, hidden and intermediate
  * multiples of 128, 16-byte aligned input),
  * OSM_PATH_PER_TOKEN always runs the per-token kernels, OSM_PATH_GROUPED
  * always buckets (token, slot) pairs by expert and reads each expert once. */

@@ -166,10 +166,12 @@ int osmd_moe_select(const osmd_moe_args* a, osmd_stream s);
  * is fp32 [T, D], or bf16 [T, D] when x_bf16 (bf16 router, no RMSNorm form).
  * Workspace sizes for T tokens, P = T * (k + shared) pairs:
  *   x_terms  bf16 [T][3][D]    x_sums   f32 [T][D/G]
- *   perm, pair_pos u32 [P]     pair_w   f32 [P]
- *   tiles    16 B [osmd_moe_grouped_max_tiles()]   tile_count u32 [1]
- *   h        f32 [P][I]        h_terms  bf16 [P][2][I]   h_sums f32 [P][I/G]
- *   partial  f32 [P][D]
+ *   pair_pos u32 [P]           pair_w   f32 [P]
+ *   tiles    80 B [osmd_moe_grouped_max_tiles()]   tile_count u32 [1]
+ *   gu_part  f32 [splits(D)][2][P][I]
+ *   h_terms  bf16 [P][2][I]    h_sums   f32 [P][I/G]
+ *   partial  f32 [splits(I)][P][D]
+ * where splits(n) = osmd_moe_grouped_splits(n) K ranges of n columns.
  * plus the decode workspace of moe (logits, ids, weights, mass, shared_gate,
  * x_norm). */
 typedef struct osmd_moe_grouped_args {
@@ -177,17 +179,17 @@ typedef struct osmd_moe_grouped_args {
   uint32_t x_bf16;
   uint16_t* x_terms;
   float* x_sums;
-  uint32_t* perm;
   uint32_t* pair_pos;
   float* pair_w;
   void* tiles;
   uint32_t* tile_count;
-  float* h;
+  float* gu_part;
   uint16_t* h_terms;
   float* h_sums;
   float* partial;
 } osmd_moe_grouped_args;
 size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t experts);
+uint32_t osmd_moe_grouped_splits(uint32_t cols);
 int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s);
 
 /* Bytes of LDS the down kernel stages for `nslot` slots of width `inter`

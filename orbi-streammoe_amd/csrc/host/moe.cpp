@@ -38,7 +38,7 @@ struct HipMoeLayer::Impl {
   // grouped (multi-token) path: allocated on its first use
   HipMoePath path = HipMoePath::automatic;
   bool grouped_ready = false;
-  DeviceBytes g_x_terms, g_x_sums, g_perm, g_pair_pos, g_pair_w, g_tiles, g_tile_count, g_h, g_h_terms,
+  DeviceBytes g_x_terms, g_x_sums, g_pair_pos, g_pair_w, g_tiles, g_tile_count, g_gu_part, g_h_terms,
       g_h_sums, g_partial;
 
   int ensure_grouped(osmd_stream st) {
@@ -49,15 +49,14 @@ struct HipMoeLayer::Impl {
     const std::size_t tiles = osmd_moe_grouped_max_tiles(max_tokens, nslot(), cfg.expert_count);
     int rc = g_x_terms.allocate(T * 3U * D * 2U);
     if (rc == 0) rc = g_x_sums.allocate(T * (D / G) * 4U);
-    if (rc == 0) rc = g_perm.allocate(P * 4U);
     if (rc == 0) rc = g_pair_pos.allocate(P * 4U);
     if (rc == 0) rc = g_pair_w.allocate(P * 4U);
-    if (rc == 0) rc = g_tiles.allocate(tiles * 16U);
+    if (rc == 0) rc = g_tiles.allocate(tiles * 80U);
     if (rc == 0) rc = g_tile_count.allocate(4U);
-    if (rc == 0) rc = g_h.allocate(P * I * 4U);
+    if (rc == 0) rc = g_gu_part.allocate(osmd_moe_grouped_splits(static_cast<std::uint32_t>(D)) * 2U * P * I * 4U);
     if (rc == 0) rc = g_h_terms.allocate(P * 2U * I * 2U);
     if (rc == 0) rc = g_h_sums.allocate(P * (I / G) * 4U);
-    if (rc == 0) rc = g_partial.allocate(P * D * 4U);
+    if (rc == 0) rc = g_partial.allocate(osmd_moe_grouped_splits(static_cast<std::uint32_t>(I)) * P * D * 4U);
     if (rc == 0) rc = osmd_zero(g_tile_count.get(), 4U, st);
     if (rc == 0) grouped_ready = true;
     return rc;
@@ -81,12 +80,11 @@ struct HipMoeLayer::Impl {
     ga.x_bf16 = x_bf16 ? 1U : 0U;
     ga.x_terms = g_x_terms.as<std::uint16_t>();
     ga.x_sums = g_x_sums.as<float>();
-    ga.perm = g_perm.as<std::uint32_t>();
     ga.pair_pos = g_pair_pos.as<std::uint32_t>();
     ga.pair_w = g_pair_w.as<float>();
     ga.tiles = g_tiles.get();
     ga.tile_count = g_tile_count.as<std::uint32_t>();
-    ga.h = g_h.as<float>();
+    ga.gu_part = g_gu_part.as<float>();
     ga.h_terms = g_h_terms.as<std::uint16_t>();
     ga.h_sums = g_h_sums.as<float>();
     ga.partial = g_partial.as<float>();

@@ -614,10 +614,11 @@ struct HipMoeResult {
 // reads its picks' weights), or grouped GEMMs (tokens bucketed by expert,
 // each expert's weights read once for all its tokens). automatic takes the
 // grouped path from kGroupedMinTokens tokens on, where it was measured to
-// overtake the per-token kernels at the Qwen3-Next shape on MI355X
-// (64 tokens: 394 vs 497 us per layer; 128: 697 vs 637; 512: 2714 vs 791).
+// overtake the per-token kernels at the Qwen3-Next shape on MI355X (us per
+// layer, per-token vs grouped: 24 tokens 156 vs 162; 32: 198 vs 189;
+// 64: 369 vs 280; 512: 2730 vs 477).
 enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2 };
-inline constexpr std::uint32_t kGroupedMinTokens = 128;
+inline constexpr std::uint32_t kGroupedMinTokens = 32;
 
 class HipMoeLayer {
  public:
