@@ -232,15 +232,34 @@ int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache 
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,
                                 uint32_t tokens, int sublayer);
-/* How decodes of several tokens run (no counterpart in the reference, which
- * pushes tokens through the sublayer one at a time,
- * src/session/greedy_token_session.cpp:170-192): OSM_PATH_AUTO takes the
- * grouped GEMMs from 32 tokens on (group 32/64/128, hidden and intermediate
- * multiples of 128, 16-byte aligned input),
- * OSM_PATH_PER_TOKEN always runs the per-token kernels, OSM_PATH_GROUPED
- * always buckets (token, slot) pairs by expert and reads each expert once. */
-enum osm_moe_path { OSM_PATH_AUTO = 0, OSM_PATH_PER_TOKEN = 1, OSM_PATH_GROUPED = 2 };
+/* How decodes run (no counterpart in the reference, which pushes tokens
+ * through the sublayer one at a time with 56 dispatches each,
+ * src/session/greedy_token_session.cpp:170-192, routed_moe.cpp:254-430):
+ * OSM_PATH_AUTO runs one token as a single launch where the shape allows it
+ * (hidden <= 2048, intermediate in (64, 512], <= 512 experts, top_k + shared
+ * <= 12, f32 or bf16 router) and takes the grouped GEMMs from 32 tokens on
+ * (group 32/64/128, hidden and intermediate multiples of 128, 16-byte
+ * aligned input); OSM_PATH_PER_TOKEN always runs the three per-token
+ * kernels; OSM_PATH_GROUPED always buckets (token, slot) pairs by expert and
+ * reads each expert once; OSM_PATH_SINGLE_LAUNCH runs one-token decodes as
+ * one launch (more tokens: the per-token kernels). The single launch and the
+ * per-token kernels give the same bits. */
+enum osm_moe_path { OSM_PATH_AUTO = 0, OSM_PATH_PER_TOKEN = 1, OSM_PATH_GROUPED = 2, OSM_PATH_SINGLE_LAUNCH = 3 };
 int osm_moe_layer_set_path(osm_moe_layer l, int path);
+/* The single launch's workgroups wait on each other with bounded spins; a
+ * wait that ran out sets a sticky flag, read here (0 = every launch of this
+ * layer completed its handshakes). Synchronises the context's stream. */
+int osm_moe_layer_wait_failures(osm_context ctx, osm_moe_layer l, uint32_t* out);
+/* Tracing (the reference times phases with steady_clock around each step,
+ * greedy_token_session.cpp:171-183; this is the device-side counterpart for
+ * the single launch): one single-launch decode of one token (MoE form) that
+ * also stamps each workgroup's timeline into trace_dev (device, [grid][8]
+ * u64: steady-clock ticks at its phase boundaries, slot 7 its compute unit's
+ * hardware id). shape[4] gets the router, gate/up and down workgroup counts
+ * and the grid (blocks: router, gate/up, down). */
+int osm_moe_layer_trace_single_launch(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                                      uint32_t slab_layer, const float* x_dev, float* y_dev,
+                                      uint64_t* trace_dev, uint32_t* shape);
 /* A prefill chunk: bf16 x [tokens, D] (device, 16-byte aligned) through the
  * grouped path, MoE form, y fp32 [tokens, D]; needs a bf16 router. Routing
  * per token is that of run_qwen_sparse_moe_vulkan_accum on the widened x. */

@@ -77,27 +77,37 @@ struct DownParams {
   float* y;                  // [B, D]
 };
 
+// Top-k selection on one 256-thread workgroup. Thread i owns experts
+// [i*PER, i*PER+PER). Probabilities are the reference's: exp(logit - max) /
+// sum over all experts (reference_ops.cpp:130-160); the max and the sum
+// combine the four wavefronts' reductions in a fixed order. The order is the
+// reference's too: probability descending, lower expert id first among
+// equals (reference_ops.cpp:170-196: strict > on insertion, stable sort by
+// probability). A probability is >= 0, so its bits order like its value; the
+// key is (bits + 1, ~id), unique per expert, and 0 for experts past E and
+// popped entries (below every real expert, even one whose probability is
+// +0). Each wavefront takes the top-k of its 64 * PER experts in k rounds
+// (the largest lane head over the wavefront, the lowest lane holding it:
+// lanes own ascending id ranges, so that is the lowest id). The 4k
+// candidates are then ranked in one pass: as (key << 32) | ~id they are
+// unique and order exactly as probability descending, id ascending, so a
+// candidate's place is the number of candidates above it. With a table,
+// each thread parks its experts' blob pointers in LDS, so a pick's blob
+// costs no dependent global load.
+constexpr uint32_t kSelThreads = 256;
+constexpr uint32_t kSelWaves = kSelThreads / kWave;
+
 // Result of one token's selection, in LDS: ids and probabilities in pick
-// order, and the blob of every expert the selecting wavefront looked up.
+// order, the blob of every expert, and the workgroup's reduction scratch.
 template <int PER>
 struct Selection {
   uint32_t id[OSMD_MAX_TOP_K];
   float p[OSMD_MAX_TOP_K];
-  const uint8_t* blob[kWave * PER];
+  const uint8_t* blob[kSelThreads * PER];
+  float red[2][kSelWaves];
+  uint64_t cand[kSelWaves * OSMD_MAX_TOP_K];  // (key << 32) | ~id, wavefront-major
 };
 
-// ---------------------------------------------------------------------------
-// Top-k selection on one wavefront. Lane l owns experts [l*PER, l*PER+PER).
-// Probabilities are the reference's: exp(logit - max) / sum over all experts
-// (reference_ops.cpp:130-160). The order is the reference's too: probability
-// descending, lower expert id first among equals (reference_ops.cpp:170-196:
-// strict > on insertion, stable sort by probability). A probability is >= 0,
-// so its bits order like its value; each lane sorts its experts on the key
-// (bits, ~id), which is unique, and each round takes the largest head bits
-// over the wave and the lowest lane holding them -- lanes own ascending id
-// ranges, so that is the lowest id. With a table, the lane's blob pointers
-// are loaded together with its logits and parked in LDS, so the pick's blob
-// costs no dependent global load.
 __device__ __forceinline__ void sort_step(uint32_t* k, uint32_t* n, int a, int b) {
   // Descending on (k, n): swap when (k[b], n[b]) > (k[a], n[a]).
   const uint64_t ka = (static_cast<uint64_t>(k[a]) << 32) | n[a];
@@ -112,38 +122,25 @@ __device__ __forceinline__ void sort_step(uint32_t* k, uint32_t* n, int a, int b
 
 template <int PER>
 __device__ __forceinline__ void sort_lane(uint32_t* k, uint32_t* n) {
-  if constexpr (PER == 8) {
-    // Batcher's odd-even merge network: 19 comparators.
-    constexpr int net[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6},
-                                {5, 7}, {1, 2}, {5, 6}, {0, 4}, {1, 5}, {2, 6}, {3, 7},
-                                {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+  // Odd-even transposition (PER is 2 or 4).
 #pragma unroll
-    for (int c = 0; c < 19; ++c) sort_step(k, n, net[c][0], net[c][1]);
-  } else {
-    // Odd-even transposition for the other widths.
+  for (int round = 0; round < PER; ++round) {
 #pragma unroll
-    for (int round = 0; round < PER; ++round) {
-#pragma unroll
-      for (int j = round & 1; j + 1 < PER; j += 2) sort_step(k, n, j, j + 1);
-    }
+    for (int j = round & 1; j + 1 < PER; j += 2) sort_step(k, n, j, j + 1);
   }
 }
 
+// Selection from this thread's logits p[j] of experts tid*PER + j (entries
+// past E are ignored) and their table pointers. Every thread of the
+// workgroup calls it; it ends with a barrier, after which out is complete.
 template <int PER>
-__device__ __forceinline__ void select_wave(const RouteView& rv, uint32_t t, uint32_t lane,
-                                            Selection<PER>& out) {
+__device__ __forceinline__ void select_values(const RouteView& rv, float (&p)[PER],
+                                              const uint8_t* const (&tab)[PER], Selection<PER>& out,
+                                              uint64_t* mark = nullptr) {
   const uint32_t E = rv.expert_count;
   const uint32_t k = rv.top_k;
-  const float* lg = rv.logits + static_cast<size_t>(t) * E;
-  const uint32_t base = lane * PER;
-  float p[PER];
-  const uint8_t* tab[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const uint32_t e = (base + j < E) ? base + j : E - 1u;  // clamped: every load in bounds
-    p[j] = lg[e];
-    tab[j] = rv.expert_table ? rv.expert_table[e] : nullptr;
-  }
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const uint32_t base = tid * PER;
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -151,6 +148,9 @@ __device__ __forceinline__ void select_wave(const RouteView& rv, uint32_t t, uin
     mx = fmaxf(mx, p[j]);
   }
   mx = wave_max(mx);
+  if (lane == 0) out.red[0][wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -158,8 +158,10 @@ __device__ __forceinline__ void select_wave(const RouteView& rv, uint32_t t, uin
     sum += p[j];
   }
   sum = wave_sum(sum);
-  // key: probability bits + 1, so 0 (experts past E, popped heads) ranks
-  // below every real expert, even one whose probability is +0.
+  if (lane == 0) out.red[1][wave] = sum;
+  __syncthreads();
+  sum = ((out.red[1][0] + out.red[1][1]) + out.red[1][2]) + out.red[1][3];
+  if (mark != nullptr && threadIdx.x == 0) mark[5] = static_cast<uint64_t>(wall_clock64());
   uint32_t key[PER], nid[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -169,33 +171,68 @@ __device__ __forceinline__ void select_wave(const RouteView& rv, uint32_t t, uin
   }
   sort_lane<PER>(key, nid);
 
-  // Unrolled: a rolled loop re-packs the loop-carried arrays every round.
-#pragma unroll
-  for (uint32_t r = 0; r < OSMD_MAX_TOP_K; ++r) {
-    if (r < k) {
+  // This wavefront's top-k. Each round is branch-free (the pop is a select
+  // on every lane) and lane r keeps round r's result, written out after the
+  // last round. The loop stays rolled: one body, fetched once, instead of
+  // k copies that each start with instruction-cache misses (the selection
+  // runs on one workgroup, so its code is cold).
+  uint32_t rk = 0u, ri = 0u;
+#pragma unroll 1
+  for (uint32_t r = 0; r < k; ++r) {
+    {
       const uint32_t m = wave_max_u32(key[0]);
-      const unsigned long long ballot = __ballot(key[0] == m);
-      const int wl = __ffsll(ballot) - 1;  // never empty: m is some lane's key
-      uint32_t sid = ~static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(nid[0]), wl));
-      sid = sid < E ? sid : E - 1u;  // a blob lookup always stays in the table
-      if (lane == 0) {
-        out.id[r] = sid;
-        out.p[r] = __uint_as_float(m - 1u);
-      }
-      if (static_cast<int>(lane) == wl) {  // pop the head
+      const int wl = __ffsll(__ballot(key[0] == m)) - 1;  // never empty: m is some lane's key
+      const uint32_t sid = ~static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(nid[0]), wl));
+      rk = lane == r ? m : rk;
+      ri = lane == r ? sid : ri;
+      const bool won = static_cast<int>(lane) == wl;  // pop the head
 #pragma unroll
-        for (int j = 0; j + 1 < PER; ++j) {
-          key[j] = key[j + 1];
-          nid[j] = nid[j + 1];
-        }
-        key[PER - 1] = 0u;
-        nid[PER - 1] = 0u;
+      for (int j = 0; j + 1 < PER; ++j) {
+        key[j] = won ? key[j + 1] : key[j];
+        nid[j] = won ? nid[j + 1] : nid[j];
       }
+      key[PER - 1] = won ? 0u : key[PER - 1];
+      nid[PER - 1] = won ? 0u : nid[PER - 1];
     }
   }
-  // LDS writes of one wavefront are visible to its later LDS reads.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
+  if (lane < k) out.cand[wave * k + lane] = (static_cast<uint64_t>(rk) << 32) | ~ri;
+  __syncthreads();
+  if (mark != nullptr && threadIdx.x == 0) mark[6] = static_cast<uint64_t>(wall_clock64());
+
+  // Wavefront 0: each lane ranks one candidate against all of them (LDS
+  // broadcast reads); the k best write their place. Candidates of key 0
+  // (fewer than k experts in a wavefront) always have k real ones above.
+  if (wave == 0) {
+    const uint32_t nc = kSelWaves * k;
+    const uint64_t mine = lane < nc ? out.cand[lane] : 0u;
+    uint32_t rank = 0;
+#pragma unroll 4
+    for (uint32_t c = 0; c < nc; ++c) rank += out.cand[c] > mine ? 1u : 0u;
+    if (lane < nc && rank < k) {
+      const uint32_t id = ~static_cast<uint32_t>(mine);
+      out.id[rank] = id < E ? id : E - 1u;  // a blob lookup always stays in the table
+      out.p[rank] = __uint_as_float(static_cast<uint32_t>(mine >> 32) - 1u);
+    }
+  }
+  __syncthreads();
+}
+
+// Loads token t's logits (and table pointers) and selects; every thread of
+// the workgroup calls it.
+template <int PER>
+__device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out) {
+  const uint32_t E = rv.expert_count;
+  const float* lg = rv.logits + static_cast<size_t>(t) * E;
+  const uint32_t base = threadIdx.x * PER;
+  float p[PER];
+  const uint8_t* tab[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t e = (base + j < E) ? base + j : E - 1u;  // clamped: every load in bounds
+    p[j] = lg[e];
+    tab[j] = rv.expert_table ? rv.expert_table[e] : nullptr;
+  }
+  select_values<PER>(rv, p, tab, out);
 }
 
 template <int PER>
@@ -208,12 +245,13 @@ __device__ __forceinline__ const uint8_t* pick_blob(const RouteView& rv, const S
 // Writes the selection of token t: ids and weights in pick order, the
 // selected mass summed in pick order and the optional renormalisation
 // (qwen_router.cpp:72-91), and each slot's blob (shared expert last).
+// Threads tid <= k of the workgroup take part.
 template <int PER>
-__device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t t, uint32_t lane,
+__device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t t, uint32_t tid,
                                                   const Selection<PER>& s) {
   const uint32_t k = rv.top_k;
   const uint32_t nslot = k + rv.has_shared;
-  if (lane == 0) {
+  if (tid == 0) {
     float mass = 0.0f;
     for (uint32_t r = 0; r < k; ++r) mass = mass + s.p[r];
     for (uint32_t r = 0; r < k; ++r) {
@@ -222,73 +260,64 @@ __device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t 
     }
     rv.mass[t] = mass;
   }
-  if (lane < k)
-    rv.slot_ptrs[static_cast<size_t>(t) * nslot + lane] = pick_blob(rv, s, lane);
-  else if (lane == k && nslot > k)
+  if (tid < k)
+    rv.slot_ptrs[static_cast<size_t>(t) * nslot + tid] = pick_blob(rv, s, tid);
+  else if (tid == k && nslot > k)
     rv.slot_ptrs[static_cast<size_t>(t) * nslot + k] = rv.shared_expert;
 }
 
 template <int PER>
-__global__ __launch_bounds__(64) void select_kernel(RouteView rv) {
+__global__ __launch_bounds__(kSelThreads) void select_kernel(RouteView rv) {
   __shared__ Selection<PER> sel;
-  select_wave<PER>(rv, blockIdx.x, threadIdx.x, sel);
+  select_block<PER>(rv, blockIdx.x, sel);
   publish_selection(rv, blockIdx.x, threadIdx.x, sel);
 }
 
 // ---------------------------------------------------------------------------
-// Router GEMV.
+// Router GEMV. A wavefront owns one router row; lane l reads elements
+// l*8 + 512u .. +8 (u = 0, 1, ...), kept as loaded until the FMA.
 constexpr int kRouteWaves = 4;
 
 template <int RD>
-__device__ __forceinline__ void load8_row(const uint8_t* row, uint32_t c, float* w) {
+struct Raw8 {  // 8 router elements as loaded
+  uint4 v[RD == OSM_META_F32 ? 2 : 1];
+};
+
+template <int RD>
+__device__ __forceinline__ void load_raw8(const uint8_t* row, uint32_t c, Raw8<RD>& r) {
   if constexpr (RD == OSM_META_F32) {
-    const float4* p = reinterpret_cast<const float4*>(row) + c / 4u;
-    const float4 a = p[0], b = p[1];
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    r.v[0] = ldg16(row + static_cast<size_t>(c) * 4u);
+    r.v[1] = ldg16(row + static_cast<size_t>(c) * 4u + 16u);
   } else {
-    const uint4 q = ldg16(row + static_cast<size_t>(c) * 2u);
-    const uint32_t v[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (RD == OSM_META_BF16) {
-        w[2 * i] = bf16_to_f32(v[i] & 0xFFFFu);
-        w[2 * i + 1] = bf16_to_f32(v[i] >> 16);
-      } else {
-        w[2 * i] = f16_to_f32(v[i] & 0xFFFFu);
-        w[2 * i + 1] = f16_to_f32(v[i] >> 16);
-      }
-    }
+    r.v[0] = ldg16(row + static_cast<size_t>(c) * 2u);
   }
 }
 
 template <int RD>
-__global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
-  extern __shared__ __align__(16) float xs[];  // [D] normalised input of this token
-  __shared__ float red[kRouteWaves];
-  const uint32_t t = blockIdx.y;
-  const uint32_t D = a.geom.hidden;
-  const uint32_t E = a.expert_count;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid % kWave;
-  const uint32_t wave = tid / kWave;
-  const uint32_t nrows = E + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  const uint32_t row = blockIdx.x * kRouteWaves + wave;
-  constexpr size_t esz = (RD == OSM_META_F32) ? 4u : 2u;
-  const uint8_t* wrow = row < E ? static_cast<const uint8_t*>(a.router) + static_cast<size_t>(row) * D * esz
-                                : static_cast<const uint8_t*>(a.shared_gate_vec);
-
-  // This wavefront's router row (hidden <= 8192 -> <= 16 loads per lane) and
-  // all of x, issued together before anything waits.
-  constexpr int kRowLoads = 16;
-  float w[kRowLoads][8];
-  if (row < nrows) {
-#pragma unroll
-    for (int u = 0; u < kRowLoads; ++u) {
-      const uint32_t c = lane * 8u + u * 8u * kWave;
-      if (c < D) load8_row<RD>(wrow, c, w[u]);
-    }
+__device__ __forceinline__ float raw8_get(const Raw8<RD>& r, int j) {
+  if constexpr (RD == OSM_META_F32) {
+    const uint4& q = r.v[j / 4];
+    const uint32_t w = (j % 4 == 0) ? q.x : (j % 4 == 1) ? q.y : (j % 4 == 2) ? q.z : q.w;
+    return __uint_as_float(w);
+  } else {
+    const uint4& q = r.v[0];
+    const uint32_t w = (j / 2 == 0) ? q.x : (j / 2 == 1) ? q.y : (j / 2 == 2) ? q.z : q.w;
+    const uint32_t bits = (j % 2 == 0) ? (w & 0xFFFFu) : (w >> 16);
+    if constexpr (RD == OSM_META_BF16)
+      return bf16_to_f32(bits);
+    else
+      return f16_to_f32(bits);
   }
+}
+
+// Token t's input, RMS-normalised when the flags ask for it
+// (reference_ops.cpp:96-128), into xs[D] in LDS; write_norm also stores it to
+// x_norm. Every workgroup that needs x normalises its own copy: the values
+// are the same bits everywhere. 256 threads, hidden <= 8192.
+__device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, float* xs, bool write_norm) {
+  __shared__ float red[kRouteWaves];
+  const uint32_t D = a.geom.hidden;
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const float4* x4 = reinterpret_cast<const float4*>(a.x + static_cast<size_t>(t) * D);
   const uint32_t n4 = D / 4u;
   constexpr int kX4PerThread = 8;
@@ -299,8 +328,6 @@ __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
     xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (a.flags & OSMD_MOE_RMSNORM) {
-    // RMSNorm of the residual input (reference_ops.cpp:96-128), fused here so
-    // every workgroup normalises its own copy instead of a separate launch.
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kX4PerThread; ++u)
@@ -332,30 +359,60 @@ __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
     const uint32_t i = tid + u * 256u;
     if (i < n4) {
       xs4[i] = xv[u];
-      if (blockIdx.x == 0) xn4[i] = xv[u];
+      if (write_norm) xn4[i] = xv[u];
     }
   }
   __syncthreads();
+}
 
-  // One router row per wavefront; row E is the shared-expert gate vector.
+// Router rows blk*4 .. blk*4+3 of token t (row E is the shared-expert gate
+// vector): logits, or the sigmoid shared gate (reference_ops.cpp:214-216).
+// RCH loads of 8 elements per lane cover hidden <= 512 * RCH.
+// also(row, value) runs on lane 0 after each row's store (row E: the gate).
+template <int RD, int RCH, typename Also>
+__device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, uint32_t blk, float* xs,
+                                            Also&& also) {
+  const uint32_t D = a.geom.hidden;
+  const uint32_t E = a.expert_count;
+  const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const uint32_t nrows = E + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
+  const uint32_t row = blk * kRouteWaves + wave;
+  constexpr size_t esz = (RD == OSM_META_F32) ? 4u : 2u;
+  const uint8_t* wrow = row < E ? static_cast<const uint8_t*>(a.router) + static_cast<size_t>(row) * D * esz
+                                : static_cast<const uint8_t*>(a.shared_gate_vec);
+  // The row is issued before x, so both are in flight together.
+  Raw8<RD> w[RCH];
+  if (row < nrows) {
+#pragma unroll
+    for (int u = 0; u < RCH; ++u) {
+      const uint32_t c = lane * 8u + u * 8u * kWave;
+      if (c < D) load_raw8<RD>(wrow, c, w[u]);
+    }
+  }
+  stage_x(a, t, xs, blk == 0);
   if (row < nrows) {
     float acc = 0.0f;
 #pragma unroll
-    for (int u = 0; u < kRowLoads; ++u) {
+    for (int u = 0; u < RCH; ++u) {
       const uint32_t c = lane * 8u + u * 8u * kWave;
       if (c < D) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf(w[u][j], xs[c + j], acc);
+        for (int j = 0; j < 8; ++j) acc = fmaf(raw8_get<RD>(w[u], j), xs[c + j], acc);
       }
     }
     acc = wave_sum(acc);
     if (lane == 0) {
-      if (row < E)
-        a.logits[static_cast<size_t>(t) * E + row] = acc;
-      else
-        a.shared_gate[t] = 1.0f / (1.0f + expf(-acc));  // reference_ops.cpp:214-216
+      const float v = row < E ? acc : 1.0f / (1.0f + expf(-acc));
+      *(row < E ? a.logits + static_cast<size_t>(t) * E + row : a.shared_gate + t) = v;
+      also(row, v);
     }
   }
+}
+
+template <int RD>
+__global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
+  extern __shared__ __align__(16) float xs[];  // [D] normalised input of this token
+  route_block<RD, 16>(a, blockIdx.y, blockIdx.x, xs, [](uint32_t, float) {});
 }
 
 // ---------------------------------------------------------------------------
@@ -365,23 +422,13 @@ __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
 // sum) stays in registers for all rows. PER > 0: routed slots select their
 // expert from the logits first (PER = experts per lane of the selection).
 constexpr int kGuWaves = 4;
-constexpr int kGuRowsPerWave = 4;
+constexpr int kGuRowsPerWave = 8;
 
-template <int META, int CPL, int PER>
-__global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
-  const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
-  const uint32_t t = blockIdx.z;
-  const uint32_t j = blockIdx.y;
-  const uint32_t D = p.g.hidden, I = p.g.inter, G = p.g.group;
-  const uint32_t nch = D / 32u;  // 16-byte chunks per row
-  const uint32_t gpr = D / G;    // groups per row
-  const float* x = p.x + static_cast<size_t>(t) * D;
-
-  // Lanes past the row end (hidden < 64*32*CPL) read chunk nch-1 again and
-  // zero their x slice, so every load is unconditional and in bounds.
-  float xr[CPL][32];
-  float xsum[CPL];
+// Lane's slices of x (chunks lane, lane+64, ... of 32 floats). Lanes past the
+// row end (hidden < 64*32*CPL) read chunk nch-1 again and zero their slice,
+// so every load is unconditional and in bounds. x may be global or LDS.
+template <int CPL>
+__device__ __forceinline__ void load_xr(const float* x, uint32_t nch, uint32_t lane, float (&xr)[CPL][32]) {
 #pragma unroll
   for (int ci = 0; ci < CPL; ++ci) {
     const uint32_t c = lane + kWave * ci;
@@ -397,31 +444,21 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
       xr[ci][4 * v + 3] = valid ? f.w : 0.0f;
     }
   }
+}
 
-  const uint8_t* blob;
-  if constexpr (PER > 0) {
-    // Routed slot: wavefront 0 selects while the others wait with their x
-    // slice loaded; block (0, 0) also publishes the selection.
-    const RouteView& rv = p.rv;
-    __shared__ Selection<PER> sel;
-    __shared__ const uint8_t* s_blob;
-    if (j < rv.top_k) {
-      if (wave == 0) {
-        select_wave<PER>(rv, t, lane, sel);
-        if (blockIdx.x == 0 && j == 0) publish_selection(rv, t, lane, sel);
-        if (lane == 0) s_blob = pick_blob(rv, sel, j);
-      }
-      __syncthreads();
-      blob = s_blob;
-    } else {
-      blob = rv.shared_expert;
-    }
-  } else {
-    blob = p.src.blob(t, j);
-  }
-  if (blob == nullptr) blob = p.rv.fallback;  // never dereference a null slot
+// Gate and up rows blk*16 .. blk*16+15 of slot j of token t from `blob`,
+// SwiGLU'd into h[t, j, row].
+// store(index, value): h[t, j, row] at index (t * nslot + j) * I + row.
+template <int META, int CPL, typename Store>
+__device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, uint32_t j, uint32_t blk,
+                                             const uint8_t* blob, const float (&xr)[CPL][32], Store&& store) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t D = p.g.hidden, I = p.g.inter, G = p.g.group;
+  const uint32_t nch = D / 32u;  // 16-byte chunks per row
+  const uint32_t gpr = D / G;    // groups per row
   const osm_expert_offsets off = osm_expert_layout(p.g);
-
+  float xsum[CPL];
 #pragma unroll
   for (int ci = 0; ci < CPL; ++ci) {
     xsum[ci] = 0.0f;
@@ -429,7 +466,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
     for (int v = 0; v < 32; ++v) xsum[ci] += xr[ci][v];
   }
 
-  const uint32_t r0 = (blockIdx.x * kGuWaves + wave) * kGuRowsPerWave;
+  const uint32_t r0 = (blk * kGuWaves + wave) * kGuRowsPerWave;
   uint4 qg[kGuRowsPerWave][CPL], qu[kGuRowsPerWave][CPL];
   uint32_t sg[kGuRowsPerWave][CPL], bg[kGuRowsPerWave][CPL];
   uint32_t su[kGuRowsPerWave][CPL], bu[kGuRowsPerWave][CPL];
@@ -463,9 +500,38 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
     ga = wave_sum(ga);
     ua = wave_sum(ua);
     const uint32_t r = r0 + i;
-    if (lane == 0 && r < I)
-      p.h[(static_cast<size_t>(t) * p.src.nslot + j) * I + r] = silu_mul(ga, ua);
+    if (lane == 0 && r < I) store((static_cast<size_t>(t) * p.src.nslot + j) * I + r, silu_mul(ga, ua));
   }
+}
+
+template <int META, int CPL, int PER>
+__global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t wave = threadIdx.x / kWave;
+  const uint32_t t = blockIdx.z;
+  const uint32_t j = blockIdx.y;
+  const uint32_t D = p.g.hidden;
+  float xr[CPL][32];
+  load_xr<CPL>(p.x + static_cast<size_t>(t) * D, D / 32u, lane, xr);
+
+  const uint8_t* blob;
+  if constexpr (PER > 0) {
+    // Routed slot: the workgroup selects with its x slices loaded; block
+    // (0, 0) also publishes the selection.
+    const RouteView& rv = p.rv;
+    __shared__ Selection<PER> sel;
+    if (j < rv.top_k) {
+      select_block<PER>(rv, t, sel);
+      if (blockIdx.x == 0 && j == 0) publish_selection(rv, t, threadIdx.x, sel);
+      blob = pick_blob(rv, sel, j);
+    } else {
+      blob = rv.shared_expert;
+    }
+  } else {
+    blob = p.src.blob(t, j);
+  }
+  if (blob == nullptr) blob = p.rv.fallback;  // never dereference a null slot
+  gate_up_rows<META, CPL>(p, t, j, blockIdx.x, blob, xr, [&](size_t i, float v) { p.h[i] = v; });
 }
 
 // ---------------------------------------------------------------------------
@@ -492,13 +558,167 @@ size_t down_lds_bytes(uint32_t inter, uint32_t nslot, uint32_t rows_per_block) {
   return (chunks * (kChunkStride + 1u) + 2u * rows_per_block) * sizeof(float);
 }
 
-template <int META, int LPR, int MAXS>
-__global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
-  extern __shared__ __align__(16) float hs[];  // chunks, then chunk sums, then [2][rows] halves
+// ---------------------------------------------------------------------------
+// Single-launch decode: how its workgroups hand data to each other.
+//
+// A one-token decode with every expert resident runs as one grid: router
+// workgroups (4 router rows each), one selector, gate/up workgroups (the
+// shared expert's first), down workgroups. A workgroup waits only on
+// workgroups with lower indices, which the dispatcher starts first.
+//
+// Everything handed from one workgroup to another -- the logits and shared
+// gate, the selection, h -- travels as 8-byte elements that carry the launch
+// number next to the value, each written with one agent-scope atomic store
+// and read with agent-scope atomic loads (coherent across the XCDs' separate
+// L2 caches; no L2 write-back or invalidate is involved). A reader re-reads
+// an element until its tag is this launch's number: the read is the wait.
+// The selector writes one record per slot (tag, expert id, weight), in eight
+// copies, so the readers on the XCD that workgroup b runs on (b % 8) share
+// one copy. h is 22 KB that every down workgroup reads, too much to re-read
+// while waiting: each gate/up workgroup, once its h stores are complete
+// (s_waitcnt vmcnt(0) in every wavefront, then a barrier), adds 1 to its
+// slot's done counter, and down workgroups poll the slot counters (one lane
+// each) before reading h, whose tags they still check. h rotates through
+// four buffers (launch number mod 4) and is first read with ordinary loads,
+// served by the reader's L2 after one miss per XCD: each 128-byte line of it
+// is written whole by one workgroup with write-through stores, so a miss
+// fetches it complete, and a line some L2 still holds from four launches
+// back carries an old tag and is read again with coherent loads.
+//
+// Launch numbers come from a per-workgroup counter, read and advanced once
+// per launch, so nothing is reset between launches. Every wait gives up after
+// kSpinLimit re-reads and sets the sticky error word; the workgroup then
+// goes on with what it read.
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kRecordCopies = 8;
+constexpr uint32_t kRecordSlots = 16;
+constexpr uint32_t kSharedId = 0xFFFFu;  // record id of the shared expert
+constexpr uint32_t kHBuffers = 4;        // h buffers, by launch number mod 4
+
+__device__ __forceinline__ void store_tagged(uint64_t* p, uint32_t epoch, float v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_tagged(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_current(uint64_t v, uint32_t epoch) {
+  return static_cast<uint32_t>(v >> 32) == epoch;
+}
+__device__ __forceinline__ float tagged_value(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
+// Selection record: tag (low 16 bits of the launch number), expert id, weight.
+__device__ __forceinline__ uint64_t record_of(uint32_t epoch, uint32_t id, float w) {
+  return (static_cast<uint64_t>(epoch & 0xFFFFu) << 48) | (static_cast<uint64_t>(id & 0xFFFFu) << 32) |
+         __float_as_uint(w);
+}
+__device__ __forceinline__ bool record_current(uint64_t v, uint32_t epoch) {
+  return static_cast<uint32_t>(v >> 48) == (epoch & 0xFFFFu);
+}
+
+// Byte offsets of the handshake buffer's parts (the error word is at 0).
+struct FusedLayout {
+  size_t launch, logits, record, done, h, bytes;
+};
+__host__ __device__ inline size_t round_up128(size_t n) { return (n + 127u) & ~static_cast<size_t>(127u); }
+__host__ __device__ inline FusedLayout fused_layout(uint32_t grid, uint32_t experts, uint32_t nslot,
+                                                    uint32_t inter) {
+  FusedLayout l;
+  l.launch = 128u;
+  l.logits = l.launch + round_up128(static_cast<size_t>(grid) * 4u);
+  l.record = l.logits + round_up128((static_cast<size_t>(experts) + 1u) * 8u);
+  l.done = l.record + static_cast<size_t>(kRecordCopies) * kRecordSlots * 8u;
+  l.h = l.done + static_cast<size_t>(kRecordSlots) * 128u;  // one counter per slot, 128 bytes apart
+  l.bytes = l.h + kHBuffers * round_up128(static_cast<size_t>(nslot) * inter * 8u);
+  return l;
+}
+
+struct FusedWaits {
+  uint32_t* err;
+  uint32_t epoch;
+  const uint64_t* record;  // this workgroup's copy
+  const uint64_t* h;       // this launch's tagged h [nslot][I]
+  const uint32_t* done;    // per-slot gate/up done counters, 128 bytes apart
+  uint32_t gu_per_slot;    // gate/up workgroups per slot
+  uint64_t* mark;          // this workgroup's timeline slots, or null
+  const RouteView* rv;
+  const uint8_t** s_blob;  // LDS: blob of each slot
+  float* s_w;              // LDS: weight of each slot
+};
+
+// Optional timeline of a single launch: thread 0 stamps the steady clock into
+// slot i of its workgroup's 8 (slot 7: the hardware id of its compute unit).
+__device__ __forceinline__ void stamp(uint64_t* mark, int i) {
+  if (mark != nullptr && threadIdx.x == 0) mark[i] = static_cast<uint64_t>(wall_clock64());
+}
+
+// Whether a wait should stop: out of spins, or another wait already gave up.
+__device__ __forceinline__ bool give_up(uint32_t spin, uint32_t* err) {
+  if (spin >= kSpinLimit ||
+      ((spin & 255u) == 255u && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
+    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+  return false;
+}
+
+// Lanes r < n of the calling wavefront read record slot r until it is this
+// launch's; returns the lane's record.
+__device__ __forceinline__ uint64_t read_record(const FusedWaits& fw, uint32_t n) {
+  const uint32_t lane = threadIdx.x % kWave;
+  uint64_t v = 0;
+  for (uint32_t spin = 0;; ++spin) {
+    bool ok = true;
+    if (lane < n) {
+      v = load_tagged(fw.record + lane);
+      ok = record_current(v, fw.epoch);
+    }
+    if (__all(ok)) break;
+    if (give_up(spin, fw.err)) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return v;
+}
+
+// s_waitcnt immediate with vmcnt = 0 and the other counters not waited on
+// (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+// Lanes c < n of the calling wavefront poll counter c (128 bytes apart from
+// `first`) until it reaches `target`; the others wait with them.
+__device__ __forceinline__ void wait_counters(const uint32_t* first, uint32_t n, uint32_t target, uint32_t* err) {
+  const uint32_t lane = threadIdx.x % kWave;
+  for (uint32_t spin = 0;; ++spin) {
+    bool ok = true;
+    if (lane < n) {
+      const uint32_t v = __hip_atomic_load(const_cast<uint32_t*>(first) + lane * 32u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      ok = static_cast<int32_t>(v - target) >= 0;
+    }
+    if (__all(ok)) break;
+    if (give_up(spin, err)) break;
+    __builtin_amdgcn_s_sleep(4);
+  }
+}
+
+// Blob of a record: the table entry of its expert (the fallback for a null
+// entry or an id out of range), or the shared expert.
+__device__ __forceinline__ const uint8_t* record_blob(const RouteView& rv, uint64_t rec) {
+  const uint32_t id = static_cast<uint32_t>(rec >> 32) & 0xFFFFu;
+  if (id == kSharedId) return rv.shared_expert;
+  const uint8_t* b = id < rv.expert_count ? rv.expert_table[id] : nullptr;
+  return b ? b : rv.fallback;
+}
+
+// down + weighted accumulate for rows blk * rows_per_block ... of token t.
+// FUSED: the slot pointers and weights are read once the selection is out,
+// and h once every gate/up workgroup is done; the down weights are already
+// in flight while h is awaited.
+template <int META, int LPR, int MAXS, bool FUSED>
+__device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint32_t blk, float* hs,
+                                           const FusedWaits& fw) {
   constexpr uint32_t kRowsPerGroup = kWave / LPR;
   constexpr uint32_t kRowsPerBlock = down_rows_per_block<LPR>();
   constexpr int kSlotsPerWave = (MAXS + 1) / 2;
-  const uint32_t t = blockIdx.y;
   const uint32_t D = p.g.hidden, I = p.g.inter, G = p.g.group;
   const uint32_t nslot = p.src.nslot;
   const uint32_t nchd = I / 32u;
@@ -510,7 +730,7 @@ __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   const uint32_t half = wave >> 1;  // slots half, half + 2, ...
   const uint32_t c = lane % LPR;
   const uint32_t row_local = rg * kRowsPerGroup + lane / LPR;
-  const uint32_t row = blockIdx.x * kRowsPerBlock + row_local;
+  const uint32_t row = blk * kRowsPerBlock + row_local;
   const bool active = row < D && c < nchd;
   const uint32_t rr = row < D ? row : D - 1u;
   const uint32_t cc = c < nchd ? c : nchd - 1u;
@@ -518,15 +738,67 @@ __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   float* hsum = hs + static_cast<size_t>(nslot) * nchd * kChunkStride;
   float* halves = hsum + static_cast<size_t>(nslot) * nchd;
 
-  // h does not depend on the slot pointers: its first batch is issued first.
   const float4* h4 = reinterpret_cast<const float4*>(p.h + static_cast<size_t>(t) * nslot * I);
   const uint32_t n4 = nslot * I / 4u;  // a multiple of 8 (I % 32 == 0)
   constexpr int kH4PerThread = 8;
   float4 hv[kH4PerThread];
+  auto load_h = [&](uint32_t pass) {
+    if constexpr (FUSED) {
+      // h comes from the gate/up workgroups of this launch: an ordinary
+      // read first, then coherent re-reads until every element this thread
+      // stages carries the launch number.
+      for (uint32_t spin = 0;; ++spin) {
+        bool ok = true;
 #pragma unroll
-  for (int u = 0; u < kH4PerThread; ++u) {
-    const uint32_t f = u * kDownThreads + tid;
-    hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < kH4PerThread; ++u) {
+          const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
+          if (f < n4) {
+            const uint64_t* src = fw.h + static_cast<size_t>(t) * nslot * I + static_cast<size_t>(f) * 4u;
+            uint64_t v0, v1, v2, v3;
+            if (spin == 0) {
+              const uint4 a = *reinterpret_cast<const uint4*>(src);
+              const uint4 c = *reinterpret_cast<const uint4*>(src + 2);
+              v0 = (static_cast<uint64_t>(a.y) << 32) | a.x;
+              v1 = (static_cast<uint64_t>(a.w) << 32) | a.z;
+              v2 = (static_cast<uint64_t>(c.y) << 32) | c.x;
+              v3 = (static_cast<uint64_t>(c.w) << 32) | c.z;
+            } else {
+              v0 = load_tagged(src);
+              v1 = load_tagged(src + 1);
+              v2 = load_tagged(src + 2);
+              v3 = load_tagged(src + 3);
+            }
+            ok = ok && tag_current(v0, fw.epoch) && tag_current(v1, fw.epoch) && tag_current(v2, fw.epoch) &&
+                 tag_current(v3, fw.epoch);
+            hv[u] = make_float4(tagged_value(v0), tagged_value(v1), tagged_value(v2), tagged_value(v3));
+          } else {
+            hv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+        if (ok || give_up(spin, fw.err)) break;
+        if (spin > 0) __builtin_amdgcn_s_sleep(2);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kH4PerThread; ++u) {
+        const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
+        hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  if constexpr (FUSED) {
+    // Each slot's blob and weight from this launch's selection record.
+    if (wave == 0) {
+      const uint64_t rec = read_record(fw, nslot);
+      if (lane < nslot) {
+        fw.s_blob[lane] = record_blob(*fw.rv, rec);
+        fw.s_w[lane] = __uint_as_float(static_cast<uint32_t>(rec));
+      }
+    }
+    __syncthreads();
+    stamp(fw.mark, 1);
+  } else {
+    load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
   }
 
   // This wavefront's slots: pointers and weights (uniform loads), then the
@@ -538,11 +810,16 @@ __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   for (int i = 0; i < kSlotsPerWave; ++i) {
     const uint32_t j = half + 2u * i;
     const uint32_t js = j < nslot ? j : 0u;
-    bp[i] = p.src.blob(t, js);
-    if (js < p.top_k)
-      w[i] = p.weights ? p.weights[static_cast<size_t>(t) * p.top_k + js] : 1.0f;
-    else
-      w[i] = p.shared_gate ? p.shared_gate[t] : 1.0f;
+    if constexpr (FUSED) {
+      bp[i] = fw.s_blob[js];
+      w[i] = fw.s_w[js];
+    } else {
+      bp[i] = p.src.blob(t, js);
+      if (js < p.top_k)
+        w[i] = p.weights ? p.weights[static_cast<size_t>(t) * p.top_k + js] : 1.0f;
+      else
+        w[i] = p.shared_gate ? p.shared_gate[t] : 1.0f;
+    }
     if (j >= nslot || bp[i] == nullptr) w[i] = 0.0f;
     if (bp[i] == nullptr) bp[i] = p.fallback;
   }
@@ -555,6 +832,13 @@ __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
     q[i] = ldg16(bp[i] + off.down_q + qo);
     sb[i] = meta_bits<META>(bp[i] + off.down_s, gi);
     bb[i] = meta_bits<META>(bp[i] + off.down_b, gi);
+  }
+  if constexpr (FUSED) {
+    stamp(fw.mark, 2);
+    if (wave == 0) wait_counters(fw.done, nslot, fw.epoch * fw.gu_per_slot, fw.err);
+    __syncthreads();
+    load_h(0);
+    stamp(fw.mark, 3);
   }
 
   // Stage h and its per-chunk sums: 8 consecutive threads hold one 32-float
@@ -571,11 +855,7 @@ __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
       }
     }
     if ((pass + 1) * kH4PerThread * kDownThreads >= n4) break;
-#pragma unroll
-    for (int u = 0; u < kH4PerThread; ++u) {
-      const uint32_t f = ((pass + 1) * kH4PerThread + u) * kDownThreads + tid;
-      hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    load_h(pass + 1);
   }
   __syncthreads();
 
@@ -599,13 +879,167 @@ __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   if (c == 0) halves[half * kRowsPerBlock + row_local] = acc;
   __syncthreads();
   if (tid < kRowsPerBlock) {
-    const uint32_t orow = blockIdx.x * kRowsPerBlock + tid;
+    const uint32_t orow = blk * kRowsPerBlock + tid;
     if (orow < D) {
       const float v = halves[tid] + halves[kRowsPerBlock + tid];
       const size_t o = static_cast<size_t>(t) * D + orow;
       p.y[o] = p.residual ? p.residual[o] + v : v;
     }
   }
+  if constexpr (FUSED) stamp(fw.mark, 4);
+}
+
+template <int META, int LPR, int MAXS>
+__global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
+  extern __shared__ __align__(16) float hs[];  // chunks, then chunk sums, then [2][rows] halves
+  down_block<META, LPR, MAXS, false>(p, blockIdx.y, blockIdx.x, hs, FusedWaits{});
+}
+
+// ---------------------------------------------------------------------------
+// The single-launch decode kernel (one token, every expert resident). Blocks
+// [0, nr) route, then ngu gate/up blocks (the shared expert's first), then
+// the down blocks. Each phase runs the code of the three-kernel decode above,
+// so both give the same bits.
+constexpr int kFusedRouteLoads = 4;  // hidden <= 2048
+constexpr int kFusedMaxSlots = 12;
+constexpr int kFusedPer = 2;  // experts <= 512
+
+struct FusedParams {
+  osmd_moe_args a;
+  GateUpParams gp;
+  DownParams dp;
+  uint32_t* sync;   // handshake buffer (fused_layout)
+  uint64_t* trace;  // [grid][8] timeline, or null
+  uint32_t nr, ngu, gu_blocks_per_slot, grid;
+};
+
+template <int RD, int META, int LPR>
+__global__ __launch_bounds__(256) void fused_decode_kernel(FusedParams f) {
+  extern __shared__ __align__(16) float lds[];  // x of the token, or the down staging
+  __shared__ uint32_t s_epoch;
+  __shared__ Selection<kFusedPer> sel;
+  __shared__ const uint8_t* s_blob[kFusedMaxSlots];
+  __shared__ float s_w[kFusedMaxSlots];
+  const uint32_t b = blockIdx.x;
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  uint8_t* base = reinterpret_cast<uint8_t*>(f.sync);
+  const FusedLayout lay = fused_layout(f.grid, f.a.expert_count, f.gp.src.nslot, f.a.geom.inter);
+  uint32_t* err = f.sync;
+  uint32_t* launch = reinterpret_cast<uint32_t*>(base + lay.launch);
+  uint64_t* tl = reinterpret_cast<uint64_t*>(base + lay.logits);  // tagged logits, then the gate
+  uint64_t* rec = reinterpret_cast<uint64_t*>(base + lay.record);
+  uint64_t* th = reinterpret_cast<uint64_t*>(base + lay.h);  // then + (e % 4) buffers, below
+  uint32_t* done = reinterpret_cast<uint32_t*>(base + lay.done);
+  uint64_t* mark = f.trace ? f.trace + static_cast<size_t>(b) * 8u : nullptr;
+  stamp(mark, 0);
+  if (mark != nullptr && tid == 0) mark[7] = __smid();
+  // This launch's number, from the workgroup's own launch counter.
+  if (tid == 0) {
+    const uint32_t e = __hip_atomic_load(launch + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    __hip_atomic_store(launch + b, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_epoch = e;
+  }
+  const RouteView& rv = f.gp.rv;
+  const uint32_t k = f.a.top_k, E = f.a.expert_count;
+  const uint32_t nslot = f.gp.src.nslot;
+
+  if (b < f.nr) {
+    // Router rows; stage_x's barrier makes s_epoch visible before the stores.
+    route_block<RD, kFusedRouteLoads>(f.a, 0u, b, lds,
+                                      [&](uint32_t row, float v) { store_tagged(tl + row, s_epoch, v); });
+    stamp(mark, 1);
+    return;
+  }
+  __syncthreads();
+  const uint32_t e = s_epoch;
+  th += static_cast<size_t>(e % kHBuffers) * (round_up128(static_cast<size_t>(nslot) * f.a.geom.inter * 8u) / 8u);
+  if (b == f.nr) {
+    // The selector: every thread reads its experts' tagged logits (thread 0
+    // also the gate) until the whole workgroup has this launch's, selects,
+    // and threads r < nslot write the records.
+    const uint32_t bs = tid * kFusedPer;
+    float pv[kFusedPer];
+    const uint8_t* tab[kFusedPer];
+#pragma unroll
+    for (int j = 0; j < kFusedPer; ++j) {
+      tab[j] = rv.expert_table[(bs + j < E) ? bs + j : E - 1u];
+      // Loaded here, while the logits are still being computed: left alone,
+      // the compiler issues these loads after the wait below.
+      asm volatile("" : : "v"(tab[j]));
+    }
+    const bool has_shared = nslot > k;
+    for (uint32_t spin = 0;; ++spin) {
+      bool ok = true;
+#pragma unroll
+      for (int j = 0; j < kFusedPer; ++j) {
+        const uint64_t v = load_tagged(tl + ((bs + j < E) ? bs + j : E - 1u));
+        ok = ok && tag_current(v, e);
+        pv[j] = tagged_value(v);
+      }
+      if (has_shared && tid == 0) {
+        const uint64_t v = load_tagged(tl + E);
+        ok = ok && tag_current(v, e);
+        s_w[0] = tagged_value(v);
+      }
+      // Both exits are decided for the whole workgroup (the loop holds barriers).
+      if (__syncthreads_and(ok)) break;
+      if (__syncthreads_or(tid == 0 && give_up(spin, err))) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    const float gate = s_w[0];
+    stamp(mark, 1);
+    select_values<kFusedPer>(rv, pv, tab, sel, mark);
+    stamp(mark, 2);
+    // Records: weights as the per-token kernels publish them (p / mass in
+    // pick order when renormalised), the shared expert last with its gate.
+    if (tid < nslot) {
+      float mass = 0.0f;
+      for (uint32_t r = 0; r < k; ++r) mass = mass + sel.p[r];
+      const uint64_t my = tid < k ? record_of(e, sel.id[tid], rv.norm_topk_prob ? sel.p[tid] / mass : sel.p[tid])
+                                  : record_of(e, kSharedId, gate);
+#pragma unroll
+      for (uint32_t c = 0; c < kRecordCopies; ++c)
+        __hip_atomic_store(rec + c * kRecordSlots + tid, my, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    stamp(mark, 3);
+    publish_selection(rv, 0u, tid, sel);  // ids, weights, mass, slot pointers for the host
+    stamp(mark, 4);
+    return;
+  }
+  FusedWaits fw{err, e, rec + (b % kRecordCopies) * kRecordSlots, th, done, f.gu_blocks_per_slot, mark, &rv,
+                s_blob, s_w};
+  const uint32_t g = b - f.nr - 1u;
+  if (g < f.ngu) {
+    const uint32_t si = g / f.gu_blocks_per_slot, blk = g % f.gu_blocks_per_slot;
+    const uint32_t j = (f.a.flags & OSMD_MOE_SHARED) ? (si == 0 ? k : si - 1u) : si;
+    stage_x(f.a, 0u, lds, false);
+    stamp(mark, 1);
+    float xr[1][32];
+    load_xr<1>(lds, f.a.geom.hidden / 32u, lane, xr);
+    const uint8_t* blob;
+    if (j < k) {
+      if (wave == 0) {
+        FusedWaits one = fw;
+        one.record += j;
+        const uint64_t r = read_record(one, 1u);
+        if (lane == 0) s_blob[0] = record_blob(rv, r);
+      }
+      __syncthreads();
+      blob = s_blob[0];
+    } else {
+      blob = f.a.shared_expert;
+    }
+    if (blob == nullptr) blob = f.a.fallback_blob;
+    stamp(mark, 2);
+    gate_up_rows<META, 1>(f.gp, 0u, j, blk, blob, xr, [&](size_t i, float v) { store_tagged(th + i, e, v); });
+    stamp(mark, 3);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this wavefront's h stores are complete
+    __syncthreads();
+    if (tid == 0) __hip_atomic_fetch_add(done + j * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    stamp(mark, 4);
+    return;
+  }
+  down_block<META, LPR, kFusedMaxSlots, true>(f.dp, 0u, g - f.ngu, lds, fw);
 }
 
 // ---------------------------------------------------------------------------
@@ -623,11 +1057,8 @@ int launch_gate_up_cpl(const GateUpParams& gp, uint32_t tokens, int per, hipStre
   const dim3 grid((gp.g.inter + rows_per_block - 1) / rows_per_block, gp.src.nslot, tokens);
   switch (per) {
     case 0: gate_up_kernel<META, CPL, 0><<<grid, 256, 0, st>>>(gp); break;
-    case 1: gate_up_kernel<META, CPL, 1><<<grid, 256, 0, st>>>(gp); break;
     case 2: gate_up_kernel<META, CPL, 2><<<grid, 256, 0, st>>>(gp); break;
-    case 4: gate_up_kernel<META, CPL, 4><<<grid, 256, 0, st>>>(gp); break;
-    case 8: gate_up_kernel<META, CPL, 8><<<grid, 256, 0, st>>>(gp); break;
-    default: gate_up_kernel<META, CPL, 16><<<grid, 256, 0, st>>>(gp); break;
+    default: gate_up_kernel<META, CPL, 4><<<grid, 256, 0, st>>>(gp); break;
   }
   return launch_status();
 }
@@ -689,7 +1120,11 @@ int launch_down(const DownParams& dp, uint32_t tokens, hipStream_t st) {
   }
 }
 
-int selection_per(uint32_t experts) { return pow2_at_least((experts + kWave - 1) / kWave); }
+// Experts per lane of a selection: 8 up to 512 experts, 16 beyond. One width
+// for every expert count in a range keeps the order of the wavefront sums of
+// the softmax the same in every kernel that selects (the per-token kernels,
+// the select kernel, the single launch), so they publish the same bits.
+int selection_per(uint32_t experts) { return experts <= 2u * kSelThreads ? 2 : 4; }
 
 template <int RD>
 int launch_route_rd(const osmd_moe_args& a, hipStream_t st) {
@@ -720,13 +1155,90 @@ RouteView route_view(const osmd_moe_args& a) {
 int launch_select(const osmd_moe_args& a, hipStream_t st) {
   const RouteView rv = route_view(a);
   switch (selection_per(a.expert_count)) {
-    case 1: select_kernel<1><<<a.tokens, kWave, 0, st>>>(rv); break;
-    case 2: select_kernel<2><<<a.tokens, kWave, 0, st>>>(rv); break;
-    case 4: select_kernel<4><<<a.tokens, kWave, 0, st>>>(rv); break;
-    case 8: select_kernel<8><<<a.tokens, kWave, 0, st>>>(rv); break;
-    default: select_kernel<16><<<a.tokens, kWave, 0, st>>>(rv); break;
+    case 2: select_kernel<2><<<a.tokens, kSelThreads, 0, st>>>(rv); break;
+    default: select_kernel<4><<<a.tokens, kSelThreads, 0, st>>>(rv); break;
   }
   return launch_status();
+}
+
+// Shape of the single-launch grid.
+struct FusedShape {
+  uint32_t nr, bps, ngu, nd, grid, lpr;
+  size_t lds;
+};
+
+FusedShape fused_shape(const osmd_moe_args& a) {
+  FusedShape f;
+  const uint32_t shared = (a.flags & OSMD_MOE_SHARED) ? 1u : 0u;
+  const uint32_t nslot = a.top_k + shared;
+  const uint32_t D = a.geom.hidden, I = a.geom.inter;
+  f.nr = (a.expert_count + shared + kRouteWaves - 1) / kRouteWaves;
+  const uint32_t gu_rows = kGuWaves * kGuRowsPerWave;
+  f.bps = (I + gu_rows - 1) / gu_rows;
+  f.ngu = nslot * f.bps;
+  f.lpr = static_cast<uint32_t>(pow2_at_least(I / 32u));
+  const uint32_t rows = 2u * (kWave / f.lpr);
+  f.nd = (D + rows - 1) / rows;
+  f.grid = f.nr + 1u + f.ngu + f.nd;
+  const size_t down = down_lds_bytes(I, nslot, rows);
+  f.lds = down > D * sizeof(float) ? down : D * sizeof(float);
+  return f;
+}
+
+bool fused_supported(const osmd_moe_args& a) {
+  const uint32_t nslot = a.top_k + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
+  const uint32_t D = a.geom.hidden, I = a.geom.inter;
+  const uint32_t lpr = static_cast<uint32_t>(pow2_at_least(I / 32u));
+  return a.tokens == 1u && a.expert_table != nullptr && a.slot_ptrs != nullptr &&
+         (a.router_dtype == OSM_META_BF16 || a.router_dtype == OSM_META_F32) && D % 32u == 0u &&
+         D <= 512u * kFusedRouteLoads && I % 32u == 0u && (lpr == 4u || lpr == 8u || lpr == 16u) &&
+         a.expert_count <= kSelThreads * kFusedPer && nslot <= static_cast<uint32_t>(kFusedMaxSlots) &&
+         fused_shape(a).lds <= 65536u;
+}
+
+template <int RD, int META>
+int launch_fused_meta(const FusedParams& f, const FusedShape& sh, hipStream_t st) {
+  switch (sh.lpr) {
+    case 4: fused_decode_kernel<RD, META, 4><<<sh.grid, 256, sh.lds, st>>>(f); break;
+    case 8: fused_decode_kernel<RD, META, 8><<<sh.grid, 256, sh.lds, st>>>(f); break;
+    default: fused_decode_kernel<RD, META, 16><<<sh.grid, 256, sh.lds, st>>>(f); break;
+  }
+  return launch_status();
+}
+
+template <int RD>
+int launch_fused_rd(const FusedParams& f, const FusedShape& sh, hipStream_t st) {
+  switch (f.a.geom.meta_dtype) {
+    case OSM_META_F32: return launch_fused_meta<RD, OSM_META_F32>(f, sh, st);
+    case OSM_META_F16: return launch_fused_meta<RD, OSM_META_F16>(f, sh, st);
+    default: return launch_fused_meta<RD, OSM_META_BF16>(f, sh, st);
+  }
+}
+
+GateUpParams gate_up_params(const osmd_moe_args& a) {
+  const uint32_t nslot = a.top_k + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
+  GateUpParams gp;
+  gp.g = a.geom;
+  gp.src = SlotSource{a.slot_ptrs, nullptr, nslot};
+  gp.rv = route_view(a);
+  gp.x = a.x_norm;
+  gp.h = a.h;
+  return gp;
+}
+
+DownParams down_params(const osmd_moe_args& a) {
+  const uint32_t nslot = a.top_k + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
+  DownParams dp;
+  dp.g = a.geom;
+  dp.src = SlotSource{a.slot_ptrs, nullptr, nslot};
+  dp.top_k = a.top_k;
+  dp.weights = a.weights;
+  dp.shared_gate = a.shared_gate;
+  dp.fallback = a.fallback_blob;
+  dp.h = a.h;
+  dp.residual = (a.flags & OSMD_MOE_RESIDUAL) ? a.x : nullptr;
+  dp.y = a.y;
+  return dp;
 }
 
 }  // namespace
@@ -758,30 +1270,12 @@ int osmd_moe_route(const osmd_moe_args* a, osmd_stream s) {
 }
 
 int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s) {
-  const uint32_t nslot = a->top_k + ((a->flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  GateUpParams gp;
-  gp.g = a->geom;
-  gp.src = SlotSource{a->slot_ptrs, nullptr, nslot};
-  gp.rv = route_view(*a);
-  gp.x = a->x_norm;
-  gp.h = a->h;
   const int per = a->expert_table ? selection_per(a->expert_count) : 0;
-  return launch_gate_up(gp, a->tokens, per, static_cast<hipStream_t>(s));
+  return launch_gate_up(gate_up_params(*a), a->tokens, per, static_cast<hipStream_t>(s));
 }
 
 int osmd_moe_down(const osmd_moe_args* a, osmd_stream s) {
-  const uint32_t nslot = a->top_k + ((a->flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  DownParams dp;
-  dp.g = a->geom;
-  dp.src = SlotSource{a->slot_ptrs, nullptr, nslot};
-  dp.top_k = a->top_k;
-  dp.weights = a->weights;
-  dp.shared_gate = a->shared_gate;
-  dp.fallback = a->fallback_blob;
-  dp.h = a->h;
-  dp.residual = (a->flags & OSMD_MOE_RESIDUAL) ? a->x : nullptr;
-  dp.y = a->y;
-  return launch_down(dp, a->tokens, static_cast<hipStream_t>(s));
+  return launch_down(down_params(*a), a->tokens, static_cast<hipStream_t>(s));
 }
 
 int osmd_moe_experts(const osmd_moe_args* a, osmd_stream s) {
@@ -793,6 +1287,42 @@ int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s) {
   // With a complete expert table the selection runs inside gate_up.
   const int r = a->expert_table ? osmd_moe_router(a, s) : osmd_moe_route(a, s);
   return r != 0 ? r : osmd_moe_experts(a, s);
+}
+
+int osmd_moe_fused_supported(const osmd_moe_args* a) { return fused_supported(*a) ? 1 : 0; }
+
+size_t osmd_moe_fused_sync_bytes(const osmd_moe_args* a) {
+  const uint32_t nslot = a->top_k + ((a->flags & OSMD_MOE_SHARED) ? 1u : 0u);
+  return fused_layout(fused_shape(*a).grid, a->expert_count, nslot, a->geom.inter).bytes;
+}
+
+size_t osmd_moe_fused_error_offset(void) { return 0u; }
+
+int osmd_moe_fused_shape(const osmd_moe_args* a, uint32_t* out4) {
+  const FusedShape sh = fused_shape(*a);
+  out4[0] = sh.nr;
+  out4[1] = sh.ngu;
+  out4[2] = sh.nd;
+  out4[3] = sh.grid;
+  return 0;
+}
+
+int osmd_moe_decode_fused(const osmd_moe_args* a, uint32_t* sync, uint64_t* trace, osmd_stream s) {
+  if (!fused_supported(*a) || sync == nullptr) return static_cast<int>(hipErrorInvalidValue);
+  const FusedShape sh = fused_shape(*a);
+  FusedParams f;
+  f.a = *a;
+  f.gp = gate_up_params(*a);
+  f.dp = down_params(*a);
+  f.sync = sync;
+  f.trace = trace;
+  f.nr = sh.nr;
+  f.ngu = sh.ngu;
+  f.gu_blocks_per_slot = sh.bps;
+  f.grid = sh.grid;
+  const hipStream_t st = static_cast<hipStream_t>(s);
+  return a->router_dtype == OSM_META_F32 ? launch_fused_rd<OSM_META_F32>(f, sh, st)
+                                         : launch_fused_rd<OSM_META_BF16>(f, sh, st);
 }
 
 int osmd_expert_forward(const uint8_t* blob, osm_expert_geometry g, const float* x, float* h,

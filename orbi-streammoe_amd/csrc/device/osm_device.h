@@ -130,7 +130,6 @@ typedef struct osmd_moe_args {
   float* x_norm;      /* [B, D]   scratch/out */
   float* h;           /* [B, k+1, I] scratch */
   const uint8_t** slot_ptrs; /* [B, k+1] scratch: blob of each pick, shared last */
-  uint32_t* counter;  /* [B] zero on entry, zero again on exit */
 } osmd_moe_args;
 
 /* Largest top-k and expert count the fused decode kernels accept. */
@@ -154,6 +153,24 @@ int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_router(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_down(const osmd_moe_args* a, osmd_stream s);
+
+/* Single-launch decode of one token with every expert resident: routing,
+ * selection, gate/up and down in one grid whose workgroups signal each other
+ * through `sync` (osmd_moe_fused_sync_bytes(a) bytes, zeroed once before the
+ * first launch and never again; one per layer, launches of one layer in
+ * stream order). A wait that exceeded its spin limit sets the sticky u32 at
+ * byte osmd_moe_fused_error_offset() of sync. osmd_moe_fused_supported tells
+ * whether a (tokens, shape, router dtype, table) can run this way; the
+ * results are the bits of osmd_moe_decode. */
+int osmd_moe_fused_supported(const osmd_moe_args* a);
+size_t osmd_moe_fused_sync_bytes(const osmd_moe_args* a);
+size_t osmd_moe_fused_error_offset(void);
+/* trace: null, or [grid][8] u64 per-workgroup timeline (steady-clock stamps
+ * at phase boundaries, slot 7 the compute unit's hardware id); the grid is
+ * router, gate/up, down blocks, counts from osmd_moe_fused_shape
+ * (router, gate/up, down, grid). */
+int osmd_moe_decode_fused(const osmd_moe_args* a, uint32_t* sync, uint64_t* trace, osmd_stream s);
+int osmd_moe_fused_shape(const osmd_moe_args* a, uint32_t* out4);
 
 /* The selection kernel alone: top-k of a->logits for a->tokens tokens into
  * ids / weights / mass (and slot_ptrs from expert_table when set). */

@@ -33,7 +33,8 @@ struct HipMoeLayer::Impl {
   DeviceBytes router, shared_gate_vec, norm_weight, shared_blob;
   DeviceBytes zero_blob;  // fallback blob when there is no shared expert
   // workspace
-  DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs, counter;
+  DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs;
+  DeviceBytes fused_sync;  // single-launch handshake words (zeroed once)
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
   // grouped (multi-token) path: allocated on its first use
   HipMoePath path = HipMoePath::automatic;
@@ -69,7 +70,7 @@ struct HipMoeLayer::Impl {
            g.inter % 128U == 0U && reinterpret_cast<std::uintptr_t>(x) % 16U == 0U;
   }
   bool use_grouped(std::uint32_t tokens, const void* x) const {
-    if (path == HipMoePath::per_token) return false;
+    if (path == HipMoePath::per_token || path == HipMoePath::single_launch) return false;
     if (path == HipMoePath::grouped) return true;
     return tokens >= kGroupedMinTokens && grouped_ok(x);
   }
@@ -121,8 +122,12 @@ struct HipMoeLayer::Impl {
     a.x_norm = x_norm.as<float>();
     a.h = h.as<float>();
     a.slot_ptrs = slot_ptrs.as<const std::uint8_t*>();
-    a.counter = counter.as<std::uint32_t>();
     return a;
+  }
+
+  bool use_single_launch(const osmd_moe_args& a) const {
+    if (path != HipMoePath::single_launch) return false;
+    return fused_sync.get() != nullptr && osmd_moe_fused_supported(&a) != 0;
   }
 };
 
@@ -217,8 +222,20 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
     if (rc == 0) rc = impl->x_norm.allocate(T * D * sizeof(float));
     if (rc == 0) rc = impl->h.allocate(T * nslot * g.inter * sizeof(float));
     if (rc == 0) rc = impl->slot_ptrs.allocate(T * nslot * sizeof(void*));
-    if (rc == 0) rc = impl->counter.allocate(T * sizeof(std::uint32_t));
-    if (rc == 0) rc = osmd_zero(impl->counter.get(), T * sizeof(std::uint32_t), st);
+    // Slot pointers start null (read as the fallback blob until a selection
+    // writes them).
+    if (rc == 0) rc = osmd_zero(impl->slot_ptrs.get(), impl->slot_ptrs.size(), st);
+    if (rc == 0) {
+      // The single-launch decode's handshake words, when the shape allows it
+      // (a stand-in table pointer: only its presence is checked).
+      const osmd_moe_args probe =
+          impl->args(nullptr, nullptr, 1U, reinterpret_cast<const std::uint8_t* const*>(impl->slot_ptrs.get()), false);
+      if (osmd_moe_fused_supported(&probe) != 0) {
+        const std::size_t bytes = osmd_moe_fused_sync_bytes(&probe);
+        rc = impl->fused_sync.allocate(bytes);
+        if (rc == 0) rc = osmd_zero(impl->fused_sync.get(), bytes, st);
+      }
+    }
     if (rc == 0) rc = osmd_zero(impl->shared_gate.get(), T * sizeof(float), st);
     if (rc == 0) rc = impl->host_ptrs.allocate(T * nslot * sizeof(void*));
     if (rc == 0) rc = osmd_stream_synchronize(st);
@@ -287,6 +304,8 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
       const osmd_moe_grouped_args ga = impl_->grouped_args(a, false);
       rc = osmd_moe_grouped(&ga, context.stream());
     }
+  } else if (impl_->use_single_launch(a)) {
+    rc = osmd_moe_decode_fused(&a, impl_->fused_sync.as<std::uint32_t>(), nullptr, context.stream());
   } else {
     rc = osmd_moe_decode(&a, context.stream());
   }
@@ -299,11 +318,58 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
   return r;
 }
 
-void HipMoeLayer::set_path(HipMoePath path) noexcept {
-  if (impl_) impl_->path = path;
+bool HipMoeLayer::set_path(HipMoePath path, std::string* diagnostic) noexcept {
+  if (!impl_) return set_diag(diagnostic, "MoE layer is not valid"), false;
+  if (path == HipMoePath::single_launch && impl_->fused_sync.get() == nullptr)
+    return set_diag(diagnostic,
+                    "single-launch decode needs hidden <= 2048, intermediate in (64, 512], <= 512 experts, "
+                    "top_k + shared <= 12 and an f32 or bf16 router"),
+           false;
+  impl_->path = path;
+  return true;
 }
 
 HipMoePath HipMoeLayer::path() const noexcept { return impl_ ? impl_->path : HipMoePath::automatic; }
+
+HipDispatchResult HipMoeLayer::trace_single_launch(HipComputeContext& context, const float* x, float* y,
+                                                  const std::uint8_t* const* expert_table, std::uint64_t* trace,
+                                                  std::uint32_t* shape) noexcept {
+  HipDispatchResult r;
+  if (!valid() || !context.activate(&r.diagnostic)) {
+    if (r.diagnostic.empty()) r.diagnostic = "MoE layer is not valid";
+    return r;
+  }
+  if (x == nullptr || y == nullptr || expert_table == nullptr || trace == nullptr || shape == nullptr) {
+    r.diagnostic = "single-launch trace: invalid arguments";
+    return r;
+  }
+  const osmd_moe_args a = impl_->args(x, y, 1U, expert_table, false);
+  if (impl_->fused_sync.get() == nullptr || osmd_moe_fused_supported(&a) == 0) {
+    r.diagnostic = "single-launch decode is not available for this layer";
+    return r;
+  }
+  osmd_moe_fused_shape(&a, shape);
+  const int rc = osmd_moe_decode_fused(&a, impl_->fused_sync.as<std::uint32_t>(), trace, context.stream());
+  if (rc != 0) {
+    r.diagnostic = hip_error("single-launch trace launch failed", rc);
+    return r;
+  }
+  r.executed = true;
+  return r;
+}
+
+bool HipMoeLayer::single_launch_failures(HipComputeContext& context, std::uint32_t* out,
+                                         std::string* diagnostic) const noexcept {
+  if (!valid() || out == nullptr) return set_diag(diagnostic, "invalid layer or output"), false;
+  *out = 0;
+  if (impl_->fused_sync.get() == nullptr) return true;
+  if (!context.activate(diagnostic)) return false;
+  const osmd_stream st = context.stream();
+  int rc = osmd_memcpy_d2h(out, impl_->fused_sync.as<std::uint8_t>() + osmd_moe_fused_error_offset(), 4, st);
+  if (rc == 0) rc = osmd_stream_synchronize(st);
+  if (rc != 0) return set_diag(diagnostic, hip_error("single-launch status download failed", rc)), false;
+  return true;
+}
 
 HipDispatchResult HipMoeLayer::prefill_device_bf16(HipComputeContext& context, const std::uint16_t* x_bf16,
                                                    float* y, std::uint32_t tokens,

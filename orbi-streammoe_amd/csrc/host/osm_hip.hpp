@@ -610,14 +610,18 @@ struct HipMoeResult {
 // Per-layer state that stays resident: router [E, D] and shared-expert gate
 // vector [D] (bf16 or f32), optional RMSNorm weight, the shared expert, and
 // scratch for up to max_tokens tokens.
-// How a decode of several tokens runs: the per-token kernels (every token
-// reads its picks' weights), or grouped GEMMs (tokens bucketed by expert,
-// each expert's weights read once for all its tokens). automatic takes the
-// grouped path from kGroupedMinTokens tokens on, where it was measured to
-// overtake the per-token kernels at the Qwen3-Next shape on MI355X (us per
-// layer, per-token vs grouped: 24 tokens 156 vs 162; 32: 198 vs 189;
-// 64: 369 vs 280; 512: 2730 vs 477).
-enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2 };
+// How a decode runs: the per-token kernels (router, gate/up, down; every
+// token reads its picks' weights), grouped GEMMs (tokens bucketed by expert,
+// each expert's weights read once for all its tokens), or, for one token,
+// the single-launch kernel (the per-token kernels' work in one grid whose
+// workgroups signal each other; same bits). automatic takes the single
+// launch for one token where the shape allows it, and the grouped path from
+// kGroupedMinTokens tokens on, where it was measured to overtake the
+// per-token kernels at the Qwen3-Next shape on MI355X (us per layer,
+// per-token vs grouped: 24 tokens 156 vs 162; 32: 198 vs 189; 64: 369 vs
+// 280; 512: 2730 vs 477). single_launch with more than one token runs the
+// per-token kernels.
+enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2, single_launch = 3 };
 inline constexpr std::uint32_t kGroupedMinTokens = 32;
 
 class HipMoeLayer {
@@ -651,8 +655,20 @@ class HipMoeLayer {
                                                 std::uint32_t tokens,
                                                 const std::uint8_t* const* expert_table,
                                                 bool sublayer) noexcept;
-  void set_path(HipMoePath path) noexcept;
+  // False (path unchanged) for single_launch on a layer whose shape cannot
+  // run as one launch.
+  bool set_path(HipMoePath path, std::string* diagnostic = nullptr) noexcept;
   [[nodiscard]] HipMoePath path() const noexcept;
+  // Waits of the single-launch kernel that ran out of spins since the layer
+  // was created (0 when every launch completed its handshakes).
+  [[nodiscard]] bool single_launch_failures(HipComputeContext& context, std::uint32_t* out,
+                                            std::string* diagnostic = nullptr) const noexcept;
+  // One single-launch decode (MoE form) that also records each workgroup's
+  // timeline into trace (device, [grid][8] u64); shape gets the router,
+  // gate/up and down workgroup counts and the grid size.
+  [[nodiscard]] HipDispatchResult trace_single_launch(HipComputeContext& context, const float* x, float* y,
+                                                      const std::uint8_t* const* expert_table,
+                                                      std::uint64_t* trace, std::uint32_t* shape) noexcept;
   // A prefill chunk in bf16 ([tokens, D], device) through the grouped path:
   // bf16 router, MoE form (no RMSNorm / residual), y fp32 [tokens, D].
   [[nodiscard]] HipDispatchResult prefill_device_bf16(HipComputeContext& context,

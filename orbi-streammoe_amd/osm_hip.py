@@ -22,7 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libosm_hip.so")
 
 OSM_OK, OSM_E_INVALID, OSM_E_RUNTIME, OSM_E_DEVICE = 0, 1, 2, 3
-PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED = 0, 1, 2
+PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED, PATH_SINGLE_LAUNCH = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
 
 
@@ -131,6 +131,8 @@ _PROTOTYPES = {
     "osm_moe_decode_layers": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_layer_launch_phase": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int, c_int]),
     "osm_moe_layer_set_path": (c_int, [_H, c_int]),
+    "osm_moe_layer_wait_failures": (c_int, [_H, _H, POINTER(c_uint32)]),
+    "osm_moe_layer_trace_single_launch": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_void_p, POINTER(c_uint32)]),
     "osm_moe_layer_prefill_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32]),
     "osm_decode_graph_create": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int, POINTER(_H)]),
     "osm_graph_capture_begin": (c_int, [_H]),
@@ -570,8 +572,22 @@ class MoeLayer(_Handle):
         check(load().osm_moe_layer_decode_device(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0))
 
     def set_path(self, path):
-        """PATH_AUTO, PATH_PER_TOKEN or PATH_GROUPED."""
+        """PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED or PATH_SINGLE_LAUNCH."""
         check(load().osm_moe_layer_set_path(self.h, path))
+
+    def trace_single_launch(self, slab, slab_layer, x_ptr, y_ptr, trace_ptr):
+        """One traced single-launch decode; returns (router, gate/up, down, grid)
+        workgroup counts. trace_ptr: device [grid][8] u64."""
+        shape = (c_uint32 * 4)()
+        check(load().osm_moe_layer_trace_single_launch(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr,
+                                                       trace_ptr, shape))
+        return tuple(shape)
+
+    def wait_failures(self) -> int:
+        """Single-launch waits that ran out of spins since creation (0 = none)."""
+        v = c_uint32(0)
+        check(load().osm_moe_layer_wait_failures(self.ctx.h, self.h, ctypes.byref(v)))
+        return v.value
 
     def prefill_device(self, slab, slab_layer, x_bf16_ptr, y_ptr, tokens):
         check(load().osm_moe_layer_prefill_device(self.ctx.h, self.h, slab.h, slab_layer, x_bf16_ptr, y_ptr, tokens))
