@@ -235,15 +235,16 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
 /* How decodes run (no counterpart in the reference, which pushes tokens
  * through the sublayer one at a time with 56 dispatches each,
  * src/session/greedy_token_session.cpp:170-192, routed_moe.cpp:254-430):
- * OSM_PATH_AUTO runs one token as a single launch where the shape allows it
- * (hidden <= 2048, intermediate in (64, 512], <= 512 experts, top_k + shared
- * <= 12, f32 or bf16 router) and takes the grouped GEMMs from 32 tokens on
- * (group 32/64/128, hidden and intermediate multiples of 128, 16-byte
- * aligned input); OSM_PATH_PER_TOKEN always runs the three per-token
- * kernels; OSM_PATH_GROUPED always buckets (token, slot) pairs by expert and
- * reads each expert once; OSM_PATH_SINGLE_LAUNCH runs one-token decodes as
- * one launch (more tokens: the per-token kernels). The single launch and the
- * per-token kernels give the same bits. */
+ * OSM_PATH_AUTO runs the three per-token kernels below 32 tokens and the
+ * grouped GEMMs from 32 tokens on (group 32/64/128, hidden and intermediate
+ * multiples of 128, 16-byte aligned input); OSM_PATH_PER_TOKEN always runs
+ * the per-token kernels; OSM_PATH_GROUPED always buckets (token, slot) pairs
+ * by expert and reads each expert once; OSM_PATH_SINGLE_LAUNCH runs one-token
+ * decodes as one launch (more tokens: the per-token kernels) where the shape
+ * allows it (hidden <= 2048, intermediate in (64, 512], <= 512 experts,
+ * top_k + shared <= 12, f32 or bf16 router; set_path fails otherwise). The
+ * single launch and the per-token kernels give the same bits; on MI355X at
+ * the Qwen3-Next shape the single launch is the slower of the two. */
 enum osm_moe_path { OSM_PATH_AUTO = 0, OSM_PATH_PER_TOKEN = 1, OSM_PATH_GROUPED = 2, OSM_PATH_SINGLE_LAUNCH = 3 };
 int osm_moe_layer_set_path(osm_moe_layer l, int path);
 /* The single launch's workgroups wait on each other with bounded spins; a

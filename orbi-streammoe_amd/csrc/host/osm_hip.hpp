@@ -614,8 +614,9 @@ struct HipMoeResult {
 // token reads its picks' weights), grouped GEMMs (tokens bucketed by expert,
 // each expert's weights read once for all its tokens), or, for one token,
 // the single-launch kernel (the per-token kernels' work in one grid whose
-// workgroups signal each other; same bits). automatic takes the single
-// launch for one token where the shape allows it, and the grouped path from
+// workgroups hand data to each other; same bits, measured slower than the
+// three kernels at the Qwen3-Next shape, so only taken when asked for).
+// automatic takes the per-token kernels, and the grouped path from
 // kGroupedMinTokens tokens on, where it was measured to overtake the
 // per-token kernels at the Qwen3-Next shape on MI355X (us per layer,
 // per-token vs grouped: 24 tokens 156 vs 162; 32: 198 vs 189; 64: 369 vs
