@@ -51,8 +51,10 @@ def parse():
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--phase-rounds", type=int, default=20)
     ap.add_argument("--cpu-tokens", type=int, default=64, help="token-layers in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cache-gb", type=float, default=16.0,
+                    help="HBM cap of the expert cache in the capped-cache decode (GB)")
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the decode-batch and prefill measurements")
+                    help="skip the decode-batch, prefill and capped-cache measurements")
     ap.add_argument("--counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no benchmark: summarise two rocprofv3 --pmc counter_collection.csv files "
                          "(FETCH_SIZE, WRITE_SIZE) of a run with --copy-probe-mb into HBM bytes per dispatch")
@@ -227,6 +229,85 @@ def prefill(ctx, moes, slab, args, layers=8):
     return res
 
 
+def correlated_trace(rng, layers, steps, repeat_p):
+    """Routed experts per (step, layer): each of the k picks repeats one of
+    that layer's previous-step picks with probability repeat_p, else it is a
+    fresh expert; picks within a step are distinct."""
+    prev = [None] * layers
+    trace = []
+    for _s in range(steps):
+        row = []
+        for l in range(layers):
+            ids = []
+            for _j in range(K):
+                cands = [e for e in (prev[l] or []) if e not in ids]
+                if cands and rng.random() < repeat_p:
+                    ids.append(int(rng.choice(cands)))
+                    continue
+                while True:
+                    e = int(rng.integers(E))
+                    if e not in ids:
+                        break
+                ids.append(e)
+            prev[l] = ids
+            row.append(np.array(ids, np.uint32).reshape(1, K))
+        trace.append(row)
+    return trace
+
+
+def capped_cache_decode(ctx, g, moes, args, steps=64, warm=8, repeat_p=0.6):
+    """Config 3b: the layer stack as chained sublayers (RMSNorm, MoE,
+    residual), one token per step, with the HBM expert cache capped at
+    --cache-gb and misses filled from the whole model in pinned host memory
+    over PCIe. Routing follows a correlated trace (correlated_trace). The
+    path is host-driven, as the reference's cache is: each layer routes on
+    the device, makes its picks resident, then runs the expert kernels."""
+    L = len(moes)
+    t0 = time.time()
+    try:
+        store = osm_hip.ExpertStore(g, L, E)
+        store.synthesize(ctx, args.seed)  # the slab's weights
+    except osm_hip.OsmError as e:
+        log(f"[bench] capped cache: host store unavailable ({e}); skipped")
+        return {"skipped": str(e)}
+    budget = int(args.cache_gb * 1e9)
+    cache = osm_hip.ExpertCache(ctx, budget, store=store)
+    log(f"[bench] capped cache: {L * E * store.stride / 1e9:.1f} GB pinned host store, "
+        f"{budget / 1e9:.0f} GB cache, ready in {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(args.seed + 7)
+    trace = correlated_trace(rng, L, steps, repeat_p)
+    w = np.arange(K, 0, -1, dtype=np.float32)
+    w = (w / w.sum()).astype(np.float32).reshape(1, K)
+    xs = osm_hip.synth_tokens(ctx, args.seed, 900000, steps, D)
+
+    def run_step(s):
+        x = xs[s:s + 1]
+        for l in range(L):
+            x = moes[l].run_cached(cache, l, x, sublayer=True, picks=(trace[s][l], w))["out"]
+
+    for s in range(warm):
+        run_step(s)
+    st0, b0 = cache.stats(), cache.bytes_filled
+    t = time.perf_counter()
+    for s in range(warm, steps):
+        run_step(s)
+    dt = time.perf_counter() - t
+    st1, b1 = cache.stats(), cache.bytes_filled
+    n = (steps - warm) * L
+    gets = (st1["hits"] - st0["hits"]) + (st1["misses"] - st0["misses"])
+    res = {"layers": L, "steps": steps - warm, "warm_steps": warm, "repeat_p": repeat_p,
+           "cache_budget_GB": round(budget / 1e9, 1), "resident_GB": round(st1["resident_bytes"] / 1e9, 2),
+           "us_per_token_layer": round(dt / n * 1e6, 1),
+           "hit_rate": round((st1["hits"] - st0["hits"]) / max(gets, 1), 4),
+           "misses_per_token_layer": round((st1["misses"] - st0["misses"]) / n, 3),
+           "evictions": st1["evictions"] - st0["evictions"],
+           "fill_GBps": round((b1 - b0) / dt / 1e9, 2),
+           "host_path": "per layer: route on the device, host reads the picks' residency, fills, expert kernels, output read back"}
+    log(f"[bench] capped cache: {json.dumps(res)}")
+    del cache, store
+    return res
+
+
 def cpu_baseline(seed, tokens):
     """The reference's CPU path (its own functions, compiled from its sources
     into oracle/_ref) on `tokens` token-layers of layer 0, one host core."""
@@ -387,6 +468,7 @@ def main():
     if not args.no_extras:
         extras["decode_batches"] = decode_batches(ctx, moes, slab, args)
         extras["prefill"] = prefill(ctx, moes, slab, args)
+        extras["capped_cache"] = capped_cache_decode(ctx, g, moes, args)
 
     cpu = None
     if args.cpu_tokens > 0:

@@ -228,6 +228,16 @@ int osm_moe_layer_run_slab(osm_context ctx, osm_moe_layer l, osm_expert_slab sla
 int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache cache,
                              uint32_t layer, const float* hidden, uint32_t tokens, int sublayer,
                              const osm_moe_outputs* outputs);
+/* Same with caller-chosen routed experts: ids [tokens, k] (< expert_count)
+ * and weights [tokens, k] (finite) replace the router's picks; the router
+ * still gives the shared gate, logits and the normalised input. No
+ * counterpart in the reference, whose routed MoE always routes itself
+ * (routed_moe.cpp:13-92); it drives the cache with an external routing
+ * trace, e.g. correlated routing across decode steps. */
+int osm_moe_layer_run_cached_picks(osm_context ctx, osm_moe_layer l, osm_expert_cache cache,
+                                   uint32_t layer, const float* hidden, uint32_t tokens, int sublayer,
+                                   const uint32_t* ids, const float* weights,
+                                   const osm_moe_outputs* outputs);
 /* Device pointers in and out, stream-ordered, no synchronisation. */
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,

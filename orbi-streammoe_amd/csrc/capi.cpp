@@ -591,6 +591,20 @@ int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache 
   OSM_GUARD_END
 }
 
+int osm_moe_layer_run_cached_picks(osm_context ctx, osm_moe_layer l, osm_expert_cache cache, uint32_t layer,
+                                   const float* hidden, uint32_t tokens, int sublayer, const uint32_t* ids,
+                                   const float* weights, const osm_moe_outputs* outputs) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !l || !cache || !hidden || !ids || !weights) return fail(OSM_E_INVALID, "null argument");
+  const std::size_t D = l->layer.config().geometry.hidden;
+  const osm::HipMoePicks picks{ids, weights};
+  auto r = osm::run_qwen_sparse_moe_hip(ctx->ctx, *cache->cache, l->layer, layer,
+                                        {hidden, static_cast<std::size_t>(tokens) * D}, sublayer != 0, &picks);
+  if (!r.executed) return fail(OSM_E_INVALID, r.diagnostic);
+  return write_outputs(r, outputs, sublayer != 0);
+  OSM_GUARD_END
+}
+
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,
                                 uint32_t tokens, int sublayer) {

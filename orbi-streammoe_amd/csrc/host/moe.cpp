@@ -541,7 +541,8 @@ struct MoeLayerAccess {
 
 HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpertCache& expert_cache,
                                      HipMoeLayer& layer_state, std::uint32_t layer,
-                                     std::span<const float> hidden, bool sublayer) noexcept {
+                                     std::span<const float> hidden, bool sublayer,
+                                     const HipMoePicks* picks) noexcept {
   HipMoeResult r;
   try {
     auto* m = MoeLayerAccess::impl(layer_state);
@@ -563,14 +564,37 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
       r.diagnostic = "MoE sublayer decode needs an RMSNorm weight";
       return r;
     }
+    if (picks != nullptr) {
+      if (picks->ids == nullptr || picks->weights == nullptr) {
+        r.diagnostic = "routed MoE picks need ids and weights";
+        return r;
+      }
+      for (std::size_t i = 0; i < tokens * K; ++i) {
+        if (picks->ids[i] >= m->cfg.expert_count) {
+          r.diagnostic = "routed MoE pick " + std::to_string(picks->ids[i]) + " is out of range";
+          return r;
+        }
+        if (!std::isfinite(picks->weights[i])) {
+          r.diagnostic = "routed MoE encountered a non-finite routing weight";  // routed_moe.cpp:33-37
+          return r;
+        }
+      }
+    }
     if (!context.activate(&r.diagnostic)) return r;
     const osmd_stream st = context.stream();
-    // 1. route on the device
+    // 1. route on the device (with given picks: for the shared gate, logits
+    // and normalised input; the picks then replace ids and weights)
     int rc = osmd_memcpy_h2d(m->x_in.get(), hidden.data(), hidden.size_bytes(), st);
     osmd_moe_args a = m->args(m->x_in.as<const float>(), m->y_out.as<float>(), tokens, nullptr, sublayer);
     if (rc == 0) rc = osmd_moe_route(&a, st);
     std::vector<std::uint32_t> ids(tokens * K);
-    if (rc == 0) rc = osmd_memcpy_d2h(ids.data(), m->ids.get(), ids.size() * 4, st);
+    if (picks != nullptr) {
+      std::copy(picks->ids, picks->ids + tokens * K, ids.begin());
+      if (rc == 0) rc = osmd_memcpy_h2d(m->ids.get(), picks->ids, ids.size() * 4, st);
+      if (rc == 0) rc = osmd_memcpy_h2d(m->weights.get(), picks->weights, ids.size() * 4, st);
+    } else if (rc == 0) {
+      rc = osmd_memcpy_d2h(ids.data(), m->ids.get(), ids.size() * 4, st);
+    }
     if (rc == 0) rc = osmd_stream_synchronize(st);
     if (rc != 0) {
       r.diagnostic = hip_error("Qwen sparse MoE routing failed", rc);

@@ -755,9 +755,18 @@ class HipGraph {
 // device, make every pick resident (misses filled on the side stream), then
 // the fused expert kernels. The cache decides residency on the host from the
 // routed ids, as the reference's cache does.
+// picks: null, or caller-chosen routed experts ([tokens, top_k] ids and
+// weights) that replace the router's picks. The router still runs for the
+// shared gate (and the logits and RMSNorm), and routing returns the given
+// ids and weights. No counterpart in the reference, whose routed MoE always
+// routes itself: it drives the cache with an external routing trace.
+struct HipMoePicks {
+  const std::uint32_t* ids = nullptr;
+  const float* weights = nullptr;
+};
 [[nodiscard]] HipMoeResult run_qwen_sparse_moe_hip(
     HipComputeContext& context, HipResidentExpertCache& expert_cache,
     HipMoeLayer& layer_state, std::uint32_t layer, std::span<const float> hidden,
-    bool sublayer) noexcept;
+    bool sublayer, const HipMoePicks* picks = nullptr) noexcept;
 
 }  // namespace osm

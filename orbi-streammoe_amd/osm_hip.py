@@ -127,6 +127,7 @@ _PROTOTYPES = {
     "osm_moe_layer_destroy": (None, [_H]),
     "osm_moe_layer_run_slab": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_uint32, c_int, POINTER(MoeOutputs)]),
     "osm_moe_layer_run_cached": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_uint32, c_int, POINTER(MoeOutputs)]),
+    "osm_moe_layer_run_cached_picks": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_uint32, c_int, c_void_p, c_void_p, POINTER(MoeOutputs)]),
     "osm_moe_layer_decode_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_decode_layers": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_layer_launch_phase": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int, c_int]),
@@ -562,10 +563,17 @@ class MoeLayer(_Handle):
         check(load().osm_moe_layer_run_slab(self.ctx.h, self.h, slab.h, slab_layer, _p(x), x.shape[0], 1 if sublayer else 0, ctypes.byref(o)))
         return res
 
-    def run_cached(self, cache: "ExpertCache", layer, hidden, sublayer=False) -> dict:
+    def run_cached(self, cache: "ExpertCache", layer, hidden, sublayer=False, picks=None) -> dict:
+        """picks: None (route), or (ids [tokens, k] uint32, weights [tokens, k] float32)."""
         x = _c(hidden, np.float32).reshape(-1, self.g.hidden)
         res, o = self._outputs(x.shape[0], sublayer)
-        check(load().osm_moe_layer_run_cached(self.ctx.h, self.h, cache.h, layer, _p(x), x.shape[0], 1 if sublayer else 0, ctypes.byref(o)))
+        if picks is None:
+            check(load().osm_moe_layer_run_cached(self.ctx.h, self.h, cache.h, layer, _p(x), x.shape[0], 1 if sublayer else 0, ctypes.byref(o)))
+        else:
+            ids = _c(picks[0], np.uint32)
+            w = _c(picks[1], np.float32)
+            check(load().osm_moe_layer_run_cached_picks(self.ctx.h, self.h, cache.h, layer, _p(x), x.shape[0], 1 if sublayer else 0,
+                                                        _p(ids), _p(w), ctypes.byref(o)))
         return res
 
     def decode_device(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer=False):

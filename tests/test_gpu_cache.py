@@ -10,7 +10,7 @@ import pytest
 
 import oracle as O
 import osm_hip
-from helpers import cache_fixture_expert, cache_fixture_token, max_abs
+from helpers import cache_fixture_expert, cache_fixture_token, max_abs, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -89,3 +89,42 @@ def test_cached_decode_matches_resident_decode(ctx):
         assert st[key] == po[key], (key, st, po)
     assert po["evictions"] > 0  # the cap was exercised
     assert cache.bytes_filled == st["loads"] * stride
+
+
+def test_cached_decode_with_given_picks(ctx):
+    # Caller-chosen routed experts through the capped cache: the output is the
+    # pick-weighted sum of the chosen experts plus the router's sigmoid gate
+    # times the shared expert (the composition of routed_moe.cpp:320-404 with
+    # the routing replaced); ids and weights come back as given.
+    seed, D, I, G, E, k = 22, 256, 128, 64, 64, 4
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    store = osm_hip.ExpertStore(g, 1, E)
+    store.synthesize(ctx, seed)
+    stride = store.stride
+    cache = osm_hip.ExpertCache(ctx, 6 * stride, store=store)
+    sg_bits = O.synth_shared_gate_bf16(seed, 0, D)
+    shared = O.synth_expert_blob(seed, 0, O.SHARED_EXPERT_ID, D, I, G)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, 0, E, D), osm_hip.BF16, sg_bits, None, shared,
+                           max_tokens=1)
+    rng = np.random.default_rng(seed)
+    sg = O.bf16_bits_to_f32(sg_bits)
+    for t in range(5):
+        x = O.synth_tokens(seed, t, 1, D)
+        ids = rng.choice(E, k, replace=False).astype(np.uint32).reshape(1, k)
+        w = rng.random(k).astype(np.float32)
+        w = (w / w.sum()).astype(np.float32).reshape(1, k)
+        got = moe.run_cached(cache, 0, x, picks=(ids, w))
+        assert np.array_equal(got["ids"], ids) and np.array_equal(got["weights"], w)
+        gate = 1.0 / (1.0 + np.exp(-np.dot(sg.astype(np.float64), x[0].astype(np.float64))))
+        assert abs(got["shared_gate"][0] - gate) <= 1e-6
+        ref = np.zeros(D, np.float64)
+        for j in range(k):
+            ref += float(w[0, j]) * O.expert_forward(store.blob_view(0, int(ids[0, j])), D, I, G, O.META_BF16, x[0])
+        ref += float(got["shared_gate"][0]) * O.expert_forward(shared, D, I, G, O.META_BF16, x[0])
+        assert rel_l2(got["out"][0], ref.astype(np.float32)) <= 1e-3
+    assert cache.stats()["evictions"] > 0  # 20 picks over a 6-expert budget
+    bad = np.array([[0, 1, 2, E]], np.uint32)
+    with pytest.raises(osm_hip.OsmError):
+        moe.run_cached(cache, 0, x, picks=(bad, w))
+    with pytest.raises(osm_hip.OsmError):
+        moe.run_cached(cache, 0, x, picks=(ids, np.full((1, k), np.nan, np.float32)))
