@@ -34,6 +34,8 @@
 // t_1 = bf16(x - t_0), ...), each term one more MFMA into the same
 // accumulator: products of bf16 pairs are exact in fp32, so 2 terms carry 16
 // significant bits and 3 terms all 24.
+#include <type_traits>
+
 #include "device_common.hpp"
 
 namespace {
@@ -66,9 +68,20 @@ __device__ __forceinline__ bf16x8 as_operand(uint4 v) {
   return __builtin_bit_cast(bf16x8, u);
 }
 
+// The eight nibbles q of a packed word as the bf16 integers 128 + q, in MFMA
+// operand order: register j holds nibble j (low half) and nibble j + 4 (high
+// half), i.e. ((w >> 4j) & 0x000F000F) | 0x43004300. Two masks split the word
+// into one byte per nibble (lo: nibbles 0, 2, 4, 6; hi: 1, 3, 5, 7), and each
+// register is one byte permutation of lo or hi with 0x43, the high byte of
+// 128.0 in bf16: seven instructions per word instead of eleven.
+// v_perm_b32(s0, s1, sel): result byte i = byte sel.byte[i] of {s0, s1}
+// (selectors 0-3 pick bytes of s1, 4-7 bytes of s0).
 __device__ __forceinline__ bf16x8 nibble_operand(uint32_t w) {
-  const uint32_t m = 0x000F000Fu, bias = 0x43004300u;
-  const u32x4 v = {(w & m) | bias, ((w >> 4) & m) | bias, ((w >> 8) & m) | bias, ((w >> 12) & m) | bias};
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu, k = 0x43434343u;
+  const uint32_t even = 0x04020400u;  // bytes 0 and 2 of s1: nibbles 0, 4 (lo) or 1, 5 (hi)
+  const uint32_t odd = 0x04030401u;   // bytes 1 and 3 of s1: nibbles 2, 6 (lo) or 3, 7 (hi)
+  const u32x4 v = {__builtin_amdgcn_perm(k, lo, even), __builtin_amdgcn_perm(k, hi, even),
+                   __builtin_amdgcn_perm(k, lo, odd), __builtin_amdgcn_perm(k, hi, odd)};
   return __builtin_bit_cast(bf16x8, v);
 }
 
@@ -147,25 +160,43 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
   const uint32_t tok = (t0 + m < T) ? t0 + m : T - 1u;
   const uint16_t* arow = terms + static_cast<size_t>(tok) * NS * D;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (uint32_t k0 = 0; k0 < D; k0 += 32u) {
-    // B: 8 router values of row rr at k0 + 8q, reordered to word order.
-    const uint4 raw = ldg16(wrow + k0 + 8u * q);
-    const uint32_t h4[4] = {raw.x, raw.y, raw.z, raw.w};
-    uint16_t h[8];
+  // C steps of 32 columns per memory round trip: every load of the chunk is
+  // issued before its MFMAs (one step per trip would make the 2048-column
+  // loop 64 round trips long).
+  auto chunk = [&](uint32_t k0, auto steps) {
+    constexpr int C = decltype(steps)::value;
+    uint4 raw[C], av[C][NS];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      h[2 * j] = static_cast<uint16_t>(h4[j] & 0xFFFFu);
-      h[2 * j + 1] = static_cast<uint16_t>(h4[j] >> 16);
+    for (int c = 0; c < C; ++c) {
+      const uint32_t k = k0 + 32u * c + 8u * q;
+      raw[c] = ldg16(wrow + k);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) av[c][s] = ldg16(arow + static_cast<size_t>(s) * D + k);
     }
-    uint4 bv;
-    bv.x = h[word_k(0)] | (static_cast<uint32_t>(h[word_k(1)]) << 16);
-    bv.y = h[word_k(2)] | (static_cast<uint32_t>(h[word_k(3)]) << 16);
-    bv.z = h[word_k(4)] | (static_cast<uint32_t>(h[word_k(5)]) << 16);
-    bv.w = h[word_k(6)] | (static_cast<uint32_t>(h[word_k(7)]) << 16);
-    const bf16x8 b = as_operand(bv);
+    __builtin_amdgcn_sched_barrier(0);  // keeps every load of the chunk ahead of its MFMAs
 #pragma unroll
-    for (int s = 0; s < NS; ++s) acc = mfma(as_operand(ldg16(arow + static_cast<size_t>(s) * D + k0 + 8u * q)), b, acc);
-  }
+    for (int c = 0; c < C; ++c) {
+      // B: 8 router values of row rr at k0 + 32c + 8q, reordered to word order.
+      const uint32_t h4[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
+      uint16_t h[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        h[2 * j] = static_cast<uint16_t>(h4[j] & 0xFFFFu);
+        h[2 * j + 1] = static_cast<uint16_t>(h4[j] >> 16);
+      }
+      uint4 bv;
+      bv.x = h[word_k(0)] | (static_cast<uint32_t>(h[word_k(1)]) << 16);
+      bv.y = h[word_k(2)] | (static_cast<uint32_t>(h[word_k(3)]) << 16);
+      bv.z = h[word_k(4)] | (static_cast<uint32_t>(h[word_k(5)]) << 16);
+      bv.w = h[word_k(6)] | (static_cast<uint32_t>(h[word_k(7)]) << 16);
+      const bf16x8 b = as_operand(bv);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) acc = mfma(as_operand(av[c][s]), b, acc);
+    }
+  };
+  uint32_t k0 = 0;
+  for (; k0 + 256u <= D; k0 += 256u) chunk(k0, std::integral_constant<int, 8>{});
+  if (k0 < D) chunk(k0, std::integral_constant<int, 4>{});  // D is a multiple of 128
 #pragma unroll
   for (int j = 0; j < 4; ++j) {  // D rows 4q + j are tokens, column m the router row
     const uint32_t t = t0 + 4u * q + j;
@@ -276,14 +307,16 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
 // ---------------------------------------------------------------------------
 // Grouped q4 GEMMs over the tile list, split along K.
 //
-// A workgroup of 4 waves takes one tile (<= 16 pairs), one block of weight
-// rows and one K range of KS = 32 * NSTEP columns. Every wave first issues
-// all of its packed-word and metadata loads for the range, then every thread
-// issues its share of the tile's activation terms for the range (rows past
-// the tile's count are not staged: MFMA rows read the last real row instead)
-// before storing them to LDS, behind one barrier. A wave so costs one memory
-// round trip and no per-chunk synchronisation, and a compute unit keeps
-// about 100 KB of weights in flight (three workgroups).
+// A work item is one tile (<= 16 pairs), one K range of KS = 32 * NSTEP
+// columns and a run of item_blocks consecutive row blocks; a workgroup of 4
+// waves works through items b, b + grid, ... (persistent, one grid of as
+// many workgroups as are resident). Per item it stages the tile's activation
+// terms for the range into LDS once (rows past the tile's count are not
+// staged: MFMA rows read the last real row instead), then streams the row
+// blocks' weights with one block in flight ahead of the one being computed:
+// the packed words and metadata of block i+1 (the next item's first block,
+// after the last) are issued before block i's MFMAs. A block is 32 weight
+// rows per wave:
 //   gate/up: 64 rows per workgroup; waves 0-1 gate, waves 2-3 up, 32 rows
 //            each; part[split][proj][pair][row] partial sums.
 //   down:    128 rows per workgroup (32 per wave), times the pair weight;
@@ -298,31 +331,41 @@ struct SplitParams {
   const float* pair_w;    // [P]
   const Tile* tiles;
   uint32_t P;
-  uint32_t max_tiles;  // tile capacity of the workspace
-  uint32_t row_blocks, nsplit;
+  uint32_t max_tiles;   // tile capacity of the workspace
+  uint32_t nsplit;      // K ranges
+  uint32_t item_blocks; // row blocks per item (kItemBlocks)
+  uint32_t chunks;      // items per tile and K range
+  uint32_t items;       // tiles (rounded to whole XCD rounds) x K ranges x chunks
   float* out;
 };
 
-// Workgroup -> (tile, K range, row block). Workgroups are dealt to the 8
-// XCDs round-robin (workgroup b runs on XCD b % 8), so tile t is given to
-// XCD t % 8 and all of its K ranges and row blocks run there, one after the
-// other: the tile's activation rows are read into one L2 only, and the K
-// ranges of the same weight rows are fetched together.
+// Work item -> (tile, K range, first row block). Workgroups are dealt to the
+// 8 XCDs round-robin (workgroup b runs on XCD b % 8) and take items b, b +
+// grid, ... with the grid a multiple of 8, so item b runs on XCD b % 8 too.
+// Tile t is given to XCD t % 8 and all of its items run there: the tile's
+// activation rows are read into one L2 only, and the K ranges of the same
+// weight rows are fetched together.
 constexpr uint32_t kXcds = 8;
+// Row blocks per work item, a compile-time even number so that the kernel's
+// two weight buffers alternate in straight-line code; a run past the last
+// row block loads clamped rows and stores nothing.
+constexpr uint32_t kItemBlocks = 4;
+// s_waitcnt operand: vector memory counter 0, the others at their maximum.
+constexpr int kWaitVmcnt0 = 0x0F70;
 struct SplitWork {
-  uint32_t tile, split, row_block;
+  uint32_t tile, split, first_block;
 };
-__device__ __forceinline__ SplitWork split_work(const SplitParams& p) {
-  const uint32_t b = blockIdx.x, per_tile = p.row_blocks * p.nsplit;
+__device__ __forceinline__ SplitWork split_work(const SplitParams& p, uint32_t b) {
+  const uint32_t per_tile = p.chunks * p.nsplit;
   const uint32_t i = b / kXcds;
   SplitWork w;
   w.tile = (i / per_tile) * kXcds + b % kXcds;
   w.split = i % per_tile % p.nsplit;
-  w.row_block = i % per_tile / p.nsplit;
+  w.first_block = i % per_tile / p.nsplit * p.item_blocks;
   return w;
 }
-uint32_t split_grid(uint32_t max_tiles, uint32_t row_blocks, uint32_t nsplit) {
-  return (max_tiles + kXcds - 1) / kXcds * kXcds * row_blocks * nsplit;
+uint32_t split_items(uint32_t max_tiles, uint32_t nsplit, uint32_t chunks) {
+  return (max_tiles + kXcds - 1) / kXcds * kXcds * nsplit * chunks;
 }
 
 // Metadata of N consecutive groups of one row, kept as loaded: 16-bit values
@@ -383,107 +426,122 @@ constexpr uint32_t split_rows() {
   return PROJ == 2 ? kSplitWaves / 2u * kWaveRows : kSplitWaves * kWaveRows;
 }
 
-template <int META, int PROJ, int S, int NSTEP>
-__global__ __launch_bounds__(kSplitThreads) void split_kernel(SplitParams p) {
-  constexpr uint32_t KS = 32u * NSTEP;
-  constexpr int GPR = NSTEP / S;  // groups per range
-  constexpr uint32_t RS = KS + 8u;  // LDS row stride (bf16), padded against bank conflicts
-  constexpr uint32_t kWgRows = split_rows<PROJ>();
-  constexpr uint32_t kUnitCols = KS / 8u;  // 16-byte units per staged row
-  constexpr uint32_t kUnitsPerThread = kActSplit * kTileTokens * kUnitCols / kSplitThreads;
-  static_assert(kActSplit * kTileTokens * kUnitCols % kSplitThreads == 0, "staging units");
-  static_assert(GPR * kTileTokens <= kSplitThreads, "group sums: one per thread");
-  __shared__ __align__(16) uint16_t a_lds[kActSplit][kTileTokens][RS];
-  __shared__ __align__(16) float xs_lds[GPR][kTileTokens];
+// Wave-uniform copies of values every lane holds alike. The builtin works on
+// (signed) int: each 32-bit half goes through uint32_t, so that the low half
+// of a pointer is zero-extended, not sign-extended, when widened.
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* ptr) {
+  const uint64_t v = reinterpret_cast<uintptr_t>(ptr);
+  const uint64_t lo = uniform_u32(static_cast<uint32_t>(v)), hi = uniform_u32(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>((hi << 32) | lo));
+}
 
-  const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid % kWave, wave = tid / kWave;
-  const uint32_t m = lane % 16u, q = lane / 16u;
-  // The tile and (gate/up) the token of tile row m are loaded together
-  // (tile < the workspace's capacity, so both reads are in bounds; rows >=
-  // count hold stale tokens, never used). Tiles past the last real one have
-  // count 0.
-  const SplitWork wk = split_work(p);
-  if (wk.tile >= p.max_tiles) return;  // the grid rounds the tiles up to whole XCD rounds
-  Tile tl = p.tiles[wk.tile];
-  uint32_t lane_act = PROJ == 2 ? p.tile_rows[wk.tile * kTileTokens + m] : 0u;
-  // The whole record and the arguments the load addresses need are fetched
-  // before the exit test (left alone, the compiler loads them after it, one
-  // more memory round trip on every workgroup's critical path).
-  osm_expert_geometry geo = p.g;
-  const uint16_t* terms = p.terms;
-  asm volatile("" : "+s"(tl.blob), "+s"(tl.start), "+s"(tl.count), "+s"(geo.hidden), "+s"(geo.inter),
-               "+s"(geo.group), "+s"(terms));
-  if (tl.count == 0u) return;  // uniform over the workgroup
-  const uint32_t split = wk.split;
-  const uint32_t D = geo.hidden, I = geo.inter, G = geo.group;
-  const uint32_t K = PROJ == 2 ? D : I;
-  const uint32_t N = PROJ == 2 ? I : D;
-  const uint32_t ngroups = K / G;
-  const uint32_t g0 = split * GPR;
-  const osm_expert_offsets off = osm_expert_layout(geo);
-  const uint8_t* blob = tl.blob;
+// One work item's tile as a workgroup sees it: the record (count 0 for an
+// empty tile or one past the capacity) and, in lane m, the activation row of
+// tile row m.
+struct TileView {
+  const uint8_t* blob;
+  uint32_t start, count, lane_act;
+};
 
-  constexpr uint32_t kProjWaves = PROJ == 2 ? kSplitWaves / 2u : kSplitWaves;
-  const uint32_t pr = wave / kProjWaves;
-  const uint32_t rows = tl.count;
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes
+// land at dst + 16 l (dst wave-uniform).
+__device__ __forceinline__ void load_lds16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
 
-  // Activation row of tile row m: its token (gate/up, loaded above before the
-  // weights, so that waiting for it never waits for them: the counter of
-  // vector loads retires in issue order) or the pair itself (down).
-  if constexpr (PROJ == 1) lane_act = tl.start + m;
-  const uint32_t row_base = wk.row_block * kWgRows + (wave % kProjWaves) * kWaveRows;
-  const size_t q_off = PROJ == 2 ? (pr ? off.up_q : off.gate_q) : off.down_q;
-  const size_t s_off = PROJ == 2 ? (pr ? off.up_s : off.gate_s) : off.down_s;
-  const size_t b_off = PROJ == 2 ? (pr ? off.up_b : off.gate_b) : off.down_b;
+// A tile record as wave-uniform (scalar) values.
+struct TileRec {
+  const uint8_t* blob;
+  uint32_t start, count;
+};
+__device__ __forceinline__ TileRec uniform_rec(const TileView& v) {
+  return TileRec{uniform_ptr(v.blob), uniform_u32(v.start), uniform_u32(v.count)};
+}
 
-  // 1. This wave's packed words and metadata for the whole range, issued now.
+// Reads an item's tile record with vector loads: they leave the LDS counter
+// alone, so the MFMA loop's LDS waits never wait for the next item's record
+// (a scalar load would count there).
+template <int PROJ>
+__device__ __forceinline__ TileView fetch_tile(const SplitParams& p, const SplitWork& wk, uint32_t m) {
+  TileView v{nullptr, 0u, 0u, 0u};
+  if (wk.tile >= p.max_tiles) return v;
+  const uint64_t* rec = reinterpret_cast<const uint64_t*>(p.tiles + wk.tile);
+  const uint64_t r0 = __hip_atomic_load(const_cast<uint64_t*>(rec), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t r1 = __hip_atomic_load(const_cast<uint64_t*>(rec + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v.blob = reinterpret_cast<const uint8_t*>(static_cast<uintptr_t>(r0));
+  v.start = static_cast<uint32_t>(r1);
+  v.count = static_cast<uint32_t>(r1 >> 32);
+  if constexpr (PROJ == 2) v.lane_act = p.tile_rows[wk.tile * kTileTokens + m];
+  return v;
+}
+
+// One wave's weights of one row block over the K range: packed words and the
+// scale / bias runs of its 2 x 16 rows.
+template <int META, int S, int NSTEP>
+struct BlockWeights {
+  static constexpr int GPR = NSTEP / S;
   uint32_t w[2][NSTEP];
   MetaRun<META, GPR> sb[2], bb[2];
+};
+
+// Where one wave's weights live: projection offsets within a blob and the
+// geometry of the matrix (N rows of K columns).
+struct WaveMatrix {
+  size_t q_off, s_off, b_off;
+  uint32_t N, K, G, ngroups, wave_row;  // wave_row: the wave's first row within a block
+};
+
+template <int META, int S, int NSTEP, uint32_t kWgRows>
+__device__ __forceinline__ void load_block(BlockWeights<META, S, NSTEP>& W, const WaveMatrix& mx,
+                                           const uint8_t* blob, uint32_t block, uint32_t split, uint32_t m,
+                                           uint32_t q) {
+  constexpr int GPR = NSTEP / S;
+  const uint32_t g0 = split * GPR;
 #pragma unroll
   for (uint32_t nb = 0; nb < 2u; ++nb) {
-    uint32_t r = row_base + nb * kBlockRows + m;
-    r = r < N ? r : N - 1u;
-    const uint8_t* qrow = blob + q_off + static_cast<size_t>(r) * (K / 2u);
+    uint32_t r = block * kWgRows + mx.wave_row + nb * kBlockRows + m;
+    r = r < mx.N ? r : mx.N - 1u;
+    const uint8_t* qrow = blob + mx.q_off + static_cast<size_t>(r) * (mx.K / 2u);
 #pragma unroll
-    for (int gg = 0; gg < GPR; ++gg) word_run<S>(qrow + ((g0 + gg) * (G / 8u) + S * q) * 4u, &w[nb][gg * S]);
-    const size_t mi = static_cast<size_t>(r) * ngroups + g0;
-    sb[nb].load(blob + s_off, mi);
-    bb[nb].load(blob + b_off, mi);
+    for (int gg = 0; gg < GPR; ++gg) word_run<S>(qrow + ((g0 + gg) * (mx.G / 8u) + S * q) * 4u, &W.w[nb][gg * S]);
+    const size_t mi = static_cast<size_t>(r) * mx.ngroups + g0;
+    W.sb[nb].load(blob + mx.s_off, mi);
+    W.bb[nb].load(blob + mx.b_off, mi);
   }
+}
 
-  // 2. The tile's activation rows for this range into LDS: all loads first,
-  // then the stores. Unit u: term u / (16 * KS/8), tile row (u / (KS/8)) % 16,
-  // 16-byte column unit u % (KS/8).
-  auto act_row = [&](uint32_t j) -> uint32_t { return __shfl(lane_act, static_cast<int>(j)); };
-  uint4 stage[kUnitsPerThread];
-#pragma unroll
-  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
-    const uint32_t u = tid + i * kSplitThreads;
-    const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
-    const uint32_t arow = act_row(row);  // every lane active here: the shuffle reads real lanes
-    if (row < rows)
-      stage[i] = ldg16(terms + (static_cast<size_t>(arow) * kActSplit + term) * K + split * KS + cu * 8u);
-  }
-  float xsum = 0.0f;
-  const uint32_t sg = tid / kTileTokens, srow = tid % kTileTokens;
-  const uint32_t sarow = act_row(srow);
-  if (sg < GPR && srow < rows) xsum = p.sums[static_cast<size_t>(sarow) * ngroups + g0 + sg];
-#pragma unroll
-  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
-    const uint32_t u = tid + i * kSplitThreads;
-    const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
-    if (row < rows) *reinterpret_cast<uint4*>(&a_lds[term][row][cu * 8u]) = stage[i];
-  }
-  if (sg < GPR && srow < rows) xs_lds[sg][srow] = xsum;
-  __syncthreads();
+template <int PROJ, int NSTEP>
+struct SplitLds {
+  static constexpr uint32_t KS = 32u * NSTEP;
+  static constexpr uint32_t RS = KS + 8u;  // row stride (bf16), padded against bank conflicts
+  uint16_t a[kActSplit][kTileTokens][RS];
+  float xs[NSTEP][kTileTokens];  // group sums (at most NSTEP groups per range)
+};
 
-  // 3. MFMAs. MFMA row m reads tile row min(m, count - 1); the D rows of
-  // lane q are tile rows 4q .. 4q+3 (those past count are not stored).
-  const uint32_t ar = m < rows ? m : rows - 1u;
+// MFMAs of one block against the staged tile, then its partial sums. MFMA
+// row m reads tile row min(m, count - 1); the D rows of lane q are tile rows
+// 4q .. 4q+3 (those past count are not stored).
+template <int META, int PROJ, int S, int NSTEP, uint32_t kWgRows>
+__device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP>& lds,
+                                              const BlockWeights<META, S, NSTEP>& W, const WaveMatrix& mx,
+                                              uint32_t block, uint32_t split, uint32_t start, uint32_t rows,
+                                              uint32_t pr, uint32_t m, uint32_t q) {
+  constexpr int GPR = NSTEP / S;
+  constexpr uint32_t G8 = (32u * S) / 8u;  // 16-byte units per group
+  // The tile row indices pass through an opaque copy per block: every block
+  // of an item reads the same LDS operands, and left alone the compiler keeps
+  // all of them in registers across the blocks instead of re-reading them.
+  uint32_t ar = m < rows ? m : rows - 1u;
+  asm volatile("" : "+v"(ar));
   uint32_t xr[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) xr[j] = 4u * q + j < rows ? 4u * q + j : rows - 1u;
+  for (int j = 0; j < 4; ++j) {
+    xr[j] = 4u * q + j < rows ? 4u * q + j : rows - 1u;
+    asm volatile("" : "+v"(xr[j]));
+  }
   f32x4 total[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int gg = 0; gg < GPR; ++gg) {
@@ -492,41 +550,185 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(SplitParams p) {
     for (int s2 = 0; s2 < S; ++s2)
 #pragma unroll
       for (uint32_t t = 0; t < kActSplit; ++t)
-        a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][ar][(gg * (G / 8u) + S * q + s2) * 8u]));
+        a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&lds.a[t][ar][(gg * G8 + S * q + s2) * 8u]));
     float xs[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xs[j] = xs_lds[gg][xr[j]];
+    for (int j = 0; j < 4; ++j) xs[j] = lds.xs[gg][xr[j]];
 #pragma unroll
     for (uint32_t nb = 0; nb < 2u; ++nb) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s2 = 0; s2 < S; ++s2) {
-        const bf16x8 b = nibble_operand(w[nb][gg * S + s2]);
+        const bf16x8 b = nibble_operand(W.w[nb][gg * S + s2]);
 #pragma unroll
         for (uint32_t t = 0; t < kActSplit; ++t) d = mfma(a[s2][t], b, d);
       }
-      const float sc = sb[nb].get(gg);
-      const float cb = bb[nb].get(gg) - 128.0f * sc;
+      const float sc = W.sb[nb].get(gg);
+      const float cb = W.bb[nb].get(gg) - 128.0f * sc;
 #pragma unroll
       for (int j = 0; j < 4; ++j) total[nb][j] += sc * d[j] + cb * xs[j];
     }
   }
-
-  // 4. Partial sums of this range.
 #pragma unroll
   for (uint32_t nb = 0; nb < 2u; ++nb) {
-    const uint32_t r = row_base + nb * kBlockRows + m;
+    const uint32_t r = block * kWgRows + mx.wave_row + nb * kBlockRows + m;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t pj = 4u * q + j;
-      if (pj < rows && r < N) {
-        const size_t pair = tl.start + pj;
+      if (pj < rows && r < mx.N) {
+        const size_t pair = start + pj;
         if constexpr (PROJ == 2)
-          p.out[((static_cast<size_t>(split) * 2u + pr) * p.P + pair) * N + r] = total[nb][j];
+          p.out[((static_cast<size_t>(split) * 2u + pr) * p.P + pair) * mx.N + r] = total[nb][j];
         else
-          p.out[(static_cast<size_t>(split) * p.P + pair) * N + r] = p.pair_w[pair] * total[nb][j];
+          p.out[(static_cast<size_t>(split) * p.P + pair) * mx.N + r] = p.pair_w[pair] * total[nb][j];
       }
     }
+  }
+}
+
+// The workgroups are persistent: workgroup b takes items b, b + grid, ...
+// (the grid a multiple of 8, so all of them on one XCD, and their tiles in
+// ascending order). Empty tiles come last, so a workgroup stops at the first
+// one. The next item's tile record is fetched while the current one is
+// staged, and the next item's first block is in flight while the current
+// item's last block computes.
+template <int META, int PROJ, int S, int NSTEP>
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2))) void split_kernel(SplitParams p) {
+  constexpr uint32_t KS = 32u * NSTEP;
+  constexpr int GPR = NSTEP / S;  // groups per range
+  constexpr uint32_t kWgRows = split_rows<PROJ>();
+  constexpr uint32_t kUnitCols = KS / 8u;  // 16-byte units per staged row
+  constexpr uint32_t kUnitsPerThread = kActSplit * kTileTokens * kUnitCols / kSplitThreads;
+  static_assert(kActSplit * kTileTokens * kUnitCols % kSplitThreads == 0, "staging units");
+  static_assert(GPR * kTileTokens <= kSplitThreads, "group sums: one per thread");
+  constexpr uint32_t kProjWaves = PROJ == 2 ? kSplitWaves / 2u : kSplitWaves;
+  __shared__ __align__(16) SplitLds<PROJ, NSTEP> lds;
+
+  // Per-lane indices and the wave's matrix, derived from the thread index.
+  // Inside the item loop the index is re-read opaquely, so that what derives
+  // from it is recomputed per item rather than kept live (or spilled) across
+  // the loop.
+  auto wave_matrix = [&](uint32_t wave) {
+    WaveMatrix mx;
+    const osm_expert_offsets off = osm_expert_layout(p.g);
+    const uint32_t pr = wave / kProjWaves;
+    mx.K = PROJ == 2 ? p.g.hidden : p.g.inter;
+    mx.N = PROJ == 2 ? p.g.inter : p.g.hidden;
+    mx.G = p.g.group;
+    mx.ngroups = mx.K / mx.G;
+    mx.wave_row = (wave % kProjWaves) * kWaveRows;
+    mx.q_off = PROJ == 2 ? (pr ? off.up_q : off.gate_q) : off.down_q;
+    mx.s_off = PROJ == 2 ? (pr ? off.up_s : off.gate_s) : off.down_s;
+    mx.b_off = PROJ == 2 ? (pr ? off.up_b : off.gate_b) : off.down_b;
+    return mx;
+  };
+
+  uint32_t item = blockIdx.x;
+  if (item >= p.items) return;
+  SplitWork wk = split_work(p, item);
+  // The loop carries the record as scalars and only the activation row of
+  // tile row m per lane.
+  uint32_t tid0 = threadIdx.x;
+  asm volatile("" : "+v"(tid0));
+  const TileView first = fetch_tile<PROJ>(p, wk, tid0 % 16u);
+  TileRec tl = uniform_rec(first);
+  uint32_t tl_lane_act = first.lane_act;
+  // An empty first tile ends the workgroup at once (a tile past the capacity
+  // has no blob at all).
+  if (tl.count == 0u) return;
+  BlockWeights<META, S, NSTEP> W0, W1;
+  // The first item's first block.
+  load_block<META, S, NSTEP, kWgRows>(W0, wave_matrix(uniform_u32(tid0 / kWave)), tl.blob, wk.first_block, wk.split,
+                                      tid0 % 16u, tid0 % kWave / 16u);
+  while (tl.count != 0u) {
+    uint32_t tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const uint32_t lane = tid % kWave, wave = uniform_u32(tid / kWave);
+    const uint32_t m = lane % 16u, q = lane / 16u;
+    const uint32_t pr = wave / kProjWaves;
+    const WaveMatrix mx = wave_matrix(wave);
+    const uint8_t* blob = tl.blob;
+    const uint32_t start = tl.start;
+    const uint32_t rows = tl.count;
+    const uint32_t split = wk.split, fb = wk.first_block;
+    // Activation row of tile row m: its token (gate/up) or the pair itself (down).
+    const uint32_t lane_act = PROJ == 2 ? tl_lane_act : start + m;
+
+    // The tile's activation rows for this range, then the next item's record.
+    // Unit u: term u / (16 * KS/8), tile row (u / (KS/8)) % 16, 16-byte
+    // column unit u % (KS/8). With 512-column ranges a wave instruction
+    // covers exactly one staged row, and the loads write LDS directly (lane
+    // l's 16 bytes land at the row start + 16 l): no registers hold the tile,
+    // and rows past the tile's count are skipped by a wave-uniform branch
+    // (their LDS rows keep stale data that no MFMA row reads). Narrower
+    // ranges go through registers, where rows past the count load the last
+    // real row (no branch around the loads).
+    auto act_row = [&](uint32_t j) -> uint32_t { return __shfl(lane_act, static_cast<int>(j)); };
+    constexpr bool kDirect = kUnitCols == kWave;
+    uint4 stage[kDirect ? 1u : kUnitsPerThread];
+#pragma unroll
+    for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+      const uint32_t u = tid + i * kSplitThreads;
+      const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+      const uint32_t arow = act_row(row < rows ? row : rows - 1u);
+      const uint16_t* src = p.terms + (static_cast<size_t>(arow) * kActSplit + term) * mx.K + split * KS + cu * 8u;
+      if constexpr (kDirect) {
+        if (uniform_u32(row) < rows) load_lds16(src, &lds.a[term][row][0]);  // term, row: wave-uniform
+      } else {
+        stage[i] = ldg16(src);
+      }
+    }
+    // Group sums: thread (sg, srow) for sg < GPR; the others load a valid
+    // element and do not store it.
+    const uint32_t sg = tid / kTileTokens, srow = tid % kTileTokens;
+    const uint32_t sarow = act_row(srow < rows ? srow : rows - 1u);
+    const float xsum = p.sums[static_cast<size_t>(sarow) * mx.ngroups + split * GPR + (sg < GPR ? sg : 0u)];
+
+    const uint32_t next = item + gridDim.x;
+    const SplitWork wk_next = split_work(p, next);
+    const TileView tl_next = next < p.items ? fetch_tile<PROJ>(p, wk_next, m) : TileView{nullptr, 0u, 0u, 0u};
+
+    if constexpr (kDirect) {
+      // Every wave's direct loads have landed before the barrier (the other
+      // waves read them).
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+        const uint32_t u = tid + i * kSplitThreads;
+        const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+        *reinterpret_cast<uint4*>(&lds.a[term][row][cu * 8u]) = stage[i];
+      }
+    }
+    if (sg < GPR) lds.xs[sg][srow] = xsum;
+    __syncthreads();
+
+    // The item's blocks, straight-line, so that each wait is for exactly the
+    // block about to be computed. The next record has arrived by the end of
+    // the first block (its wait covers every older load) and turns into
+    // scalars there. After the last block W0 loads the next item's first
+    // block, or (no next item) this item's first block again, read and not
+    // used.
+    TileRec next_rec{blob, 0u, 0u};
+#pragma unroll
+    for (uint32_t bi = 0; bi < kItemBlocks; bi += 2u) {
+      load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, fb + bi + 1u, split, m, q);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_block<META, PROJ, S, NSTEP, kWgRows>(p, lds, W0, mx, fb + bi, split, start, rows, pr, m, q);
+      if (bi == 0u) next_rec = uniform_rec(tl_next);
+      const bool last = bi + 2u >= kItemBlocks;
+      const bool has_next = next_rec.count != 0u;
+      load_block<META, S, NSTEP, kWgRows>(W0, mx, last && has_next ? next_rec.blob : blob,
+                                          last ? (has_next ? wk_next.first_block : fb) : fb + bi + 2u,
+                                          last && has_next ? wk_next.split : split, m, q);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_block<META, PROJ, S, NSTEP, kWgRows>(p, lds, W1, mx, fb + bi + 1u, split, start, rows, pr, m, q);
+    }
+    __syncthreads();  // the LDS tile is restaged by the next item
+    item = next;
+    wk = wk_next;
+    tl = next_rec;
+    tl_lane_act = tl_next.lane_act;
   }
 }
 
@@ -606,32 +808,81 @@ __global__ void combine_kernel(const float* __restrict__ partial, uint32_t nspli
 }
 
 // Columns per K range: the largest of 512 / 256 / 128 that divides K.
-uint32_t range_cols(uint32_t K) { return K % 512u == 0 ? 512u : (K % 256u == 0 ? 256u : 128u); }
+// Columns per K range: the widest of 512 / 256 / 128 that divides K and
+// keeps one row's scale (or bias) run for the range within 16 bytes, so that
+// a wave's two blocks of weights in flight fit its registers (512 columns
+// for bf16 / f16 metadata at group 64, or any metadata at group 128).
+uint32_t range_cols(const osm_expert_geometry& g, uint32_t K) {
+  const uint32_t meta_bytes = g.meta_dtype == OSM_META_F32 ? 4u : 2u;
+  for (uint32_t r = 512u; r > 128u; r /= 2u)
+    if (K % r == 0u && r / g.group * meta_bytes <= 16u) return r;
+  return 128u;
+}
+
+void set_item_blocks(SplitParams& sp, uint32_t row_blocks, uint32_t nsplit) {
+  sp.nsplit = nsplit;
+  sp.item_blocks = kItemBlocks;
+  sp.chunks = (row_blocks + kItemBlocks - 1u) / kItemBlocks;
+  sp.items = split_items(sp.max_tiles, nsplit, sp.chunks);
+}
+
+// Workgroups of a persistent split kernel: as many as are resident at once
+// (the instantiation's workgroups per compute unit times the compute units),
+// a multiple of 8, and no more than there are items (also a multiple of 8).
+// A larger grid would leave workgroups waiting for a free slot, to start
+// their whole item list after the others end.
+template <int META, int PROJ, int S, int NSTEP>
+uint32_t split_grid(uint32_t items) {
+  static const uint32_t per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP>, kSplitThreads, 0) !=
+            hipSuccess ||
+        n < 1)
+      n = 1;
+    return static_cast<uint32_t>(n);
+  }();
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 1;
+  uint32_t grid = per_cu * static_cast<uint32_t>(cus) / kXcds * kXcds;
+  if (grid < kXcds) grid = kXcds;
+  return items < grid ? items : grid;
+}
+
+template <int META, int PROJ, int S, int NSTEP>
+void launch_split_r(const SplitParams& sp, hipStream_t st) {
+  // Only the ranges range_cols() can choose for this metadata and group are
+  // instantiated (a wider one would not fit the registers).
+  constexpr uint32_t kMetaBytes = META == OSM_META_F32 ? 4u : 2u;
+  if constexpr (NSTEP / S * kMetaBytes <= 16u)
+    split_kernel<META, PROJ, S, NSTEP><<<split_grid<META, PROJ, S, NSTEP>(sp.items), kSplitThreads, 0, st>>>(sp);
+}
 
 template <int META, int PROJ, int S>
-void launch_split_s(const SplitParams& sp, dim3 grid, hipStream_t st) {
-  switch (range_cols(PROJ == 2 ? sp.g.hidden : sp.g.inter)) {
-    case 512: split_kernel<META, PROJ, S, 16><<<grid, kSplitThreads, 0, st>>>(sp); break;
-    case 256: split_kernel<META, PROJ, S, 8><<<grid, kSplitThreads, 0, st>>>(sp); break;
-    default: split_kernel<META, PROJ, S, 4><<<grid, kSplitThreads, 0, st>>>(sp); break;
+void launch_split_s(const SplitParams& sp, hipStream_t st) {
+  switch (range_cols(sp.g, PROJ == 2 ? sp.g.hidden : sp.g.inter)) {
+    case 512: launch_split_r<META, PROJ, S, 16>(sp, st); break;
+    case 256: launch_split_r<META, PROJ, S, 8>(sp, st); break;
+    default: launch_split_r<META, PROJ, S, 4>(sp, st); break;
   }
 }
 
 template <int META, int PROJ>
-void launch_split_meta(const SplitParams& sp, dim3 grid, hipStream_t st) {
+void launch_split_meta(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.group) {
-    case 32: launch_split_s<META, PROJ, 1>(sp, grid, st); break;
-    case 64: launch_split_s<META, PROJ, 2>(sp, grid, st); break;
-    default: launch_split_s<META, PROJ, 4>(sp, grid, st); break;
+    case 32: launch_split_s<META, PROJ, 1>(sp, st); break;
+    case 64: launch_split_s<META, PROJ, 2>(sp, st); break;
+    default: launch_split_s<META, PROJ, 4>(sp, st); break;
   }
 }
 
 template <int PROJ>
-void launch_split(const SplitParams& sp, dim3 grid, hipStream_t st) {
+void launch_split(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.meta_dtype) {
-    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ>(sp, grid, st); break;
-    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ>(sp, grid, st); break;
-    default: launch_split_meta<OSM_META_BF16, PROJ>(sp, grid, st); break;
+    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ>(sp, st); break;
+    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ>(sp, st); break;
+    default: launch_split_meta<OSM_META_BF16, PROJ>(sp, st); break;
   }
 }
 
@@ -651,7 +902,7 @@ size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t expe
   return (buckets < pairs ? buckets : pairs) + pairs / kTileTokens + 1u;
 }
 
-uint32_t osmd_moe_grouped_splits(uint32_t cols) { return cols / range_cols(cols); }
+uint32_t osmd_moe_grouped_splits(const osm_expert_geometry* g, uint32_t cols) { return cols / range_cols(*g, cols); }
 
 int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   const hipStream_t st = static_cast<hipStream_t>(s);
@@ -722,20 +973,18 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   sp.P = P;
   sp.max_tiles = static_cast<uint32_t>(max_tiles);
   sp.out = a->gu_part;
-  const uint32_t gu_splits = osmd_moe_grouped_splits(D);
-  sp.row_blocks = (I + split_rows<2>() - 1) / split_rows<2>();
-  sp.nsplit = gu_splits;
-  launch_split<2>(sp, dim3(split_grid(sp.max_tiles, sp.row_blocks, sp.nsplit)), st);
+  const uint32_t gu_splits = osmd_moe_grouped_splits(&g, D);
+  set_item_blocks(sp, (I + split_rows<2>() - 1) / split_rows<2>(), gu_splits);
+  launch_split<2>(sp, st);
   const size_t hwords = static_cast<size_t>(P) * (I / 8u);
   swiglu_terms_kernel<<<blocks_for(hwords, 4096), 256, 0, st>>>(a->gu_part, gu_splits, P, I, G, a->h_terms,
                                                                 a->h_sums);
   sp.terms = a->h_terms;
   sp.sums = a->h_sums;
   sp.out = a->partial;
-  const uint32_t dn_splits = osmd_moe_grouped_splits(I);
-  sp.row_blocks = (D + split_rows<1>() - 1) / split_rows<1>();
-  sp.nsplit = dn_splits;
-  launch_split<1>(sp, dim3(split_grid(sp.max_tiles, sp.row_blocks, sp.nsplit)), st);
+  const uint32_t dn_splits = osmd_moe_grouped_splits(&g, I);
+  set_item_blocks(sp, (D + split_rows<1>() - 1) / split_rows<1>(), dn_splits);
+  launch_split<1>(sp, st);
   combine_kernel<<<blocks_for(static_cast<size_t>(T) * D, 4096), 256, 0, st>>>(
       a->partial, dn_splits, P, a->pair_pos, T, D, nslot,
       (m.flags & OSMD_MOE_RESIDUAL) ? static_cast<const float*>(m.x) : nullptr, m.y);

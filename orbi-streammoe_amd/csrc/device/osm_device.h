@@ -188,7 +188,8 @@ int osmd_moe_select(const osmd_moe_args* a, osmd_stream s);
  *   gu_part  f32 [splits(D)][2][P][I]
  *   h_terms  bf16 [P][2][I]    h_sums   f32 [P][I/G]
  *   partial  f32 [splits(I)][P][D]
- * where splits(n) = osmd_moe_grouped_splits(n) K ranges of n columns.
+ * where splits(n) = osmd_moe_grouped_splits(&moe.geom, n) K ranges of the
+ * n columns (hidden for gate/up, inter for down).
  * plus the decode workspace of moe (logits, ids, weights, mass, shared_gate,
  * x_norm). */
 typedef struct osmd_moe_grouped_args {
@@ -206,7 +207,7 @@ typedef struct osmd_moe_grouped_args {
   float* partial;
 } osmd_moe_grouped_args;
 size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t experts);
-uint32_t osmd_moe_grouped_splits(uint32_t cols);
+uint32_t osmd_moe_grouped_splits(const osm_expert_geometry* g, uint32_t cols);
 int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s);
 
 /* Bytes of LDS the down kernel stages for `nslot` slots of width `inter`

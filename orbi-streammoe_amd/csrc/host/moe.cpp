@@ -54,10 +54,10 @@ struct HipMoeLayer::Impl {
     if (rc == 0) rc = g_pair_w.allocate(P * 4U);
     if (rc == 0) rc = g_tiles.allocate(tiles * 80U);
     if (rc == 0) rc = g_tile_count.allocate(4U);
-    if (rc == 0) rc = g_gu_part.allocate(osmd_moe_grouped_splits(static_cast<std::uint32_t>(D)) * 2U * P * I * 4U);
+    if (rc == 0) rc = g_gu_part.allocate(osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(D)) * 2U * P * I * 4U);
     if (rc == 0) rc = g_h_terms.allocate(P * 2U * I * 2U);
     if (rc == 0) rc = g_h_sums.allocate(P * (I / G) * 4U);
-    if (rc == 0) rc = g_partial.allocate(osmd_moe_grouped_splits(static_cast<std::uint32_t>(I)) * P * D * 4U);
+    if (rc == 0) rc = g_partial.allocate(osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(I)) * P * D * 4U);
     if (rc == 0) rc = osmd_zero(g_tile_count.get(), 4U, st);
     if (rc == 0) grouped_ready = true;
     return rc;

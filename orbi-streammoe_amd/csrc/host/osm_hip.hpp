@@ -617,13 +617,13 @@ struct HipMoeResult {
 // workgroups hand data to each other; same bits, measured slower than the
 // three kernels at the Qwen3-Next shape, so only taken when asked for).
 // automatic takes the per-token kernels, and the grouped path from
-// kGroupedMinTokens tokens on, where it was measured to overtake the
-// per-token kernels at the Qwen3-Next shape on MI355X (us per layer,
-// per-token vs grouped: 24 tokens 156 vs 162; 32: 198 vs 189; 64: 369 vs
-// 280; 512: 2730 vs 477). single_launch with more than one token runs the
-// per-token kernels.
+// kGroupedMinTokens tokens on, between the batch sizes where it was
+// measured to overtake the per-token kernels at the Qwen3-Next shape on
+// MI355X (us per layer, per-token vs grouped: 32 tokens 166 vs 183; 48: 239
+// vs 227; 64: 304 vs 258; 512: 2730 vs 454). single_launch with more than
+// one token runs the per-token kernels.
 enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2, single_launch = 3 };
-inline constexpr std::uint32_t kGroupedMinTokens = 32;
+inline constexpr std::uint32_t kGroupedMinTokens = 40;
 
 class HipMoeLayer {
  public:
