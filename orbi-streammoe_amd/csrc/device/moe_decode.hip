@@ -416,13 +416,20 @@ __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
 }
 
 // ---------------------------------------------------------------------------
-// gate/up + SwiGLU. Each wavefront owns kGuRowsPerWave consecutive rows of one
+// gate/up + SwiGLU. Each wavefront owns ROWS consecutive rows of one
 // slot; lane l reads 16-byte chunks l, l+64, ... of each row, so a wavefront
 // load is 1 KB of contiguous packed weights. The lane's slice of x (and its
 // sum) stays in registers for all rows. PER > 0: routed slots select their
 // expert from the logits first (PER = experts per lane of the selection).
+// One token takes three rows per wavefront (12 per workgroup, 43 workgroups
+// per slot at intermediate 512): more workgroups share the VALU-bound dot
+// products that follow the weight loads (batch-1 µs per token-layer for
+// 8 / 6 / 4 / 3 / 2 rows: 20.95 / 20.66 / 20.52 / 20.33 / 20.76). Several
+// tokens take eight: every workgroup repeats the selection of its token, and
+// at 4 and 16 tokens three rows measured 14% and 20% slower than eight.
 constexpr int kGuWaves = 4;
-constexpr int kGuRowsPerWave = 8;
+constexpr int kGuRowsOneToken = 3;
+constexpr int kGuRowsBatched = 8;
 
 // Lane's slices of x (chunks lane, lane+64, ... of 32 floats). Lanes past the
 // row end (hidden < 64*32*CPL) read chunk nch-1 again and zero their slice,
@@ -449,7 +456,7 @@ __device__ __forceinline__ void load_xr(const float* x, uint32_t nch, uint32_t l
 // Gate and up rows blk*16 .. blk*16+15 of slot j of token t from `blob`,
 // SwiGLU'd into h[t, j, row].
 // store(index, value): h[t, j, row] at index (t * nslot + j) * I + row.
-template <int META, int CPL, typename Store>
+template <int META, int CPL, int ROWS, typename Store>
 __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, uint32_t j, uint32_t blk,
                                              const uint8_t* blob, const float (&xr)[CPL][32], Store&& store) {
   const uint32_t lane = threadIdx.x % kWave;
@@ -466,12 +473,12 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
     for (int v = 0; v < 32; ++v) xsum[ci] += xr[ci][v];
   }
 
-  const uint32_t r0 = (blk * kGuWaves + wave) * kGuRowsPerWave;
-  uint4 qg[kGuRowsPerWave][CPL], qu[kGuRowsPerWave][CPL];
-  uint32_t sg[kGuRowsPerWave][CPL], bg[kGuRowsPerWave][CPL];
-  uint32_t su[kGuRowsPerWave][CPL], bu[kGuRowsPerWave][CPL];
+  const uint32_t r0 = (blk * kGuWaves + wave) * ROWS;
+  uint4 qg[ROWS][CPL], qu[ROWS][CPL];
+  uint32_t sg[ROWS][CPL], bg[ROWS][CPL];
+  uint32_t su[ROWS][CPL], bu[ROWS][CPL];
 #pragma unroll
-  for (int i = 0; i < kGuRowsPerWave; ++i) {
+  for (int i = 0; i < ROWS; ++i) {
     const uint32_t r = (r0 + i < I) ? r0 + i : I - 1u;
 #pragma unroll
     for (int ci = 0; ci < CPL; ++ci) {
@@ -488,7 +495,7 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
     }
   }
 #pragma unroll
-  for (int i = 0; i < kGuRowsPerWave; ++i) {
+  for (int i = 0; i < ROWS; ++i) {
     float ga = 0.0f, ua = 0.0f;
 #pragma unroll
     for (int ci = 0; ci < CPL; ++ci) {
@@ -504,7 +511,7 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
   }
 }
 
-template <int META, int CPL, int PER>
+template <int META, int CPL, int PER, int ROWS>
 __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = threadIdx.x / kWave;
@@ -531,7 +538,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
     blob = p.src.blob(t, j);
   }
   if (blob == nullptr) blob = p.rv.fallback;  // never dereference a null slot
-  gate_up_rows<META, CPL>(p, t, j, blockIdx.x, blob, xr, [&](size_t i, float v) { p.h[i] = v; });
+  gate_up_rows<META, CPL, ROWS>(p, t, j, blockIdx.x, blob, xr, [&](size_t i, float v) { p.h[i] = v; });
 }
 
 // ---------------------------------------------------------------------------
@@ -1031,7 +1038,8 @@ __global__ __launch_bounds__(256) void fused_decode_kernel(FusedParams f) {
     }
     if (blob == nullptr) blob = f.a.fallback_blob;
     stamp(mark, 2);
-    gate_up_rows<META, 1>(f.gp, 0u, j, blk, blob, xr, [&](size_t i, float v) { store_tagged(th + i, e, v); });
+    gate_up_rows<META, 1, kGuRowsOneToken>(f.gp, 0u, j, blk, blob, xr,
+                                           [&](size_t i, float v) { store_tagged(th + i, e, v); });
     stamp(mark, 3);
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this wavefront's h stores are complete
     __syncthreads();
@@ -1053,12 +1061,22 @@ int pow2_at_least(uint32_t v) {
 
 template <int META, int CPL>
 int launch_gate_up_cpl(const GateUpParams& gp, uint32_t tokens, int per, hipStream_t st) {
-  const uint32_t rows_per_block = kGuWaves * kGuRowsPerWave;
+  const bool one = tokens == 1u;
+  const uint32_t rows_per_block = kGuWaves * (one ? kGuRowsOneToken : kGuRowsBatched);
   const dim3 grid((gp.g.inter + rows_per_block - 1) / rows_per_block, gp.src.nslot, tokens);
   switch (per) {
-    case 0: gate_up_kernel<META, CPL, 0><<<grid, 256, 0, st>>>(gp); break;
-    case 2: gate_up_kernel<META, CPL, 2><<<grid, 256, 0, st>>>(gp); break;
-    default: gate_up_kernel<META, CPL, 4><<<grid, 256, 0, st>>>(gp); break;
+    case 0:
+      if (one) gate_up_kernel<META, CPL, 0, kGuRowsOneToken><<<grid, 256, 0, st>>>(gp);
+      else gate_up_kernel<META, CPL, 0, kGuRowsBatched><<<grid, 256, 0, st>>>(gp);
+      break;
+    case 2:
+      if (one) gate_up_kernel<META, CPL, 2, kGuRowsOneToken><<<grid, 256, 0, st>>>(gp);
+      else gate_up_kernel<META, CPL, 2, kGuRowsBatched><<<grid, 256, 0, st>>>(gp);
+      break;
+    default:
+      if (one) gate_up_kernel<META, CPL, 4, kGuRowsOneToken><<<grid, 256, 0, st>>>(gp);
+      else gate_up_kernel<META, CPL, 4, kGuRowsBatched><<<grid, 256, 0, st>>>(gp);
+      break;
   }
   return launch_status();
 }
@@ -1173,7 +1191,7 @@ FusedShape fused_shape(const osmd_moe_args& a) {
   const uint32_t nslot = a.top_k + shared;
   const uint32_t D = a.geom.hidden, I = a.geom.inter;
   f.nr = (a.expert_count + shared + kRouteWaves - 1) / kRouteWaves;
-  const uint32_t gu_rows = kGuWaves * kGuRowsPerWave;
+  const uint32_t gu_rows = kGuWaves * kGuRowsOneToken;
   f.bps = (I + gu_rows - 1) / gu_rows;
   f.ngu = nslot * f.bps;
   f.lpr = static_cast<uint32_t>(pow2_at_least(I / 32u));
