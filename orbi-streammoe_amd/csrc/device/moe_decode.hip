@@ -47,6 +47,10 @@ struct SlotSource {
 // What a routed wavefront needs to select its expert from the logits.
 struct RouteView {
   const float* logits;                // [B, E]
+  const float* planes;                // null, or `parts` planes [B][E + 1] of partial sums
+  uint32_t parts, tokens;
+  float* logits_out;                  // [B, E]  with planes: the summed logits
+  float* gate_out;                    // [B]     with planes: the shared gate
   uint32_t expert_count, top_k, norm_topk_prob, has_shared;
   const uint8_t* const* expert_table;  // [E] or null (picks read `fallback`)
   const uint8_t* shared_expert;
@@ -229,8 +233,25 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint32_t e = (base + j < E) ? base + j : E - 1u;  // clamped: every load in bounds
-    p[j] = lg[e];
+    if (rv.planes != nullptr) {
+      // Partial sums of the router GEMM's K ranges, added in plane order.
+      const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
+      const float* pl = rv.planes + static_cast<size_t>(t) * (E + 1u) + e;
+      float v = pl[0];
+      for (uint32_t part = 1; part < rv.parts; ++part) v += pl[part * ps];
+      p[j] = v;
+      if (base + j < E) rv.logits_out[static_cast<size_t>(t) * E + e] = v;
+    } else {
+      p[j] = lg[e];
+    }
     tab[j] = rv.expert_table ? rv.expert_table[e] : nullptr;
+  }
+  if (rv.planes != nullptr && rv.has_shared && threadIdx.x == 0) {
+    const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
+    const float* pl = rv.planes + static_cast<size_t>(t) * (E + 1u) + E;
+    float g = pl[0];
+    for (uint32_t part = 1; part < rv.parts; ++part) g += pl[part * ps];
+    rv.gate_out[t] = 1.0f / (1.0f + expf(-g));  // reference_ops.cpp:214-216
   }
   select_values<PER>(rv, p, tab, out);
 }
@@ -514,7 +535,6 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
 template <int META, int CPL, int PER, int ROWS>
 __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = threadIdx.x / kWave;
   const uint32_t t = blockIdx.z;
   const uint32_t j = blockIdx.y;
   const uint32_t D = p.g.hidden;
@@ -1156,6 +1176,11 @@ int launch_route_rd(const osmd_moe_args& a, hipStream_t st) {
 RouteView route_view(const osmd_moe_args& a) {
   RouteView rv;
   rv.logits = a.logits;
+  rv.planes = a.logit_planes;
+  rv.parts = a.logit_parts;
+  rv.tokens = a.tokens;
+  rv.logits_out = a.logits;
+  rv.gate_out = a.shared_gate;
   rv.expert_count = a.expert_count;
   rv.top_k = a.top_k;
   rv.norm_topk_prob = a.norm_topk_prob;

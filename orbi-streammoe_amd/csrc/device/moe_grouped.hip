@@ -143,69 +143,85 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
 }
 
 // ---------------------------------------------------------------------------
-// Router GEMM: logits [T, E] and, as row E, the shared gate sigmoid(w_sg . x).
-// Workgroup = 16 tokens x 4 waves x 16 router rows (bf16).
-template <int NS>
+// Router GEMM: partial logits [T, E] and, as column E, the shared-gate dot
+// w_sg . x, one plane per K range (the selection adds the planes in order
+// and applies the sigmoid). A workgroup is 16 tokens x 64 router rows (4
+// waves x 16, bf16) x one K range of R = 32 * NSTEP columns. The tile's
+// activation terms are staged in LDS once and read by all four waves; each
+// wave's router values for the range are loaded before the staging, so both
+// streams are in flight together. Splitting K keeps a workgroup's reads small
+// (48 KB of terms, 64 KB of router rows at R = 512) and the grid large; a
+// wave that read its own copy of the terms, over all of K, moved 4x more
+// bytes through L2 than the tile holds.
+template <int NS, int NSTEP>
 __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
     const uint16_t* __restrict__ terms, uint32_t T, uint32_t D, const uint16_t* __restrict__ router,
-    const uint16_t* __restrict__ shared_gate_vec, uint32_t E, float* __restrict__ logits,
-    float* __restrict__ shared_gate) {
-  const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const uint32_t t0 = blockIdx.y * kTileTokens;
+    const uint16_t* __restrict__ shared_gate_vec, uint32_t E, float* __restrict__ planes) {
+  constexpr uint32_t R = 32u * NSTEP;
+  constexpr uint32_t RS = R + 8u;  // LDS row stride (bf16), padded against bank conflicts
+  constexpr uint32_t kUnitCols = R / 8u;
+  constexpr uint32_t kUnitsPerThread = NS * kTileTokens * kUnitCols / kGroupedThreads;
+  static_assert(NS * kTileTokens * kUnitCols % kGroupedThreads == 0, "staging units");
+  __shared__ __align__(16) uint16_t a_lds[NS][kTileTokens][RS];
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const uint32_t t0 = blockIdx.y * kTileTokens, k0 = blockIdx.z * R;
   const uint32_t nrows = E + (shared_gate_vec ? 1u : 0u);
   const uint32_t m = lane % 16u, q = lane / 16u;
   const uint32_t row = (blockIdx.x * kGroupedWaves + wave) * kBlockRows + m;
   const uint32_t rr = row < nrows ? row : nrows - 1u;
-  const uint16_t* wrow = rr < E ? router + static_cast<size_t>(rr) * D : shared_gate_vec;
-  const uint32_t tok = (t0 + m < T) ? t0 + m : T - 1u;
-  const uint16_t* arow = terms + static_cast<size_t>(tok) * NS * D;
+  const uint16_t* wrow = (rr < E ? router + static_cast<size_t>(rr) * D : shared_gate_vec) + k0;
+
+  // 1. B: this wave's router values for the range; then the tile's terms
+  // (unit u: term u / (16 * R/8), token row (u / (R/8)) % 16, 16-byte column
+  // unit u % (R/8); rows past T load the last token).
+  uint4 raw[NSTEP];
+#pragma unroll
+  for (int st = 0; st < NSTEP; ++st) raw[st] = ldg16(wrow + 32u * st + 8u * q);
+  uint4 stage[kUnitsPerThread];
+#pragma unroll
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+    const uint32_t u = tid + i * kGroupedThreads;
+    const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+    const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
+    stage[i] = ldg16(terms + (static_cast<size_t>(tok) * NS + term) * D + k0 + cu * 8u);
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+    const uint32_t u = tid + i * kGroupedThreads;
+    const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+    *reinterpret_cast<uint4*>(&a_lds[term][r][cu * 8u]) = stage[i];
+  }
+  __syncthreads();
+
+  // 2. MFMAs: A = token m's terms at k0 + 32 st + 8q (word order), B = 8
+  // router values of row rr reordered to word order.
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  // C steps of 32 columns per memory round trip: every load of the chunk is
-  // issued before its MFMAs (one step per trip would make the 2048-column
-  // loop 64 round trips long).
-  auto chunk = [&](uint32_t k0, auto steps) {
-    constexpr int C = decltype(steps)::value;
-    uint4 raw[C], av[C][NS];
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const uint32_t k = k0 + 32u * c + 8u * q;
-      raw[c] = ldg16(wrow + k);
+  for (int st = 0; st < NSTEP; ++st) {
+    const uint32_t h4[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
+    uint16_t h[8];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) av[c][s] = ldg16(arow + static_cast<size_t>(s) * D + k);
+    for (int j = 0; j < 4; ++j) {
+      h[2 * j] = static_cast<uint16_t>(h4[j] & 0xFFFFu);
+      h[2 * j + 1] = static_cast<uint16_t>(h4[j] >> 16);
     }
-    __builtin_amdgcn_sched_barrier(0);  // keeps every load of the chunk ahead of its MFMAs
+    uint4 bv;
+    bv.x = h[word_k(0)] | (static_cast<uint32_t>(h[word_k(1)]) << 16);
+    bv.y = h[word_k(2)] | (static_cast<uint32_t>(h[word_k(3)]) << 16);
+    bv.z = h[word_k(4)] | (static_cast<uint32_t>(h[word_k(5)]) << 16);
+    bv.w = h[word_k(6)] | (static_cast<uint32_t>(h[word_k(7)]) << 16);
+    const bf16x8 b = as_operand(bv);
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      // B: 8 router values of row rr at k0 + 32c + 8q, reordered to word order.
-      const uint32_t h4[4] = {raw[c].x, raw[c].y, raw[c].z, raw[c].w};
-      uint16_t h[8];
+    for (int t = 0; t < NS; ++t)
+      acc = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * st + 8u * q])), b, acc);
+  }
+
+  // 3. Plane blockIdx.z, [T][E + 1] (column E: the shared gate, when there is
+  // one): D rows 4q + j are tokens, column m the router row.
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        h[2 * j] = static_cast<uint16_t>(h4[j] & 0xFFFFu);
-        h[2 * j + 1] = static_cast<uint16_t>(h4[j] >> 16);
-      }
-      uint4 bv;
-      bv.x = h[word_k(0)] | (static_cast<uint32_t>(h[word_k(1)]) << 16);
-      bv.y = h[word_k(2)] | (static_cast<uint32_t>(h[word_k(3)]) << 16);
-      bv.z = h[word_k(4)] | (static_cast<uint32_t>(h[word_k(5)]) << 16);
-      bv.w = h[word_k(6)] | (static_cast<uint32_t>(h[word_k(7)]) << 16);
-      const bf16x8 b = as_operand(bv);
-#pragma unroll
-      for (int s = 0; s < NS; ++s) acc = mfma(as_operand(av[c][s]), b, acc);
-    }
-  };
-  uint32_t k0 = 0;
-  for (; k0 + 256u <= D; k0 += 256u) chunk(k0, std::integral_constant<int, 8>{});
-  if (k0 < D) chunk(k0, std::integral_constant<int, 4>{});  // D is a multiple of 128
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {  // D rows 4q + j are tokens, column m the router row
+  for (int j = 0; j < 4; ++j) {
     const uint32_t t = t0 + 4u * q + j;
-    if (t < T && row < nrows) {
-      if (row < E)
-        logits[static_cast<size_t>(t) * E + row] = acc[j];
-      else
-        shared_gate[t] = 1.0f / (1.0f + expf(-acc[j]));  // reference_ops.cpp:214-216
-    }
+    if (t < T && row < nrows) planes[(static_cast<size_t>(blockIdx.z) * T + t) * (E + 1u) + row] = acc[j];
   }
 }
 
@@ -808,6 +824,10 @@ __global__ void combine_kernel(const float* __restrict__ partial, uint32_t nspli
 }
 
 // Columns per K range: the largest of 512 / 256 / 128 that divides K.
+// Columns per K range of the router GEMM: the widest of 512 / 256 / 128 that
+// divides the hidden size (a multiple of 128 on the grouped path).
+uint32_t router_range(uint32_t D) { return D % 512u == 0 ? 512u : (D % 256u == 0 ? 256u : 128u); }
+
 // Columns per K range: the widest of 512 / 256 / 128 that divides K and
 // keeps one row's scale (or bias) run for the range within 16 bytes, so that
 // a wave's two blocks of weights in flight fit its registers (512 columns
@@ -904,6 +924,8 @@ size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t expe
 
 uint32_t osmd_moe_grouped_splits(const osm_expert_geometry* g, uint32_t cols) { return cols / range_cols(*g, cols); }
 
+uint32_t osmd_moe_grouped_router_parts(uint32_t hidden) { return hidden / router_range(hidden); }
+
 int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   const hipStream_t st = static_cast<hipStream_t>(s);
   const osmd_moe_args& m = a->moe;
@@ -927,19 +949,36 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   const size_t groups = static_cast<size_t>(T) * (D / G);
   int r = 0;
   // Up to 64 tokens the per-token router kernel (one wavefront per router
-  // row and token) has the shorter latency; beyond, the MFMA router GEMM.
+  // row and token) has the shorter latency; beyond, the MFMA router GEMM,
+  // whose K-range planes the selection adds.
+  osmd_moe_args ms = m;
   if (m.router_dtype == OSM_META_BF16 && (xbf16 || T > kRouterGemmMinTokens)) {
     if (xbf16)
       prepare_kernel<true, kRouterSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
     else
       prepare_kernel<false, kRouterSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
     const uint32_t nrows = m.expert_count + has_shared;
-    router_gemm_kernel<kRouterSplit><<<dim3((nrows + kGroupedWaves * kBlockRows - 1) / (kGroupedWaves * kBlockRows),
-                                            (T + kTileTokens - 1) / kTileTokens),
-                                       kGroupedThreads, 0, st>>>(
-        a->x_terms, T, D, static_cast<const uint16_t*>(m.router),
-        has_shared ? static_cast<const uint16_t*>(m.shared_gate_vec) : nullptr, m.expert_count, m.logits,
-        m.shared_gate);
+    const uint32_t rcols = router_range(D);
+    const dim3 grid((nrows + kGroupedWaves * kBlockRows - 1) / (kGroupedWaves * kBlockRows),
+                    (T + kTileTokens - 1) / kTileTokens, D / rcols);
+    const uint16_t* router = static_cast<const uint16_t*>(m.router);
+    const uint16_t* sgv = has_shared ? static_cast<const uint16_t*>(m.shared_gate_vec) : nullptr;
+    switch (rcols) {
+      case 512:
+        router_gemm_kernel<kRouterSplit, 16><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
+                                                                              m.expert_count, a->logit_planes);
+        break;
+      case 256:
+        router_gemm_kernel<kRouterSplit, 8><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
+                                                                             m.expert_count, a->logit_planes);
+        break;
+      default:
+        router_gemm_kernel<kRouterSplit, 4><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
+                                                                             m.expert_count, a->logit_planes);
+        break;
+    }
+    ms.logit_planes = a->logit_planes;
+    ms.logit_parts = D / rcols;
   } else {
     // The decode router kernel, one token per grid row (fp32 input).
     osmd_moe_args ra = m;
@@ -949,7 +988,7 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     r = osmd_moe_router(&ra, s);
     if (r != 0) return r;
   }
-  r = osmd_moe_select(&m, s);
+  r = osmd_moe_select(&ms, s);
   if (r != 0) return r;
   bucket_kernel<<<1, kBucketThreads, 0, st>>>(m.ids, m.weights, has_shared ? m.shared_gate : nullptr, T, m.top_k,
                                               nslot, m.expert_count, m.expert_table, m.shared_expert,

@@ -130,6 +130,12 @@ typedef struct osmd_moe_args {
   float* x_norm;      /* [B, D]   scratch/out */
   float* h;           /* [B, k+1, I] scratch */
   const uint8_t** slot_ptrs; /* [B, k+1] scratch: blob of each pick, shared last */
+  /* Router partial sums (the grouped router GEMM splits K): when logit_planes
+   * is set, it holds logit_parts planes [B][E + 1] (column E: the shared-gate
+   * dot) that the selection adds in plane order, writing logits and
+   * shared_gate itself; when null, logits and shared_gate are final. */
+  const float* logit_planes;
+  uint32_t logit_parts;
 } osmd_moe_args;
 
 /* Largest top-k and expert count the fused decode kernels accept. */
@@ -188,6 +194,7 @@ int osmd_moe_select(const osmd_moe_args* a, osmd_stream s);
  *   gu_part  f32 [splits(D)][2][P][I]
  *   h_terms  bf16 [P][2][I]    h_sums   f32 [P][I/G]
  *   partial  f32 [splits(I)][P][D]
+ *   logit_planes f32 [osmd_moe_grouped_router_parts(D)][T][E + 1] (router GEMM partials)
  * where splits(n) = osmd_moe_grouped_splits(&moe.geom, n) K ranges of the
  * n columns (hidden for gate/up, inter for down).
  * plus the decode workspace of moe (logits, ids, weights, mass, shared_gate,
@@ -205,9 +212,11 @@ typedef struct osmd_moe_grouped_args {
   uint16_t* h_terms;
   float* h_sums;
   float* partial;
+  float* logit_planes;
 } osmd_moe_grouped_args;
 size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t experts);
 uint32_t osmd_moe_grouped_splits(const osm_expert_geometry* g, uint32_t cols);
+uint32_t osmd_moe_grouped_router_parts(uint32_t hidden);
 int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s);
 
 /* Bytes of LDS the down kernel stages for `nslot` slots of width `inter`

@@ -40,7 +40,7 @@ struct HipMoeLayer::Impl {
   HipMoePath path = HipMoePath::automatic;
   bool grouped_ready = false;
   DeviceBytes g_x_terms, g_x_sums, g_pair_pos, g_pair_w, g_tiles, g_tile_count, g_gu_part, g_h_terms,
-      g_h_sums, g_partial;
+      g_h_sums, g_partial, g_logit_planes;
 
   int ensure_grouped(osmd_stream st) {
     if (grouped_ready) return 0;
@@ -58,6 +58,9 @@ struct HipMoeLayer::Impl {
     if (rc == 0) rc = g_h_terms.allocate(P * 2U * I * 2U);
     if (rc == 0) rc = g_h_sums.allocate(P * (I / G) * 4U);
     if (rc == 0) rc = g_partial.allocate(osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(I)) * P * D * 4U);
+    if (rc == 0)
+      rc = g_logit_planes.allocate(osmd_moe_grouped_router_parts(static_cast<std::uint32_t>(D)) * T *
+                                   (cfg.expert_count + 1U) * 4U);
     if (rc == 0) rc = osmd_zero(g_tile_count.get(), 4U, st);
     if (rc == 0) grouped_ready = true;
     return rc;
@@ -89,6 +92,7 @@ struct HipMoeLayer::Impl {
     ga.h_terms = g_h_terms.as<std::uint16_t>();
     ga.h_sums = g_h_sums.as<float>();
     ga.partial = g_partial.as<float>();
+    ga.logit_planes = g_logit_planes.as<float>();
     return ga;
   }
 
