@@ -69,6 +69,40 @@ def test_grouped_small_f32_meta_f32_router_no_shared(ctx):
         assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
 
 
+def test_grouped_router_gemm_planes_no_shared(ctx):
+    # 96 fp32 tokens (more than 64: the router runs as the MFMA GEMM) with a
+    # bf16 router at hidden 768 (three 256-column K planes that the selection
+    # adds) and no shared expert (the planes' shared-gate column is unused).
+    # Ids, weights and logits against the per-token path (decode router
+    # kernel) and the oracle.
+    rng = np.random.default_rng(45)
+    D, I, G, E, k, T = 768, 256, 64, 100, 7, 96
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    blobs = [random_blob(rng, D, I, G, O.META_BF16)[0] for _ in range(E)]
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blobs[e])
+    router_f = rng.normal(0, 0.9 / np.sqrt(D), (E, D)).astype(np.float32)
+    u = router_f.view(np.uint32)
+    router = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    router_f = O.bf16_bits_to_f32(router)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, router, osm_hip.BF16, max_tokens=T)
+    x = rng.normal(0, 1, (T, D)).astype(np.float32)
+    moe.set_path(osm_hip.PATH_GROUPED)
+    gpu = moe.run_slab(slab, 0, x)
+    moe.set_path(osm_hip.PATH_PER_TOKEN)
+    per_token = moe.run_slab(slab, 0, x)
+    assert np.array_equal(gpu["ids"], per_token["ids"])
+    assert max_abs(gpu["weights"], per_token["weights"]) <= 1e-6
+    assert rel_l2(gpu["logits"], per_token["logits"]) <= 1e-5
+    assert rel_l2(gpu["out"], per_token["out"]) <= 2e-5
+    for t in range(0, T, 19):
+        ora = O.qwen_sparse_moe(x[t], router_f, blobs, None, None, D, I, G, O.META_BF16, k)
+        assert np.array_equal(gpu["ids"][t], ora["ids"])
+        assert max_abs(gpu["weights"][t], ora["weights"]) <= 1e-6
+        assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
+
+
 def test_prefill_bf16_chunk(ctx):
     # A 256-token prefill chunk in bf16 at the Qwen3-Next shape: every token
     # against the per-token kernels on the widened input, a sample of tokens
