@@ -91,18 +91,23 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 
 // ---------------------------------------------------------------------------
 // prepare: rows [R, K] (fp32, or bf16 when XBF16) -> terms [R][NS][K] bf16 in
-// word order and sums [R][K/G] of the values the terms represent. One thread
-// per (row, group).
+// word order and sums [R][K/G] of the values the first two terms represent
+// (the expert GEMMs read terms 0 and 1 of this layout; the router GEMM reads
+// all three when NS = 3). One thread per (row, 8-column word); the G/8
+// threads of a group are adjacent lanes of one wavefront and add their sums
+// by butterfly.
 template <bool XBF16, int NS>
 __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t K, uint32_t G,
                                uint16_t* __restrict__ terms, float* __restrict__ sums) {
-  const uint32_t groups = K / G;
-  const size_t n = static_cast<size_t>(R) * groups;
+  static_assert(NS >= kActSplit, "the expert GEMMs read the first two terms");
+  const uint32_t words = K / 8u, wpg = G / 8u;
+  const size_t n = static_cast<size_t>(R) * words;  // a multiple of wpg, so groups never straddle waves
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const uint32_t r = static_cast<uint32_t>(i / groups), g = static_cast<uint32_t>(i % groups);
+  for (size_t i0 = static_cast<size_t>(blockIdx.x) * blockDim.x; i0 < n; i0 += stride) {
+    const size_t i = i0 + threadIdx.x;
     float total = 0.0f;
-    for (uint32_t wd = g * (G / 8u); wd < (g + 1u) * (G / 8u); ++wd) {
+    if (i < n) {
+      const uint32_t r = static_cast<uint32_t>(i / words), wd = static_cast<uint32_t>(i % words);
       float v[8];
       if constexpr (XBF16) {
         const uint4 raw = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + static_cast<size_t>(r) * K + wd * 8u);
@@ -134,11 +139,15 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
         pk.z = out[4] | (static_cast<uint32_t>(out[5]) << 16);
         pk.w = out[6] | (static_cast<uint32_t>(out[7]) << 16);
         *reinterpret_cast<uint4*>(terms + (static_cast<size_t>(r) * NS + s) * K + wd * 8u) = pk;
-      }
+        if (s + 1 == kActSplit) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) total += rep[k];
+          for (int k = 0; k < 8; ++k) total += rep[k];
+        }
+      }
     }
-    sums[i] = total;
+    // Sum of the group's G/8 words, then written by its first lane.
+    for (uint32_t m = 1; m < wpg; m <<= 1) total += __shfl_xor(total, static_cast<int>(m), kWave);
+    if (i < n && (i % wpg) == 0u) sums[i / wpg] = total;
   }
 }
 
@@ -341,7 +350,8 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
 // of each group (step s: word S*q + s), so one lane load covers a group.
 struct SplitParams {
   osm_expert_geometry g;
-  const uint16_t* terms;  // A terms [rows][kActSplit][K]
+  const uint16_t* terms;  // A terms [rows][term_count][K]; the GEMM reads the first kActSplit
+  uint32_t term_count;
   const float* sums;      // [rows][K/G]
   const uint32_t* tile_rows;  // [tiles][16] token of each pair of a tile
   const float* pair_w;    // [P]
@@ -687,7 +697,7 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
       const uint32_t u = tid + i * kSplitThreads;
       const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
       const uint32_t arow = act_row(row < rows ? row : rows - 1u);
-      const uint16_t* src = p.terms + (static_cast<size_t>(arow) * kActSplit + term) * mx.K + split * KS + cu * 8u;
+      const uint16_t* src = p.terms + (static_cast<size_t>(arow) * p.term_count + term) * mx.K + split * KS + cu * 8u;
       if constexpr (kDirect) {
         if (uniform_u32(row) < rows) load_lds16(src, &lds.a[term][row][0]);  // term, row: wave-uniform
       } else {
@@ -946,17 +956,29 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     xin = m.x_norm;
     xbf16 = false;
   }
-  const size_t groups = static_cast<size_t>(T) * (D / G);
-  int r = 0;
   // Up to 64 tokens the per-token router kernel (one wavefront per router
   // row and token) has the shorter latency; beyond, the MFMA router GEMM,
-  // whose K-range planes the selection adds.
-  osmd_moe_args ms = m;
-  if (m.router_dtype == OSM_META_BF16 && (xbf16 || T > kRouterGemmMinTokens)) {
+  // whose K-range planes the selection adds. One preparation serves both
+  // GEMMs: 3 bf16 terms per activation for the router, of which the expert
+  // GEMMs read the first 2 (the group sums are of those 2).
+  const bool router_gemm = m.router_dtype == OSM_META_BF16 && (xbf16 || T > kRouterGemmMinTokens);
+  if (xbf16 && !router_gemm) return 1;  // the caller only passes bf16 input with a bf16 router
+  const uint32_t x_term_count = router_gemm ? kRouterSplit : kActSplit;
+  const size_t words = static_cast<size_t>(T) * (D / 8u);
+  if (router_gemm) {
     if (xbf16)
-      prepare_kernel<true, kRouterSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+      prepare_kernel<true, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
     else
-      prepare_kernel<false, kRouterSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+      prepare_kernel<false, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+  } else {
+    if (xbf16)
+      prepare_kernel<true, kActSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+    else
+      prepare_kernel<false, kActSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+  }
+  int r = 0;
+  osmd_moe_args ms = m;
+  if (router_gemm) {
     const uint32_t nrows = m.expert_count + has_shared;
     const uint32_t rcols = router_range(D);
     const dim3 grid((nrows + kGroupedWaves * kBlockRows - 1) / (kGroupedWaves * kBlockRows),
@@ -984,7 +1006,6 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     osmd_moe_args ra = m;
     ra.flags &= ~static_cast<uint32_t>(OSMD_MOE_RMSNORM);  // x is normalised above
     ra.x = static_cast<const float*>(xin);
-    if (xbf16) return 1;  // the caller only passes bf16 input with a bf16 router
     r = osmd_moe_router(&ra, s);
     if (r != 0) return r;
   }
@@ -995,16 +1016,10 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
                                               m.fallback_blob, a->pair_pos, a->pair_w, static_cast<Tile*>(a->tiles),
                                               tile_rows, a->tile_count, static_cast<uint32_t>(max_tiles));
 
-  // The expert GEMMs take 2 terms per activation; the router's 3-term data
-  // is re-packed (its group sums must be of the terms the GEMMs multiply).
-  if (xbf16)
-    prepare_kernel<true, kActSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
-  else
-    prepare_kernel<false, kActSplit><<<blocks_for(groups, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
-
   SplitParams sp{};
   sp.g = g;
   sp.terms = a->x_terms;
+  sp.term_count = x_term_count;
   sp.sums = a->x_sums;
   sp.tile_rows = tile_rows;
   sp.pair_w = a->pair_w;
@@ -1019,6 +1034,7 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   swiglu_terms_kernel<<<blocks_for(hwords, 4096), 256, 0, st>>>(a->gu_part, gu_splits, P, I, G, a->h_terms,
                                                                 a->h_sums);
   sp.terms = a->h_terms;
+  sp.term_count = kActSplit;
   sp.sums = a->h_sums;
   sp.out = a->partial;
   const uint32_t dn_splits = osmd_moe_grouped_splits(&g, I);
