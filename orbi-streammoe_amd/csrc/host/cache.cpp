@@ -284,6 +284,10 @@ struct HipResidentExpertCache::Impl {
   std::unordered_map<std::uint64_t, std::unique_ptr<HipResidentExpert>> views;
   osmd_event reuse_ev = nullptr, fill_ev = nullptr;
   std::uint64_t filled = 0;
+  // Fill batch (begin_fills .. end_fills): one reuse wait before the first
+  // copy and one fill wait after the last, instead of two per copy.
+  bool batching = false, batch_waited = false;
+  std::uint32_t batch_fills = 0;
 
   Impl(HipComputeContext& c, ExpertBlobSource& s, std::size_t budget)
       : ctx(c), source(s), policy(budget) {}
@@ -350,12 +354,21 @@ HipResidentExpert* HipResidentExpertCache::get(std::uint32_t layer, std::uint32_
     }
     // The side stream waits for everything enqueued so far on the compute
     // stream (earlier readers of this slot), copies, and the compute stream
-    // waits for the copy.
-    int rc = osmd_event_record(m.reuse_ev, m.ctx.stream());
-    if (rc == 0) rc = osmd_stream_wait_event(m.ctx.copy_stream(), m.reuse_ev);
+    // waits for the copy. In a fill batch nothing is enqueued on the compute
+    // stream between the gets, so the first copy's wait covers them all and
+    // end_fills makes the compute stream wait once for the last copy.
+    int rc = 0;
+    if (!m.batching || !m.batch_waited) {
+      rc = osmd_event_record(m.reuse_ev, m.ctx.stream());
+      if (rc == 0) rc = osmd_stream_wait_event(m.ctx.copy_stream(), m.reuse_ev);
+      m.batch_waited = m.batching && rc == 0;
+    }
     if (rc == 0) rc = osmd_memcpy_h2d(dst, src, m.stride, m.ctx.copy_stream());
-    if (rc == 0) rc = osmd_event_record(m.fill_ev, m.ctx.copy_stream());
-    if (rc == 0) rc = osmd_stream_wait_event(m.ctx.stream(), m.fill_ev);
+    if (rc == 0 && !m.batching) {
+      rc = osmd_event_record(m.fill_ev, m.ctx.copy_stream());
+      if (rc == 0) rc = osmd_stream_wait_event(m.ctx.stream(), m.fill_ev);
+    }
+    if (rc == 0 && m.batching) ++m.batch_fills;
     if (rc == 0 && !m.source.stable_pointers()) rc = osmd_stream_synchronize(m.ctx.copy_stream());
     if (rc != 0) {
       m.policy.forget(key);
@@ -379,6 +392,25 @@ HipResidentExpert* HipResidentExpertCache::get(std::uint32_t layer, std::uint32_
     set_diag(diagnostic, std::string("resident expert cache exception: ") + e.what());
     return nullptr;
   }
+}
+
+void HipResidentExpertCache::begin_fills() noexcept {
+  impl_->batching = true;
+  impl_->batch_waited = false;
+  impl_->batch_fills = 0;
+}
+
+int HipResidentExpertCache::end_fills() noexcept {
+  Impl& m = *impl_;
+  int rc = 0;
+  if (m.batching && m.batch_fills > 0) {
+    rc = osmd_event_record(m.fill_ev, m.ctx.copy_stream());
+    if (rc == 0) rc = osmd_stream_wait_event(m.ctx.stream(), m.fill_ev);
+  }
+  m.batching = false;
+  m.batch_waited = false;
+  m.batch_fills = 0;
+  return rc;
 }
 
 HipValuesResult HipResidentExpertCache::run(std::uint32_t layer, std::uint32_t expert,

@@ -36,6 +36,8 @@ struct HipMoeLayer::Impl {
   DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs;
   DeviceBytes fused_sync;  // single-launch handshake words (zeroed once)
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
+  PinnedBytes host_io;    // cache-driven path: pinned staging of inputs and outputs (grown on use)
+  DeviceBytes dev_io;     // its device mirror: one copy in, one copy out per call
   // grouped (multi-token) path: allocated on its first use
   HipMoePath path = HipMoePath::automatic;
   bool grouped_ready = false;
@@ -586,39 +588,86 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
     }
     if (!context.activate(&r.diagnostic)) return r;
     const osmd_stream st = context.stream();
-    // 1. route on the device (with given picks: for the shared gate, logits
-    // and normalised input; the picks then replace ids and weights)
-    int rc = osmd_memcpy_h2d(m->x_in.get(), hidden.data(), hidden.size_bytes(), st);
-    osmd_moe_args a = m->args(m->x_in.as<const float>(), m->y_out.as<float>(), tokens, nullptr, sublayer);
-    if (rc == 0) rc = osmd_moe_route(&a, st);
-    std::vector<std::uint32_t> ids(tokens * K);
-    if (picks != nullptr) {
-      std::copy(picks->ids, picks->ids + tokens * K, ids.begin());
-      if (rc == 0) rc = osmd_memcpy_h2d(m->ids.get(), picks->ids, ids.size() * 4, st);
-      if (rc == 0) rc = osmd_memcpy_h2d(m->weights.get(), picks->weights, ids.size() * 4, st);
-    } else if (rc == 0) {
-      rc = osmd_memcpy_d2h(ids.data(), m->ids.get(), ids.size() * 4, st);
-    }
-    if (rc == 0) rc = osmd_stream_synchronize(st);
-    if (rc != 0) {
-      r.diagnostic = hip_error("Qwen sparse MoE routing failed", rc);
-      return r;
-    }
-    // 2. make every pick resident (in pick order, as the reference does)
+    const std::size_t E = m->cfg.expert_count;
     const std::uint32_t nslot = m->nslot();
-    auto* host_ptrs = static_cast<const std::uint8_t**>(m->host_ptrs.get());
+    // Inputs and outputs of the call sit in one device block mirrored by
+    // pinned host staging: [x | pick ids | pick weights | slot pointers]
+    // then [y | normalised x | mass | shared gate | logits | ids | weights].
+    // With given picks that is one copy in and one out; with device routing
+    // the ids come back first (one wait) and the slot pointers go in after.
+    auto al = [](std::size_t n) { return (n + 255U) & ~static_cast<std::size_t>(255U); };
+    const std::size_t xb = hidden.size_bytes(), kb = tokens * K * 4U, tb = tokens * 4U, eb = tokens * E * 4U,
+                      pb = tokens * nslot * sizeof(void*);
+    const std::size_t o_x = 0, o_pid = al(xb), o_pw = o_pid + al(kb), o_ptr = o_pw + al(kb),
+                      o_out = o_ptr + al(pb), o_y = o_out, o_norm = o_y + al(xb), o_mass = o_norm + al(xb),
+                      o_gate = o_mass + al(tb), o_lg = o_gate + al(tb), o_rid = o_lg + al(eb),
+                      o_rw = o_rid + al(kb), io_bytes = o_rw + al(kb);
+    if (m->host_io.size() < io_bytes || m->dev_io.size() < io_bytes) {
+      m->host_io.reset();
+      m->dev_io.reset();
+      int arc = m->host_io.allocate(io_bytes);
+      if (arc == 0) arc = m->dev_io.allocate(io_bytes);
+      if (arc != 0) {
+        m->host_io.reset();
+        m->dev_io.reset();
+        r.diagnostic = hip_error("Qwen sparse MoE staging allocation failed", arc);
+        return r;
+      }
+    }
+    auto* io = static_cast<std::uint8_t*>(m->host_io.get());
+    auto* dio = m->dev_io.as<std::uint8_t>();
+    auto dptr = [&](std::size_t off) { return reinterpret_cast<float*>(dio + off); };
+    osmd_moe_args ar = m->args(dptr(o_x), dptr(o_y), tokens, nullptr, sublayer);
+    ar.x_norm = dptr(o_norm);
+    ar.logits = dptr(o_lg);
+    ar.ids = reinterpret_cast<std::uint32_t*>(dio + o_rid);
+    ar.weights = dptr(o_rw);
+    ar.mass = dptr(o_mass);
+    ar.shared_gate = dptr(o_gate);
+    osmd_moe_args ae = ar;  // the experts read the host's slot pointers and the picks' weights
+    ae.slot_ptrs = reinterpret_cast<const std::uint8_t**>(dio + o_ptr);
+    if (picks != nullptr) ae.weights = dptr(o_pw);
+
+    std::memcpy(io + o_x, hidden.data(), xb);
+    const std::uint32_t* ids = nullptr;
+    int rc = 0;
+    if (picks != nullptr) {
+      std::memcpy(io + o_pid, picks->ids, kb);
+      std::memcpy(io + o_pw, picks->weights, kb);
+      ids = picks->ids;
+    } else {
+      // 1. route on the device and read the ids back
+      rc = osmd_memcpy_h2d(dio + o_x, io + o_x, xb, st);
+      if (rc == 0) rc = osmd_moe_route(&ar, st);
+      if (rc == 0) rc = osmd_memcpy_d2h(io + o_rid, dio + o_rid, kb, st);
+      if (rc == 0) rc = osmd_stream_synchronize(st);
+      if (rc != 0) {
+        r.diagnostic = hip_error("Qwen sparse MoE routing failed", rc);
+        return r;
+      }
+      ids = reinterpret_cast<const std::uint32_t*>(io + o_rid);
+    }
+    // 2. make every pick resident (in pick order, as the reference does).
+    // The misses are copied back to back on the side stream, which waits
+    // once for the compute stream's earlier work; the compute stream waits
+    // once for the copies, before the expert kernels (with given picks the
+    // routing kernels run meanwhile: they read no expert slot).
+    auto* host_ptrs = reinterpret_cast<const std::uint8_t**>(io + o_ptr);
     std::unordered_set<std::uint64_t> needed;
+    expert_cache.begin_fills();
     for (std::uint32_t t = 0; t < tokens; ++t) {
       for (std::size_t j = 0; j < K; ++j) {
         const std::uint32_t id = ids[t * K + j];
         std::string d;
         HipResidentExpert* e = expert_cache.get(layer, id, &d);
         if (e == nullptr) {
+          (void)expert_cache.end_fills();
           r.diagnostic = "Qwen sparse MoE routed expert " + std::to_string(id) + " load failed: " + d;
           return r;
         }
         if (e->input_dim() != D || e->output_dim() != D ||
             e->intermediate_dim() != m->cfg.geometry.inter) {
+          (void)expert_cache.end_fills();
           r.diagnostic = "Qwen sparse MoE routed expert geometry mismatch";
           return r;
         }
@@ -627,29 +676,49 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
       }
       if (nslot > K) host_ptrs[t * nslot + K] = m->shared_blob.as<const std::uint8_t>();
     }
+    if (picks != nullptr) {
+      rc = osmd_memcpy_h2d(dio, io, o_out, st);  // x, picks and slot pointers
+      if (rc == 0) rc = osmd_moe_route(&ar, st);
+    } else {
+      rc = osmd_memcpy_h2d(dio + o_ptr, io + o_ptr, pb, st);
+    }
+    const int frc = expert_cache.end_fills();
+    if (rc == 0) rc = frc;
+    if (rc != 0) {
+      r.diagnostic = hip_error("Qwen sparse MoE: routing or expert fills failed", rc);
+      return r;
+    }
     for (const std::uint64_t key : needed)
       if (!expert_cache.contains(layer, static_cast<std::uint32_t>(key & 0xFFFFFFFFU))) {
         r.diagnostic = "Qwen sparse MoE: the cache budget cannot hold every expert of this batch at once";
         return r;
       }
-    // 3. expert kernels over the resident slots
-    rc = osmd_memcpy_h2d(m->slot_ptrs.get(), host_ptrs, tokens * nslot * sizeof(void*), st);
-    if (rc == 0) rc = osmd_moe_experts(&a, st);
-    r.values.resize(hidden.size());
-    if (rc == 0) rc = osmd_memcpy_d2h(r.values.data(), m->y_out.get(), hidden.size_bytes(), st);
-    if (rc == 0 && sublayer) {
-      r.normalized.resize(hidden.size());
-      rc = osmd_memcpy_d2h(r.normalized.data(), m->x_norm.get(), hidden.size_bytes(), st);
-    }
+    // 3. expert kernels over the resident slots, then every output in one copy
+    rc = osmd_moe_experts(&ae, st);
+    if (rc == 0) rc = osmd_memcpy_d2h(io + o_out, dio + o_out, io_bytes - o_out, st);
+    if (rc == 0) rc = osmd_stream_synchronize(st);
     if (rc != 0) {
-      r.values.clear();
       r.diagnostic = hip_error("Qwen sparse MoE expert phase failed", rc);
       return r;
     }
-    if (!layer_state.download_routing(context, tokens, r.routing, &r.diagnostic)) {
-      r.values.clear();
-      return r;
+    auto take = [&](std::size_t off, std::size_t n) {
+      const float* f = reinterpret_cast<const float*>(io + off);
+      return std::vector<float>(f, f + n);
+    };
+    r.values = take(o_y, hidden.size());
+    if (sublayer) r.normalized = take(o_norm, hidden.size());
+    if (picks != nullptr) {
+      r.routing.ids.assign(picks->ids, picks->ids + tokens * K);
+      r.routing.weights.assign(picks->weights, picks->weights + tokens * K);
+    } else {
+      const auto* rid = reinterpret_cast<const std::uint32_t*>(io + o_rid);
+      r.routing.ids.assign(rid, rid + tokens * K);
+      r.routing.weights = take(o_rw, tokens * K);
     }
+    r.routing.mass = take(o_mass, tokens);
+    r.routing.shared_gate = take(o_gate, tokens);
+    if (!m->cfg.has_shared_expert) std::fill(r.routing.shared_gate.begin(), r.routing.shared_gate.end(), 0.0F);
+    r.routing.logits = take(o_lg, tokens * E);
     r.executed = true;
     r.diagnostic = "Qwen sparse MoE combined routed and shared experts on the device.";
   } catch (const std::exception& e) {

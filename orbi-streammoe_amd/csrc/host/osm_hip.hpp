@@ -537,6 +537,14 @@ class HipResidentExpertCache {
                                     std::span<const float> x) noexcept;
   [[nodiscard]] bool contains(std::uint32_t layer, std::uint32_t expert) const noexcept;
   [[nodiscard]] HipResidentExpertCacheStats stats() const noexcept;
+  // Fill batch: the misses of the gets between the two calls are copied
+  // back to back on the side stream, which waits once (at the first miss)
+  // for the compute stream's earlier work; the compute stream waits once for
+  // the copies, in end_fills (which returns the HIP status of that wait).
+  // Work enqueued on the compute stream between the two calls must not read
+  // the cache's slots.
+  void begin_fills() noexcept;
+  [[nodiscard]] int end_fills() noexcept;
 
   [[nodiscard]] std::size_t slot_count() const noexcept;
   [[nodiscard]] std::size_t stride() const noexcept;
