@@ -285,18 +285,29 @@ struct HipResidentExpertCache::Impl {
   osmd_event reuse_ev = nullptr, fill_ev = nullptr;
   std::uint64_t filled = 0;
   // Fill batch (begin_fills .. end_fills): one reuse wait before the first
-  // copy and one fill wait after the last, instead of two per copy.
+  // copy and one fill wait after the last, instead of two per copy. Its
+  // copies alternate between the context's side stream and a second one of
+  // the cache's own: two copies in flight keep PCIe busier than one.
   bool batching = false, batch_waited = false;
   std::uint32_t batch_fills = 0;
+  osmd_stream copy2 = nullptr;
+  osmd_event fill_ev2 = nullptr;
+  // Slots written in this batch and the stream that wrote them: a slot
+  // evicted and refilled within one batch is written again on the same
+  // stream, so its two copies land in order.
+  std::vector<std::pair<std::size_t, osmd_stream>> batch_slots;
 
   Impl(HipComputeContext& c, ExpertBlobSource& s, std::size_t budget)
       : ctx(c), source(s), policy(budget) {}
   ~Impl() {
-    if (reuse_ev || fill_ev) {
+    if (reuse_ev || fill_ev || copy2 || fill_ev2) {
       (void)ctx.activate();
       if (ctx.valid()) osmd_stream_synchronize(ctx.copy_stream());
+      if (copy2) osmd_stream_synchronize(copy2);
       if (reuse_ev) osmd_event_destroy(reuse_ev);
       if (fill_ev) osmd_event_destroy(fill_ev);
+      if (fill_ev2) osmd_event_destroy(fill_ev2);
+      if (copy2) osmd_stream_destroy(copy2);
     }
   }
 };
@@ -319,6 +330,8 @@ HipResidentExpertCache::HipResidentExpertCache(HipComputeContext& context, Exper
   for (std::size_t s = impl_->nslots; s-- > 0;) impl_->free_slots.push_back(s);
   int rc = osmd_event_create(&impl_->reuse_ev);
   if (rc == 0) rc = osmd_event_create(&impl_->fill_ev);
+  if (rc == 0) rc = osmd_event_create(&impl_->fill_ev2);
+  if (rc == 0) rc = osmd_stream_create(&impl_->copy2);
   if (rc != 0) throw std::runtime_error(hip_error("resident expert cache: event creation failed", rc));
 }
 
@@ -361,15 +374,22 @@ HipResidentExpert* HipResidentExpertCache::get(std::uint32_t layer, std::uint32_
     if (!m.batching || !m.batch_waited) {
       rc = osmd_event_record(m.reuse_ev, m.ctx.stream());
       if (rc == 0) rc = osmd_stream_wait_event(m.ctx.copy_stream(), m.reuse_ev);
+      if (rc == 0 && m.batching) rc = osmd_stream_wait_event(m.copy2, m.reuse_ev);
       m.batch_waited = m.batching && rc == 0;
     }
-    if (rc == 0) rc = osmd_memcpy_h2d(dst, src, m.stride, m.ctx.copy_stream());
+    osmd_stream cs = (m.batching && (m.batch_fills & 1U)) ? m.copy2 : m.ctx.copy_stream();
+    if (m.batching) {
+      for (const auto& [bs, bst] : m.batch_slots)
+        if (bs == slot) cs = bst;
+      m.batch_slots.emplace_back(slot, cs);
+    }
+    if (rc == 0) rc = osmd_memcpy_h2d(dst, src, m.stride, cs);
     if (rc == 0 && !m.batching) {
       rc = osmd_event_record(m.fill_ev, m.ctx.copy_stream());
       if (rc == 0) rc = osmd_stream_wait_event(m.ctx.stream(), m.fill_ev);
     }
     if (rc == 0 && m.batching) ++m.batch_fills;
-    if (rc == 0 && !m.source.stable_pointers()) rc = osmd_stream_synchronize(m.ctx.copy_stream());
+    if (rc == 0 && !m.source.stable_pointers()) rc = osmd_stream_synchronize(cs);
     if (rc != 0) {
       m.policy.forget(key);
       set_diag(diagnostic, hip_error("resident expert cache: fill failed", rc));
@@ -398,6 +418,7 @@ void HipResidentExpertCache::begin_fills() noexcept {
   impl_->batching = true;
   impl_->batch_waited = false;
   impl_->batch_fills = 0;
+  impl_->batch_slots.clear();
 }
 
 int HipResidentExpertCache::end_fills() noexcept {
@@ -407,6 +428,11 @@ int HipResidentExpertCache::end_fills() noexcept {
     rc = osmd_event_record(m.fill_ev, m.ctx.copy_stream());
     if (rc == 0) rc = osmd_stream_wait_event(m.ctx.stream(), m.fill_ev);
   }
+  if (rc == 0 && m.batching && m.batch_fills > 1) {
+    rc = osmd_event_record(m.fill_ev2, m.copy2);
+    if (rc == 0) rc = osmd_stream_wait_event(m.ctx.stream(), m.fill_ev2);
+  }
+  m.batch_slots.clear();
   m.batching = false;
   m.batch_waited = false;
   m.batch_fills = 0;

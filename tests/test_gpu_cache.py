@@ -128,3 +128,38 @@ def test_cached_decode_with_given_picks(ctx):
         moe.run_cached(cache, 0, x, picks=(bad, w))
     with pytest.raises(osm_hip.OsmError):
         moe.run_cached(cache, 0, x, picks=(ids, np.full((1, k), np.nan, np.float32)))
+
+
+def test_cached_batch_refills_its_own_slot(ctx):
+    # A 4-expert budget, experts 0-3 used twice each. Picks [4, 5, 0, 1]: 4
+    # misses and takes 0's slot (oldest of equal frequency), 5 misses and
+    # evicts 4 (frequency 1, this call's own fill) into the same slot, 0
+    # misses and evicts 5 into it again (restated policy: 3 evictions). The
+    # call fails, since 4 and 5 are no longer resident, and the slot must
+    # then hold 0's bytes, the last of its three copies in one fill batch:
+    # the later all-hit calls are checked against the oracle.
+    seed, D, I, G, E, k = 23, 256, 128, 64, 16, 4
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    store = osm_hip.ExpertStore(g, 1, E)
+    store.synthesize(ctx, seed)
+    cache = osm_hip.ExpertCache(ctx, 4 * store.stride, store=store)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, 0, E, D), osm_hip.BF16, None, None, None,
+                           max_tokens=1)
+    w = np.full((1, k), 1.0 / k, np.float32)
+
+    def check(ids, t):
+        x = O.synth_tokens(seed, t, 1, D)
+        got = moe.run_cached(cache, 0, x, picks=(np.array([ids], np.uint32), w))
+        ref = np.zeros(D, np.float64)
+        for e in ids:
+            ref += float(w[0, 0]) * O.expert_forward(store.blob_view(0, e), D, I, G, O.META_BF16, x[0])
+        assert rel_l2(got["out"][0], ref.astype(np.float32)) <= 1e-3, (ids, t)
+
+    check([0, 1, 2, 3], 0)
+    check([0, 1, 2, 3], 1)
+    with pytest.raises(osm_hip.OsmError):
+        moe.run_cached(cache, 0, O.synth_tokens(seed, 2, 1, D), picks=(np.array([[4, 5, 0, 1]], np.uint32), w))
+    assert cache.stats()["evictions"] == 3
+    check([0, 1, 2, 3], 3)
+    check([1, 2, 3, 0], 4)
+    assert cache.stats()["evictions"] == 3  # both were all hits
