@@ -51,6 +51,7 @@ typedef struct osm_shared_expert_s* osm_shared_expert;
 typedef struct osm_expert_slab_s* osm_expert_slab;
 typedef struct osm_expert_store_s* osm_expert_store;
 typedef struct osm_host_cache_s* osm_host_cache;
+typedef struct osm_expert_storage_s* osm_expert_storage;
 typedef struct osm_expert_cache_s* osm_expert_cache;
 typedef struct osm_cache_policy_s* osm_cache_policy;
 typedef struct osm_moe_layer_s* osm_moe_layer;
@@ -328,6 +329,22 @@ int osm_expert_store_synthesize(osm_context ctx, osm_expert_store s, uint64_t se
 typedef int (*osm_read_experts_fn)(void* user, const uint32_t* layers, const uint32_t* experts,
                                    void* const* destinations, size_t count, size_t stride);
 
+/* PosixPreadExpertStorage (storage/posix_pread_expert_storage.hpp:13-30,
+ * posix_pread_expert_storage.cpp:98-187): <container_dir>/packed_experts/
+ * layer_LL.bin holds layer LL's `experts` blobs back to back at `stride`
+ * (the counts come from the caller; the reference reads them from the
+ * container's layout.json). */
+int osm_pread_storage_create(const char* container_dir, uint32_t layers, uint32_t experts, size_t stride,
+                             osm_expert_storage* out);
+void osm_expert_storage_destroy(osm_expert_storage s);
+size_t osm_expert_storage_stride(osm_expert_storage s);
+/* ExpertStorage::read_experts: every destination (destination_bytes each, at
+ * least the stride) is filled, or the call fails: OSM_E_INVALID for a layer
+ * or expert out of range or a small destination (checked before any read),
+ * OSM_E_RUNTIME for an open or read error or a short read. */
+int osm_expert_storage_read(osm_expert_storage s, const uint32_t* layers, const uint32_t* experts,
+                            void* const* destinations, size_t count, size_t destination_bytes);
+
 typedef struct osm_host_cache_stats {
   uint64_t hits, misses, allocated_slots, capacity_slots, logical_bytes, budget_bytes;
 } osm_host_cache_stats;
@@ -336,6 +353,9 @@ typedef struct osm_host_cache_stats {
  * pinned memory (needs a device). */
 int osm_host_cache_create(size_t stride, size_t budget_bytes, size_t minimum_slots, int pinned,
                           osm_read_experts_fn read, void* user, osm_host_cache* out);
+/* The same cache over a storage handle, which must outlive the cache. */
+int osm_host_cache_create_with_storage(osm_expert_storage storage, size_t budget_bytes, size_t minimum_slots,
+                                       int pinned, osm_host_cache* out);
 void osm_host_cache_destroy(osm_host_cache c);
 /* ExpertCache::fetch: out_slots[i] is the slot of experts[i]; out_bytes[i]
  * (optional) points at its bytes until the next fetch. */

@@ -115,6 +115,9 @@ struct osm_host_cache_s {
   std::unique_ptr<CallbackStorage> storage;
   std::unique_ptr<osm::HostExpertCache> cache;
 };
+struct osm_expert_storage_s {
+  std::unique_ptr<osm::PosixPreadExpertStorage> storage;
+};
 struct osm_expert_cache_s {
   osm_context owner = nullptr;
   std::unique_ptr<osm::HostCacheSource> host_source;  // when built over an L1 cache
@@ -797,6 +800,36 @@ int osm_expert_store_synthesize(osm_context ctx, osm_expert_store s, uint64_t se
   OSM_GUARD_END
 }
 
+// ---- storage ------------------------------------------------------------------
+int osm_pread_storage_create(const char* container_dir, uint32_t layers, uint32_t experts, size_t stride,
+                             osm_expert_storage* out) {
+  OSM_GUARD_BEGIN
+  if (!container_dir || !out) return fail(OSM_E_INVALID, "null argument");
+  *out = new osm_expert_storage_s{
+      std::make_unique<osm::PosixPreadExpertStorage>(container_dir, layers, experts, stride)};
+  return ok();
+  OSM_GUARD_END
+}
+void osm_expert_storage_destroy(osm_expert_storage s) { delete s; }
+size_t osm_expert_storage_stride(osm_expert_storage s) { return s ? s->storage->expert_stride_bytes() : 0; }
+int osm_expert_storage_read(osm_expert_storage s, const uint32_t* layers, const uint32_t* experts,
+                            void* const* destinations, size_t count, size_t destination_bytes) {
+  OSM_GUARD_BEGIN
+  if (!s || (count && (!layers || !experts || !destinations))) return fail(OSM_E_INVALID, "null argument");
+  std::vector<osm::ExpertReadRequest> req(count);
+  for (size_t i = 0; i < count; ++i) {
+    if (!destinations[i]) return fail(OSM_E_INVALID, "null destination");
+    req[i] = {{layers[i], experts[i]}, {static_cast<std::byte*>(destinations[i]), destination_bytes}};
+  }
+  try {
+    s->storage->read_experts(req);
+  } catch (const std::out_of_range& e) {
+    return fail(OSM_E_INVALID, e.what());
+  }
+  return ok();
+  OSM_GUARD_END
+}
+
 // ---- host L1 cache --------------------------------------------------------------
 int osm_host_cache_create(size_t stride, size_t budget_bytes, size_t minimum_slots, int pinned,
                           osm_read_experts_fn read, void* user, osm_host_cache* out) {
@@ -805,6 +838,15 @@ int osm_host_cache_create(size_t stride, size_t budget_bytes, size_t minimum_slo
   auto storage = std::make_unique<CallbackStorage>(stride, read, user);
   auto cache = std::make_unique<osm::HostExpertCache>(*storage, budget_bytes, minimum_slots, pinned != 0);
   *out = new osm_host_cache_s{std::move(storage), std::move(cache)};
+  return ok();
+  OSM_GUARD_END
+}
+int osm_host_cache_create_with_storage(osm_expert_storage storage, size_t budget_bytes, size_t minimum_slots,
+                                       int pinned, osm_host_cache* out) {
+  OSM_GUARD_BEGIN
+  if (!storage || !out) return fail(OSM_E_INVALID, "null argument");
+  auto cache = std::make_unique<osm::HostExpertCache>(*storage->storage, budget_bytes, minimum_slots, pinned != 0);
+  *out = new osm_host_cache_s{nullptr, std::move(cache)};
   return ok();
   OSM_GUARD_END
 }

@@ -11,8 +11,10 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <filesystem>
 #include <functional>
 #include <memory>
+#include <mutex>
 #include <optional>
 #include <span>
 #include <string>
@@ -341,6 +343,30 @@ class ExpertStorage {
   virtual ~ExpertStorage() = default;
   [[nodiscard]] virtual std::size_t expert_stride_bytes() const noexcept = 0;
   virtual void read_experts(std::span<ExpertReadRequest> requests) = 0;
+};
+
+// PosixPreadExpertStorage (storage/posix_pread_expert_storage.hpp:13-30):
+// <dir>/packed_experts/layer_LL.bin holds layer LL's `experts` blobs at
+// `stride`. Reads run in parallel; any failure or short read throws.
+class PosixPreadExpertStorage final : public ExpertStorage {
+ public:
+  PosixPreadExpertStorage(std::filesystem::path container_dir, std::uint32_t layers, std::uint32_t experts,
+                          std::size_t stride);
+  ~PosixPreadExpertStorage() override;
+  PosixPreadExpertStorage(const PosixPreadExpertStorage&) = delete;
+  PosixPreadExpertStorage& operator=(const PosixPreadExpertStorage&) = delete;
+
+  [[nodiscard]] std::size_t expert_stride_bytes() const noexcept override { return stride_; }
+  void read_experts(std::span<ExpertReadRequest> requests) override;
+  [[nodiscard]] static std::filesystem::path layer_path(const std::filesystem::path& dir, std::uint32_t layer);
+
+ private:
+  int fd_for_layer(std::uint32_t layer);
+  std::filesystem::path dir_;
+  std::uint32_t layers_, experts_;
+  std::size_t stride_;
+  std::vector<int> fds_;
+  std::mutex mutex_;
 };
 
 struct ExpertCacheEntry {

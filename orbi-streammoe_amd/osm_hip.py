@@ -147,6 +147,11 @@ _PROTOTYPES = {
     "osm_expert_store_synthesize": (c_int, [_H, _H, c_uint64]),
     "osm_host_cache_create": (c_int, [c_size_t, c_size_t, c_size_t, c_int, READ_EXPERTS_FN, c_void_p, POINTER(_H)]),
     "osm_host_cache_destroy": (None, [_H]),
+    "osm_host_cache_create_with_storage": (c_int, [_H, c_size_t, c_size_t, c_int, POINTER(_H)]),
+    "osm_pread_storage_create": (c_int, [c_char_p, c_uint32, c_uint32, c_size_t, POINTER(_H)]),
+    "osm_expert_storage_destroy": (None, [_H]),
+    "osm_expert_storage_stride": (c_size_t, [_H]),
+    "osm_expert_storage_read": (c_int, [_H, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
     "osm_host_cache_fetch": (c_int, [_H, c_uint32, c_void_p, c_size_t, c_void_p, c_void_p]),
     "osm_host_cache_resident_slot": (c_int64, [_H, c_uint32, c_uint32]),
     "osm_host_cache_stats_get": (None, [_H, POINTER(HostCacheStats)]),
@@ -683,8 +688,36 @@ class ExpertStore(_Handle):
         check(load().osm_expert_store_synthesize(ctx.h, self.h, seed))
 
 
+class PreadStorage(_Handle):
+    """PosixPreadExpertStorage: <container_dir>/packed_experts/layer_LL.bin
+    holds layer LL's `experts` blobs back to back at `stride`."""
+
+    _destroy = "osm_expert_storage_destroy"
+
+    def __init__(self, container_dir, layers, experts, stride):
+        h = c_void_p()
+        check(load().osm_pread_storage_create(os.fsencode(container_dir), layers, experts, stride, ctypes.byref(h)))
+        super().__init__(h)
+        self.stride = stride
+
+    @staticmethod
+    def layer_path(container_dir, layer):
+        return os.path.join(container_dir, "packed_experts", f"layer_{layer:02d}.bin")
+
+    def read(self, layers, experts, dest_bytes=None) -> list:
+        """Blobs of (layers[i], experts[i]), read in one call."""
+        n = len(experts)
+        size = self.stride if dest_bytes is None else dest_bytes
+        outs = [np.empty(size, np.uint8) for _ in range(n)]
+        ls, es = _c(layers, np.uint32), _c(experts, np.uint32)
+        dests = (c_void_p * max(n, 1))(*[o.ctypes.data for o in outs])
+        check(load().osm_expert_storage_read(self.h, _p(ls), _p(es), dests, n, size))
+        return outs
+
+
 class HostExpertCache(_Handle):
-    """ExpertCache (host L1) over a Python storage callback."""
+    """ExpertCache (host L1) over a Python storage callback, or over a
+    native storage (from_storage)."""
 
     _destroy = "osm_host_cache_destroy"
 
@@ -703,6 +736,17 @@ class HostExpertCache(_Handle):
         check(load().osm_host_cache_create(stride, budget, minimum_slots, 1 if pinned else 0, self._cb, None, ctypes.byref(h)))
         super().__init__(h)
         self.stride = stride
+
+    @classmethod
+    def from_storage(cls, storage: "PreadStorage", budget, minimum_slots=1, pinned=False) -> "HostExpertCache":
+        h = c_void_p()
+        check(load().osm_host_cache_create_with_storage(storage.h, budget, minimum_slots, 1 if pinned else 0,
+                                                        ctypes.byref(h)))
+        obj = cls.__new__(cls)
+        _Handle.__init__(obj, h)
+        obj.stride = storage.stride
+        obj._storage = storage  # the storage must outlive the cache
+        return obj
 
     def fetch(self, layer, experts):
         e = _c(experts, np.uint32)

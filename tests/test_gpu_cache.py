@@ -5,6 +5,8 @@ The reference's own scenario (tests/vulkan_resident_expert_cache_test.cpp:
 decode (capped budget, misses filled from pinned host memory) against the
 all-resident decode and the restated cache policy."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -163,3 +165,32 @@ def test_cached_batch_refills_its_own_slot(ctx):
     check([0, 1, 2, 3], 3)
     check([1, 2, 3, 0], 4)
     assert cache.stats()["evictions"] == 3  # both were all hits
+
+
+def test_cached_decode_from_pread_storage(ctx, tmp_path):
+    # The whole miss path from files: pread storage -> pinned host L1 cache
+    # -> HBM cache, against the all-resident decode (bit-identical outputs).
+    seed, D, I, G, E, k = 24, 256, 128, 64, 32, 4
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    slab.synthesize(seed)
+    stride = osm_hip.expert_blob_bytes(g)
+    os.makedirs(tmp_path / "packed_experts")
+    np.concatenate([O.synth_expert_blob(seed, 0, e, D, I, G) for e in range(E)]).tofile(
+        osm_hip.PreadStorage.layer_path(str(tmp_path), 0))
+    storage = osm_hip.PreadStorage(str(tmp_path), 1, E, stride)
+    # 16 HBM slots: the restated policy replayed over these tokens' routing
+    # evicts 13 times and never a pick of the batch being made resident (at
+    # 12 slots the last two tokens would lose one; the layer needs all of a
+    # token's picks resident at once).
+    host = osm_hip.HostExpertCache.from_storage(storage, 20 * stride, pinned=True)
+    cache = osm_hip.ExpertCache(ctx, 16 * stride, host_cache=host, g=g)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, 0, E, D), osm_hip.BF16,
+                           O.synth_shared_gate_bf16(seed, 0, D), O.synth_norm_weight(seed, 0, D),
+                           O.synth_expert_blob(seed, 0, O.SHARED_EXPERT_ID, D, I, G), max_tokens=1)
+    x = O.synth_tokens(seed, 0, 12, D)
+    for t in range(12):
+        got = moe.run_cached(cache, 0, x[t], sublayer=t % 2 == 0)
+        ref = moe.run_slab(slab, 0, x[t], sublayer=t % 2 == 0)
+        assert np.array_equal(got["ids"], ref["ids"]) and np.array_equal(got["out"], ref["out"])
+    assert cache.stats()["evictions"] > 0 and host.stats()["misses"] > 0
