@@ -36,6 +36,18 @@ typedef enum osm_status {
 
 enum osm_meta_dtype_c { OSM_F32 = 0, OSM_F16 = 1, OSM_BF16 = 2 };
 
+/* Router / shared-gate dtype beyond the three above: MLX affine 8-bit, as
+ * real checkpoints store mlp.gate and shared_expert_gate
+ * (checkpoint_sparse_moe_test.cpp:455-460). The layer's router and
+ * shared-gate pointers then point at an osm_affine_q8_c each. */
+enum { OSM_AFFINE_Q8 = 3 };
+typedef struct osm_affine_q8_c {
+  const uint32_t* packed; /* [rows, cols/4], four values per word, low byte first */
+  const float* scales;    /* [rows, cols/group] */
+  const float* biases;    /* [rows, cols/group] */
+  uint32_t group;         /* a multiple of 4 dividing hidden; the same for router and shared gate */
+} osm_affine_q8_c;
+
 typedef struct osm_expert_geometry_c {
   uint32_t hidden;     /* model width D: gate/up input, down output */
   uint32_t inter;      /* expert intermediate width I */
@@ -200,6 +212,9 @@ typedef struct osm_moe_config {
   float rms_eps;           /* RMSNorm epsilon of the sublayer form */
 } osm_moe_config;
 
+/* router: [E, D] in router_dtype (OSM_F32 / OSM_F16 / OSM_BF16), or an
+ * osm_affine_q8_c of [E, D] for OSM_AFFINE_Q8; shared_gate_vec likewise
+ * [D] or an osm_affine_q8_c of [1, D]. */
 int osm_moe_layer_create(osm_context ctx, const osm_moe_config* cfg, const void* router,
                          uint32_t router_dtype, const void* shared_gate_vec,
                          const float* norm_weight, const void* shared_blob, size_t shared_bytes,

@@ -522,6 +522,10 @@ int osm_expert_slab_synthesize(osm_expert_slab s, uint64_t seed) {
 }
 
 // ---- MoE layer ----------------------------------------------------------------
+static_assert(sizeof(osm_affine_q8_c) == sizeof(osm_affine_q8) &&
+                  offsetof(osm_affine_q8_c, group) == offsetof(osm_affine_q8, group) &&
+                  static_cast<uint32_t>(OSM_AFFINE_Q8) == OSM_ROUTER_AFFINE_Q8,
+              "the public affine-q8 view is the internal one");
 int osm_moe_layer_create(osm_context ctx, const osm_moe_config* cfg, const void* router,
                          uint32_t router_dtype, const void* shared_gate_vec, const float* norm_weight,
                          const void* shared_blob, size_t shared_bytes, uint32_t max_tokens,

@@ -303,6 +303,45 @@ template <int RD>
 struct Raw8 {  // 8 router elements as loaded
   uint4 v[RD == OSM_META_F32 ? 2 : 1];
 };
+// Affine q8: two words of four bytes and the scale and bias of each word's
+// group (a group is a multiple of 4 columns, so a word never straddles one).
+template <>
+struct Raw8<OSM_ROUTER_AFFINE_Q8> {
+  uint2 q;
+  float s[2], b[2];
+};
+
+// Row r of an affine-q8 matrix of `rows` rows held as one buffer
+// [packed rows x D/4][scales rows x D/g][biases rows x D/g]: element c is
+// scale * q + bias, the product rounded before the add, as the reference's
+// dequantisation computes it (reference_ops.cpp:48-63).
+struct Q8Row {
+  const uint32_t* q;
+  const float* s;
+  const float* b;
+  uint32_t group;
+};
+__device__ __forceinline__ Q8Row q8_row(const void* base, uint32_t rows, uint32_t r, uint32_t D, uint32_t group) {
+  const uint32_t* q = static_cast<const uint32_t*>(base);
+  const uint32_t gpr = D / group;
+  const float* s = reinterpret_cast<const float*>(q + static_cast<size_t>(rows) * (D / 4u));
+  const float* b = s + static_cast<size_t>(rows) * gpr;
+  return Q8Row{q + static_cast<size_t>(r) * (D / 4u), s + static_cast<size_t>(r) * gpr,
+               b + static_cast<size_t>(r) * gpr, group};
+}
+// scale * q + bias with the product rounded first: hipcc would otherwise
+// fuse the two into one FMA.
+__device__ __forceinline__ float dequant_q8(float s, float q, float b) {
+#pragma clang fp contract(off)
+  return s * q + b;
+}
+__device__ __forceinline__ void load_q8x8(const Q8Row& row, uint32_t c, Raw8<OSM_ROUTER_AFFINE_Q8>& r) {
+  r.q = ldg8(row.q + c / 4u);
+  r.s[0] = ldg<float>(row.s + c / row.group);
+  r.b[0] = ldg<float>(row.b + c / row.group);
+  r.s[1] = ldg<float>(row.s + (c + 4u) / row.group);
+  r.b[1] = ldg<float>(row.b + (c + 4u) / row.group);
+}
 
 template <int RD>
 __device__ __forceinline__ void load_raw8(const uint8_t* row, uint32_t c, Raw8<RD>& r) {
@@ -316,7 +355,11 @@ __device__ __forceinline__ void load_raw8(const uint8_t* row, uint32_t c, Raw8<R
 
 template <int RD>
 __device__ __forceinline__ float raw8_get(const Raw8<RD>& r, int j) {
-  if constexpr (RD == OSM_META_F32) {
+  if constexpr (RD == OSM_ROUTER_AFFINE_Q8) {
+    const uint32_t w = j < 4 ? r.q.x : r.q.y;
+    const float q = static_cast<float>((w >> (8 * (j % 4))) & 0xFFu);
+    return dequant_q8(r.s[j / 4], q, r.b[j / 4]);
+  } else if constexpr (RD == OSM_META_F32) {
     const uint4& q = r.v[j / 4];
     const uint32_t w = (j % 4 == 0) ? q.x : (j % 4 == 1) ? q.y : (j % 4 == 2) ? q.z : q.w;
     return __uint_as_float(w);
@@ -399,15 +442,25 @@ __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, 
   const uint32_t nrows = E + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
   const uint32_t row = blk * kRouteWaves + wave;
   constexpr size_t esz = (RD == OSM_META_F32) ? 4u : 2u;
-  const uint8_t* wrow = row < E ? static_cast<const uint8_t*>(a.router) + static_cast<size_t>(row) * D * esz
-                                : static_cast<const uint8_t*>(a.shared_gate_vec);
   // The row is issued before x, so both are in flight together.
   Raw8<RD> w[RCH];
   if (row < nrows) {
+    if constexpr (RD == OSM_ROUTER_AFFINE_Q8) {
+      const Q8Row qr = row < E ? q8_row(a.router, E, row, D, a.router_group)
+                               : q8_row(a.shared_gate_vec, 1u, 0u, D, a.router_group);
 #pragma unroll
-    for (int u = 0; u < RCH; ++u) {
-      const uint32_t c = lane * 8u + u * 8u * kWave;
-      if (c < D) load_raw8<RD>(wrow, c, w[u]);
+      for (int u = 0; u < RCH; ++u) {
+        const uint32_t c = lane * 8u + u * 8u * kWave;
+        if (c < D) load_q8x8(qr, c, w[u]);
+      }
+    } else {
+      const uint8_t* wrow = row < E ? static_cast<const uint8_t*>(a.router) + static_cast<size_t>(row) * D * esz
+                                    : static_cast<const uint8_t*>(a.shared_gate_vec);
+#pragma unroll
+      for (int u = 0; u < RCH; ++u) {
+        const uint32_t c = lane * 8u + u * 8u * kWave;
+        if (c < D) load_raw8<RD>(wrow, c, w[u]);
+      }
     }
   }
   stage_x(a, t, xs, blk == 0);
@@ -1299,6 +1352,7 @@ int osmd_moe_router(const osmd_moe_args* a, osmd_stream s) {
   switch (a->router_dtype) {
     case OSM_META_F32: return launch_route_rd<OSM_META_F32>(*a, st);
     case OSM_META_F16: return launch_route_rd<OSM_META_F16>(*a, st);
+    case OSM_ROUTER_AFFINE_Q8: return launch_route_rd<OSM_ROUTER_AFFINE_Q8>(*a, st);
     default: return launch_route_rd<OSM_META_BF16>(*a, st);
   }
 }

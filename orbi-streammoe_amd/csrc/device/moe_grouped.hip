@@ -90,6 +90,15 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 // ---------------------------------------------------------------------------
+// bf16 rows widened to fp32 (exact), for the per-token router kernel when the
+// router is not bf16 and so cannot run as the MFMA GEMM.
+__global__ void widen_bf16_kernel(const uint16_t* __restrict__ x, size_t n, float* __restrict__ out) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    out[i] = bf16_to_f32(x[i]);
+}
+
+// ---------------------------------------------------------------------------
 // prepare: rows [R, K] (fp32, or bf16 when XBF16) -> terms [R][NS][K] bf16 in
 // word order and sums [R][K/G] of the values the first two terms represent
 // (the expert GEMMs read terms 0 and 1 of this layout; the router GEMM reads
@@ -962,7 +971,13 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   // GEMMs: 3 bf16 terms per activation for the router, of which the expert
   // GEMMs read the first 2 (the group sums are of those 2).
   const bool router_gemm = m.router_dtype == OSM_META_BF16 && (xbf16 || T > kRouterGemmMinTokens);
-  if (xbf16 && !router_gemm) return 1;  // the caller only passes bf16 input with a bf16 router
+  if (xbf16 && !router_gemm) {
+    // A router of another dtype runs as the per-token kernel, on fp32 input.
+    const size_t n = static_cast<size_t>(T) * D;
+    widen_bf16_kernel<<<blocks_for(n, 4096), 256, 0, st>>>(static_cast<const uint16_t*>(xin), n, m.x_norm);
+    xin = m.x_norm;
+    xbf16 = false;
+  }
   const uint32_t x_term_count = router_gemm ? kRouterSplit : kActSplit;
   const size_t words = static_cast<size_t>(T) * (D / 8u);
   if (router_gemm) {

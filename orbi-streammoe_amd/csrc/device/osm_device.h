@@ -110,7 +110,8 @@ typedef struct osmd_moe_args {
   uint32_t expert_count;   /* E */
   uint32_t top_k;          /* k */
   uint32_t norm_topk_prob; /* renormalise the selected probabilities */
-  uint32_t router_dtype;   /* OSM_META_F32 / F16 / BF16 for router, w_sg */
+  uint32_t router_dtype;   /* OSM_META_F32 / F16 / BF16 or OSM_ROUTER_AFFINE_Q8 for router, w_sg */
+  uint32_t router_group;   /* OSM_ROUTER_AFFINE_Q8: quantisation group (a multiple of 4 dividing D) */
   uint32_t flags;          /* OSMD_MOE_* */
   uint32_t tokens;         /* B */
   float rms_eps;

@@ -23,11 +23,25 @@ bool finite_weights(const void* p, std::size_t n, std::uint32_t dtype) {
   return true;
 }
 
+// Every value scale * q + bias of an affine-q8 matrix is finite (the
+// reference scans its dequantised router, qwen_router.cpp:54-59).
+bool finite_q8(const osm_affine_q8& m, std::size_t rows, std::size_t cols) {
+  const std::size_t gpr = cols / m.group;
+  for (std::size_t r = 0; r < rows; ++r)
+    for (std::size_t c = 0; c < cols; ++c) {
+      const float q = static_cast<float>((m.packed[r * (cols / 4) + c / 4] >> (8 * (c % 4))) & 0xFFU);
+      const volatile float prod = m.scales[r * gpr + c / m.group] * q;  // rounded before the add
+      if (!std::isfinite(prod + m.biases[r * gpr + c / m.group])) return false;
+    }
+  return true;
+}
+
 }  // namespace
 
 struct HipMoeLayer::Impl {
   HipMoeLayerConfig cfg{};
   std::uint32_t router_dtype = OSM_META_BF16;
+  std::uint32_t router_group = 0;  // OSM_ROUTER_AFFINE_Q8 only
   std::uint32_t max_tokens = 0;
   int device = -1;
   DeviceBytes router, shared_gate_vec, norm_weight, shared_blob;
@@ -108,6 +122,7 @@ struct HipMoeLayer::Impl {
     a.top_k = cfg.top_k;
     a.norm_topk_prob = cfg.norm_topk_prob ? 1U : 0U;
     a.router_dtype = router_dtype;
+    a.router_group = router_group;
     a.flags = (cfg.has_shared_expert ? static_cast<std::uint32_t>(OSMD_MOE_SHARED) : 0U) |
               (sublayer ? static_cast<std::uint32_t>(OSMD_MOE_RMSNORM | OSMD_MOE_RESIDUAL) : 0U);
     a.tokens = tokens;
@@ -170,9 +185,24 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
       set_diag(diagnostic, "MoE layer: (top_k + shared) * intermediate exceeds the 64 KiB LDS staging");
       return std::nullopt;
     }
-    if (router_dtype > OSM_META_BF16 || router == nullptr) {
-      set_diag(diagnostic, "MoE layer: router must be F32, F16 or BF16");
+    if ((router_dtype > OSM_META_BF16 && router_dtype != OSM_ROUTER_AFFINE_Q8) || router == nullptr) {
+      set_diag(diagnostic, "MoE layer: router must be F32, F16, BF16 or affine Q8");
       return std::nullopt;
+    }
+    const bool q8 = router_dtype == OSM_ROUTER_AFFINE_Q8;
+    const auto* rq = static_cast<const osm_affine_q8*>(router);
+    const auto* sq = static_cast<const osm_affine_q8*>(shared_gate_vec);
+    if (q8) {
+      // checkpoint_sparse_moe.cpp:59-90 dequantises both modules at load; here
+      // they stay 8-bit in HBM and the router kernel dequantises in registers.
+      auto ok = [&](const osm_affine_q8* m) {
+        return m && m->packed && m->scales && m->biases && m->group != 0 && m->group % 4U == 0 &&
+               g.hidden % m->group == 0;
+      };
+      if (!ok(rq) || (config.has_shared_expert && (!ok(sq) || sq->group != rq->group))) {
+        set_diag(diagnostic, "MoE layer: affine Q8 router and shared gate need one group size, a multiple of 4 dividing hidden");
+        return std::nullopt;
+      }
     }
     if (max_tokens == 0 || max_tokens > 65535U) {
       set_diag(diagnostic, "MoE layer: max_tokens must be in [1, 65535]");
@@ -188,19 +218,21 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
         return std::nullopt;
       }
     }
-    const std::size_t esz = osm_meta_bytes(router_dtype);
+    const std::size_t esz = q8 ? 0U : osm_meta_bytes(router_dtype);
     const std::size_t router_n = static_cast<std::size_t>(config.expert_count) * g.hidden;
-    if (!finite_weights(router, router_n, router_dtype)) {
+    if (q8 ? !finite_q8(*rq, config.expert_count, g.hidden) : !finite_weights(router, router_n, router_dtype)) {
       set_diag(diagnostic, "qwen router: router weight contains non-finite value");
       return std::nullopt;
     }
-    if (config.has_shared_expert && !finite_weights(shared_gate_vec, g.hidden, router_dtype)) {
+    if (config.has_shared_expert &&
+        (q8 ? !finite_q8(*sq, 1U, g.hidden) : !finite_weights(shared_gate_vec, g.hidden, router_dtype))) {
       set_diag(diagnostic, "shared expert scalar gate contains non-finite value");
       return std::nullopt;
     }
     auto impl = std::make_unique<Impl>();
     impl->cfg = config;
     impl->router_dtype = router_dtype;
+    impl->router_group = q8 ? rq->group : 0U;
     impl->max_tokens = max_tokens;
     impl->device = context.device();
     const osmd_stream st = context.stream();
@@ -210,8 +242,18 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
       return rc;
     };
     const std::size_t T = max_tokens, D = g.hidden, E = config.expert_count, K = config.top_k;
-    int rc = up(impl->router, router, router_n * esz);
-    if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_gate_vec, shared_gate_vec, D * esz);
+    // Affine q8: one buffer [packed rows x D/4][scales rows x D/g][biases].
+    auto up_q8 = [&](DeviceBytes& d, const osm_affine_q8& m, std::size_t rows) {
+      const std::size_t qb = rows * D, mb = rows * (D / m.group) * sizeof(float);
+      int rc2 = d.allocate(qb + 2 * mb);
+      if (rc2 == 0) rc2 = osmd_memcpy_h2d(d.get(), m.packed, qb, st);
+      if (rc2 == 0) rc2 = osmd_memcpy_h2d(d.as<std::uint8_t>() + qb, m.scales, mb, st);
+      if (rc2 == 0) rc2 = osmd_memcpy_h2d(d.as<std::uint8_t>() + qb + mb, m.biases, mb, st);
+      return rc2;
+    };
+    int rc = q8 ? up_q8(impl->router, *rq, E) : up(impl->router, router, router_n * esz);
+    if (rc == 0 && config.has_shared_expert)
+      rc = q8 ? up_q8(impl->shared_gate_vec, *sq, 1U) : up(impl->shared_gate_vec, shared_gate_vec, D * esz);
     if (rc == 0 && !norm_weight.empty()) rc = up(impl->norm_weight, norm_weight.data(), norm_weight.size_bytes());
     if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_blob, shared_blob.data(), shared_blob.size());
     if (rc == 0 && !config.has_shared_expert) {
@@ -388,10 +430,6 @@ HipDispatchResult HipMoeLayer::prefill_device_bf16(HipComputeContext& context, c
   if (!context.activate(&r.diagnostic)) return r;
   if (tokens == 0 || tokens > impl_->max_tokens || x_bf16 == nullptr || y == nullptr || expert_table == nullptr) {
     r.diagnostic = "MoE prefill: invalid arguments";
-    return r;
-  }
-  if (impl_->router_dtype != OSM_META_BF16) {
-    r.diagnostic = "MoE prefill from bf16 input needs a bf16 router";
     return r;
   }
   if (!impl_->grouped_ok(x_bf16)) {

@@ -42,6 +42,21 @@ enum osm_meta_dtype {
   OSM_META_BF16 = 2
 };
 
+/* Router and shared-gate storage beyond the dtypes above: MLX affine 8-bit
+ * (4 values per u32, low byte first) with f32 scale and bias per group,
+ * held as one buffer [packed rows x D/4 words][scales rows x D/g][biases]. */
+#define OSM_ROUTER_AFFINE_Q8 3u
+
+/* Host view of one affine-q8 matrix [rows, cols]: what the router and
+ * shared-gate pointers of a layer point at when their dtype is
+ * OSM_ROUTER_AFFINE_Q8 (the checkpoint's MlxAffineModule at 8 bits). */
+typedef struct osm_affine_q8 {
+  const uint32_t* packed; /* [rows, cols/4], low byte first */
+  const float* scales;    /* [rows, cols/group] */
+  const float* biases;    /* [rows, cols/group] */
+  uint32_t group;         /* group size: a multiple of 4 dividing cols */
+} osm_affine_q8;
+
 typedef struct osm_expert_geometry {
   uint32_t hidden;       /* model width D (gate/up input, down output) */
   uint32_t inter;        /* expert intermediate width I */

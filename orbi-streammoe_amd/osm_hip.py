@@ -24,6 +24,7 @@ LIB_PATH = os.path.join(HERE, "libosm_hip.so")
 OSM_OK, OSM_E_INVALID, OSM_E_RUNTIME, OSM_E_DEVICE = 0, 1, 2, 3
 PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED, PATH_SINGLE_LAUNCH = 0, 1, 2, 3
 F32, F16, BF16 = 0, 1, 2
+AFFINE_Q8 = 3  # router / shared-gate dtype: MLX affine 8-bit (osm_affine_q8_c)
 
 
 class OsmError(RuntimeError):
@@ -525,23 +526,45 @@ class ExpertSlab(_Handle):
         check(load().osm_expert_slab_synthesize(self.h, seed))
 
 
+class AffineQ8(ctypes.Structure):
+    """osm_affine_q8_c: one MLX affine 8-bit matrix [rows, cols]."""
+
+    _fields_ = [("packed", c_void_p), ("scales", c_void_p), ("biases", c_void_p), ("group", c_uint32)]
+
+    @classmethod
+    def of(cls, packed, scales, biases, group):
+        arrs = (_c(packed, np.uint32), _c(scales, np.float32), _c(biases, np.float32))
+        obj = cls(arrs[0].ctypes.data, arrs[1].ctypes.data, arrs[2].ctypes.data, group)
+        obj._arrays = arrs  # the views must outlive the struct
+        return obj
+
+
 class MoeLayer(_Handle):
-    """Layer state of QwenCheckpointSparseMoeLayer / QwenCheckpointMoeSublayer."""
+    """Layer state of QwenCheckpointSparseMoeLayer / QwenCheckpointMoeSublayer.
+    router_dtype AFFINE_Q8: router and shared_gate_vec are (packed, scales,
+    biases, group) tuples of [E, D] and [1, D] 8-bit matrices."""
 
     _destroy = "osm_moe_layer_destroy"
 
     def __init__(self, ctx, g: Geometry, expert_count, top_k, router, router_dtype=BF16, shared_gate_vec=None,
                  norm_weight=None, shared_blob=None, max_tokens=1, norm_topk_prob=True, rms_eps=1e-6):
-        rdt = {F32: np.float32, F16: np.float16, BF16: np.uint16}[router_dtype]
-        r = _c(router, rdt)
         has_shared = shared_blob is not None
         cfg = MoeConfig(g, expert_count, top_k, 1 if norm_topk_prob else 0, 1 if has_shared else 0, rms_eps)
-        sg = _c(shared_gate_vec, rdt) if shared_gate_vec is not None else None
+        if router_dtype == AFFINE_Q8:
+            r = AffineQ8.of(*router)
+            sg = AffineQ8.of(*shared_gate_vec) if shared_gate_vec is not None else None
+            rp = ctypes.cast(ctypes.pointer(r), c_void_p)
+            sp = ctypes.cast(ctypes.pointer(sg), c_void_p) if sg is not None else None
+        else:
+            rdt = {F32: np.float32, F16: np.float16, BF16: np.uint16}[router_dtype]
+            r = _c(router, rdt)
+            sg = _c(shared_gate_vec, rdt) if shared_gate_vec is not None else None
+            rp, sp = _p(r), (_p(sg) if sg is not None else None)
         nw = _c(norm_weight, np.float32) if norm_weight is not None else None
         sb = np.ascontiguousarray(shared_blob).view(np.uint8) if has_shared else None
         h = c_void_p()
         check(load().osm_moe_layer_create(
-            ctx.h, ctypes.byref(cfg), _p(r), router_dtype, _p(sg) if sg is not None else None,
+            ctx.h, ctypes.byref(cfg), rp, router_dtype, sp,
             _p(nw) if nw is not None else None, _p(sb) if sb is not None else None,
             sb.size if sb is not None else 0, max_tokens, ctypes.byref(h)))
         super().__init__(h)
