@@ -360,6 +360,28 @@ size_t osm_expert_storage_stride(osm_expert_storage s);
 int osm_expert_storage_read(osm_expert_storage s, const uint32_t* layers, const uint32_t* experts,
                             void* const* destinations, size_t count, size_t destination_bytes);
 
+/* An expert's qpack cache slot bound by section name: the entries of the
+ * container's section table (container/qpack.hpp:15-21) for gate_proj,
+ * up_proj and down_proj (.weight / .scales / .biases), offsets within the
+ * slot. The checks are bind_qpack_q4_projection's
+ * (vulkan_qpack_expert.cpp:149-239), plus scales/biases in the geometry's
+ * metadata dtype. The nine sections are copied into `blob` (blob_bytes =
+ * osm_expert_blob_bytes(g)) in the blob's order; *identity (optional) is 1
+ * when the slot already is the blob, as in the official contiguous layout,
+ * so its first blob_bytes bytes can be uploaded unchanged. slot and blob
+ * may be NULL to validate only. OSM_E_RUNTIME for a section table that
+ * fails a check, OSM_E_INVALID for bad arguments or a metadata dtype
+ * other than the geometry's. */
+typedef struct osm_qpack_section_c {
+  const char* name;  /* e.g. "gate_proj.weight" */
+  const char* dtype; /* "U32", "F32", "F16" or "BF16" */
+  uint32_t rank;     /* 2 */
+  uint64_t rows, cols, offset, size;
+} osm_qpack_section_c;
+int osm_qpack_expert_repack(const osm_expert_geometry_c* g, const osm_qpack_section_c* sections, size_t n,
+                            uint64_t slot_stride, const void* slot, void* blob, size_t blob_bytes,
+                            int* identity);
+
 typedef struct osm_host_cache_stats {
   uint64_t hits, misses, allocated_slots, capacity_slots, logical_bytes, budget_bytes;
 } osm_host_cache_stats;

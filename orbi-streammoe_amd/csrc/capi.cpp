@@ -834,6 +834,28 @@ int osm_expert_storage_read(osm_expert_storage s, const uint32_t* layers, const 
   OSM_GUARD_END
 }
 
+// ---- qpack slot binding ---------------------------------------------------------
+int osm_qpack_expert_repack(const osm_expert_geometry_c* g, const osm_qpack_section_c* sections, size_t n,
+                            uint64_t slot_stride, const void* slot, void* blob, size_t blob_bytes,
+                            int* identity) {
+  OSM_GUARD_BEGIN
+  if (!g || (!sections && n)) return fail(OSM_E_INVALID, "null argument");
+  std::vector<osm::QpackSectionView> views(n);
+  for (size_t i = 0; i < n; ++i) {
+    if (!sections[i].name || !sections[i].dtype) return fail(OSM_E_INVALID, "qpack section without name or dtype");
+    views[i] = {sections[i].name, sections[i].dtype, sections[i].rank, sections[i].rows, sections[i].cols,
+                sections[i].offset, sections[i].size};
+  }
+  const auto plan = osm::plan_qpack_expert(views, slot_stride, geom_of(g));
+  if (identity) *identity = plan.identity ? 1 : 0;
+  if (slot || blob) {
+    if (!slot || !blob || blob_bytes < plan.blob_bytes) return fail(OSM_E_INVALID, "qpack repack: slot and a blob of osm_expert_blob_bytes needed");
+    osm::repack_qpack_expert(plan, static_cast<const std::byte*>(slot), static_cast<std::byte*>(blob));
+  }
+  return ok();
+  OSM_GUARD_END
+}
+
 // ---- host L1 cache --------------------------------------------------------------
 int osm_host_cache_create(size_t stride, size_t budget_bytes, size_t minimum_slots, int pinned,
                           osm_read_experts_fn read, void* user, osm_host_cache* out) {

@@ -9,6 +9,7 @@
 // csrc/device/osm_device.h.
 #pragma once
 
+#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <filesystem>
@@ -18,6 +19,7 @@
 #include <optional>
 #include <span>
 #include <string>
+#include <string_view>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -368,6 +370,30 @@ class PosixPreadExpertStorage final : public ExpertStorage {
   std::vector<int> fds_;
   std::mutex mutex_;
 };
+
+// One entry of a qpack container's section table (container/qpack.hpp:15-21),
+// as it applies to one expert's cache slot.
+struct QpackSectionView {
+  std::string_view name, dtype;  // "gate_proj.weight", "U32" / "F32" / "F16" / "BF16"
+  std::uint32_t rank = 2;
+  std::uint64_t rows = 0, cols = 0;
+  std::uint64_t offset = 0, size = 0;  // within the slot, bytes
+};
+// Where each of the blob's nine sections comes from in the slot, in blob
+// order; identity when the slot already is the blob.
+struct QpackExpertPlan {
+  std::array<std::uint64_t, 9> src{};
+  std::array<std::size_t, 9> dst{};
+  std::array<std::size_t, 9> bytes{};
+  std::size_t blob_bytes = 0;
+  bool identity = false;
+};
+// bind_qpack_q4_projection's checks (vulkan_qpack_expert.cpp:149-239) for
+// the three projections against `g`; throws std::runtime_error (or
+// std::invalid_argument for a metadata dtype other than the geometry's).
+[[nodiscard]] QpackExpertPlan plan_qpack_expert(std::span<const QpackSectionView> sections,
+                                                std::uint64_t slot_stride, const osm_expert_geometry& g);
+void repack_qpack_expert(const QpackExpertPlan& plan, const std::byte* slot, std::byte* blob);
 
 struct ExpertCacheEntry {
   ExpertId id{};

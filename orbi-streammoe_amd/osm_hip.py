@@ -150,6 +150,7 @@ _PROTOTYPES = {
     "osm_host_cache_destroy": (None, [_H]),
     "osm_host_cache_create_with_storage": (c_int, [_H, c_size_t, c_size_t, c_int, POINTER(_H)]),
     "osm_pread_storage_create": (c_int, [c_char_p, c_uint32, c_uint32, c_size_t, POINTER(_H)]),
+    "osm_qpack_expert_repack": (c_int, [POINTER(Geometry), c_void_p, c_size_t, c_uint64, c_void_p, c_void_p, c_size_t, POINTER(c_int)]),
     "osm_expert_storage_destroy": (None, [_H]),
     "osm_expert_storage_stride": (c_size_t, [_H]),
     "osm_expert_storage_read": (c_int, [_H, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
@@ -709,6 +710,32 @@ class ExpertStore(_Handle):
 
     def synthesize(self, ctx, seed):
         check(load().osm_expert_store_synthesize(ctx.h, self.h, seed))
+
+
+class QpackSection(ctypes.Structure):
+    """osm_qpack_section_c: one entry of a qpack section table."""
+
+    _fields_ = [("name", c_char_p), ("dtype", c_char_p), ("rank", c_uint32), ("rows", c_uint64),
+                ("cols", c_uint64), ("offset", c_uint64), ("size", c_uint64)]
+
+
+def qpack_expert_repack(g: Geometry, sections, slot_stride, slot=None):
+    """sections: dicts with name, dtype, shape (rows, cols), offset, size.
+    Returns (blob or None, identity)."""
+    arr = (QpackSection * max(len(sections), 1))(*[
+        QpackSection(s["name"].encode(), s["dtype"].encode(), len(s["shape"]), s["shape"][0],
+                     s["shape"][1] if len(s["shape"]) > 1 else 0, s["offset"], s["size"]) for s in sections])
+    ident = c_int(0)
+    blob = None
+    if slot is not None:
+        sl = np.ascontiguousarray(slot).view(np.uint8)
+        blob = np.zeros(expert_blob_bytes(g), np.uint8)
+        check(load().osm_qpack_expert_repack(ctypes.byref(g), ctypes.cast(arr, c_void_p), len(sections), slot_stride,
+                                             _p(sl), _p(blob), blob.size, ctypes.byref(ident)))
+    else:
+        check(load().osm_qpack_expert_repack(ctypes.byref(g), ctypes.cast(arr, c_void_p), len(sections), slot_stride,
+                                             None, None, 0, ctypes.byref(ident)))
+    return blob, bool(ident.value)
 
 
 class PreadStorage(_Handle):
