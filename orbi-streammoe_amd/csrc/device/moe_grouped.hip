@@ -268,34 +268,45 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     float* __restrict__ pair_w, Tile* __restrict__ tiles, uint32_t* __restrict__ tile_rows,
     uint32_t* __restrict__ tile_count, uint32_t max_tiles) {
   __shared__ uint32_t counts[kMaxBuckets], offsets[kMaxBuckets], cursor[kMaxBuckets], tbase[kMaxBuckets];
-  __shared__ uint32_t scan[kBucketThreads];
-  const uint32_t tid = threadIdx.x;
+  __shared__ uint32_t wave_total[kBucketThreads / kWave];
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const uint32_t nb = E + (nslot > k ? 1u : 0u);
   const uint32_t P = T * nslot;
   for (uint32_t b = tid; b < nb; b += kBucketThreads) counts[b] = 0u, cursor[b] = 0u;
   __syncthreads();
+  // Routed pairs only: the shared expert's bucket (E) holds one pair per
+  // token, in token order, so it needs no counting or cursor.
+#pragma unroll 4
   for (uint32_t i = tid; i < P; i += kBucketThreads) {
     const uint32_t t = i / nslot, j = i % nslot;
-    uint32_t e = j < k ? ids[static_cast<size_t>(t) * k + j] : E;
-    e = e < nb ? e : nb - 1u;
-    atomicAdd(&counts[e], 1u);
+    if (j < k) {
+      uint32_t e = ids[static_cast<size_t>(t) * k + j];
+      e = e < E ? e : E - 1u;
+      atomicAdd(&counts[e], 1u);
+    }
   }
+  if (nb > E && tid == 0) counts[E] = T;
   __syncthreads();
   // Exclusive scans of the counts and of the tile counts, two buckets per
-  // thread at most (nb <= 1025).
+  // thread at most (nb <= 1025): a wavefront scan, then each thread adds the
+  // totals of the wavefronts before its own.
   for (int pass = 0; pass < 2; ++pass) {
     uint32_t local = 0;
     for (uint32_t b = tid * 2u; b < tid * 2u + 2u && b < nb; ++b)
       local += pass == 0 ? counts[b] : (counts[b] + kTileTokens - 1u) / kTileTokens;
-    scan[tid] = local;
-    __syncthreads();
-    for (uint32_t off = 1; off < kBucketThreads; off <<= 1) {
-      const uint32_t v = tid >= off ? scan[tid - off] : 0u;
-      __syncthreads();
-      scan[tid] += v;
-      __syncthreads();
+    uint32_t incl = local;
+    for (uint32_t off = 1; off < kWave; off <<= 1) {
+      const uint32_t v = __shfl_up(incl, off, kWave);
+      incl += lane >= off ? v : 0u;
     }
-    uint32_t run = scan[tid] - local;
+    if (lane == kWave - 1u) wave_total[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (uint32_t w = 0; w < kBucketThreads / kWave; ++w) {
+      before += w < wave ? wave_total[w] : 0u;
+      all += wave_total[w];
+    }
+    uint32_t run = before + incl - local;
     for (uint32_t b = tid * 2u; b < tid * 2u + 2u && b < nb; ++b) {
       if (pass == 0) {
         offsets[b] = run;
@@ -306,11 +317,10 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
       }
     }
     if (pass == 1) {
-      if (tid == kBucketThreads - 1u) *tile_count = scan[tid];
+      if (tid == 0) *tile_count = all;
       // Tiles past the last real one are empty (count 0): the GEMM grids
       // span the whole capacity and their workgroups read only their tile.
-      for (uint32_t t = scan[kBucketThreads - 1u] + tid; t < max_tiles; t += kBucketThreads)
-        tiles[t] = Tile{fallback, 0u, 0u};
+      for (uint32_t t = all + tid; t < max_tiles; t += kBucketThreads) tiles[t] = Tile{fallback, 0u, 0u};
     }
     __syncthreads();
   }
@@ -326,11 +336,15 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
       tiles[tbase[b] + s] = tl;
     }
   }
+#pragma unroll 4
   for (uint32_t i = tid; i < P; i += kBucketThreads) {
     const uint32_t t = i / nslot, j = i % nslot;
-    uint32_t e = j < k ? ids[static_cast<size_t>(t) * k + j] : E;
-    e = e < nb ? e : nb - 1u;
-    const uint32_t in_bucket = atomicAdd(&cursor[e], 1u);
+    uint32_t e = E;  // the shared expert's bucket
+    if (j < k) {
+      e = ids[static_cast<size_t>(t) * k + j];
+      e = e < E ? e : E - 1u;  // as counted above
+    }
+    const uint32_t in_bucket = e == E ? t : atomicAdd(&cursor[e], 1u);
     const uint32_t pos = offsets[e] + in_bucket;
     tile_rows[(tbase[e] + in_bucket / kTileTokens) * kTileTokens + in_bucket % kTileTokens] = t;
     pair_pos[i] = pos;
@@ -842,6 +856,35 @@ __global__ void combine_kernel(const float* __restrict__ partial, uint32_t nspli
   }
 }
 
+// The same sums four columns per thread with 16-byte loads (D % 4 == 0,
+// every row 16-byte aligned); each column's additions keep the order above.
+__global__ void combine4_kernel(const float* __restrict__ partial, uint32_t nsplit, uint32_t P,
+                                const uint32_t* __restrict__ pair_pos, uint32_t T, uint32_t D, uint32_t nslot,
+                                const float* __restrict__ residual, float* __restrict__ y) {
+  const uint32_t D4 = D / 4u;
+  const size_t n = static_cast<size_t>(T) * D4;
+  const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint32_t t = static_cast<uint32_t>(i / D4), r4 = static_cast<uint32_t>(i % D4);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t j = 0; j < nslot; ++j) {
+      const size_t pos = pair_pos[t * nslot + j];
+      for (uint32_t sp = 0; sp < nsplit; ++sp) {
+        const float4 v = reinterpret_cast<const float4*>(partial + (static_cast<size_t>(sp) * P + pos) * D)[r4];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+    }
+    if (residual) {
+      const float4 x = reinterpret_cast<const float4*>(residual)[i];
+      acc = make_float4(x.x + acc.x, x.y + acc.y, x.z + acc.z, x.w + acc.w);
+    }
+    reinterpret_cast<float4*>(y)[i] = acc;
+  }
+}
+
 // Columns per K range: the largest of 512 / 256 / 128 that divides K.
 // Columns per K range of the router GEMM: the widest of 512 / 256 / 128 that
 // divides the hidden size (a multiple of 128 on the grouped path).
@@ -1055,9 +1098,13 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   const uint32_t dn_splits = osmd_moe_grouped_splits(&g, I);
   set_item_blocks(sp, (D + split_rows<1>() - 1) / split_rows<1>(), dn_splits);
   launch_split<1>(sp, st);
-  combine_kernel<<<blocks_for(static_cast<size_t>(T) * D, 4096), 256, 0, st>>>(
-      a->partial, dn_splits, P, a->pair_pos, T, D, nslot,
-      (m.flags & OSMD_MOE_RESIDUAL) ? static_cast<const float*>(m.x) : nullptr, m.y);
+  const float* residual = (m.flags & OSMD_MOE_RESIDUAL) ? static_cast<const float*>(m.x) : nullptr;
+  if (D % 4u == 0u && ((reinterpret_cast<uintptr_t>(m.y) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0u)
+    combine4_kernel<<<blocks_for(static_cast<size_t>(T) * (D / 4u), 4096), 256, 0, st>>>(
+        a->partial, dn_splits, P, a->pair_pos, T, D, nslot, residual, m.y);
+  else
+    combine_kernel<<<blocks_for(static_cast<size_t>(T) * D, 4096), 256, 0, st>>>(
+        a->partial, dn_splits, P, a->pair_pos, T, D, nslot, residual, m.y);
   return launch_status();
 }
 
