@@ -154,14 +154,37 @@ __device__ __forceinline__ float nib_dot8(uint32_t w, const float* x) {
   return nib_dot8_s24(w, x, opaque_zero()) * kTwo24;
 }
 
-// 32 columns held by one 16-byte chunk: four independent chains of eight.
+// 32 columns held by one 16-byte chunk, in two chains. Masking a word in
+// place with 0x00F000F0 leaves nibbles 1 and 5 as the f16 subnormals q * 2^-20
+// (bits 4-7 of each half), so with w and w >> 8 every nibble is one AND away
+// from an f16: five instructions per word unpack eight nibbles, against seven
+// when each nibble is shifted down first. Chain a holds the 2^-24 products
+// (nibbles 0, 4, 2, 6 of each word), chain b the 2^-20 ones (1, 5, 3, 7);
+// each is the plain fp32 chain times its power of two, and the two are
+// scaled back and added once.
+constexpr float kTwo20 = 1048576.0f;
+
 __device__ __forceinline__ float nib_dot32(uint4 q, const float* x) {
-  const float z = opaque_zero();
-  float d = nib_dot8_s24(q.x, x, z);
-  d += nib_dot8_s24(q.y, x + 8, z);
-  d += nib_dot8_s24(q.z, x + 16, z);
-  d += nib_dot8_s24(q.w, x + 24, z);
-  return d * kTwo24;
+  float a = opaque_zero(), b = opaque_zero();
+  const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = w4[i], t = w >> 8;
+    const float* xi = x + 8 * i;
+    const uint32_t p0 = w & 0x000F000Fu;  // nibbles 0, 4
+    const uint32_t p1 = w & 0x00F000F0u;  // nibbles 1, 5 (times 16)
+    const uint32_t p2 = t & 0x000F000Fu;  // nibbles 2, 6
+    const uint32_t p3 = t & 0x00F000F0u;  // nibbles 3, 7 (times 16)
+    a = fmaf(f16_lo(p0), xi[0], a);
+    b = fmaf(f16_lo(p1), xi[1], b);
+    a = fmaf(f16_lo(p2), xi[2], a);
+    b = fmaf(f16_lo(p3), xi[3], b);
+    a = fmaf(f16_hi(p0), xi[4], a);
+    b = fmaf(f16_hi(p1), xi[5], b);
+    a = fmaf(f16_hi(p2), xi[6], a);
+    b = fmaf(f16_hi(p3), xi[7], b);
+  }
+  return fmaf(b, kTwo20, a * kTwo24);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) {
