@@ -300,6 +300,16 @@ int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_sl
  * chained == 0: layer i reads x_dev + i*tokens*D and writes y_dev +
  * i*tokens*D (MoE form). Layer i uses layers[i] and slab layer
  * slab_layers[i]. */
+/* The decoder stack's MoE sublayers through the capped cache
+ * (checkpoint_decoder_stack.cpp:191-204 with run_qwen_sparse_moe_vulkan_accum
+ * per layer): layer i runs layers[i] on cache layer cache_layers[i] as a
+ * sublayer (RMSNorm, MoE, residual), on the previous layer's output; x and
+ * y are host [tokens, D]. pick_ids / pick_weights (both or neither):
+ * [n_layers][tokens][k] routed picks given from outside, as
+ * osm_moe_layer_run_cached_picks takes them; NULL routes on the device. */
+int osm_moe_run_cached_layers(osm_context ctx, const osm_moe_layer* layers, const uint32_t* cache_layers,
+                              uint32_t n_layers, osm_expert_cache cache, const float* x, uint32_t tokens,
+                              const uint32_t* pick_ids, const float* pick_weights, float* y);
 int osm_moe_decode_layers(osm_context ctx, const osm_moe_layer* layers,
                           const uint32_t* slab_layers, uint32_t n_layers, osm_expert_slab slab,
                           const float* x_dev, float* y_dev, float* scratch_dev, uint32_t tokens,

@@ -612,6 +612,35 @@ int osm_moe_layer_run_cached_picks(osm_context ctx, osm_moe_layer l, osm_expert_
   OSM_GUARD_END
 }
 
+int osm_moe_run_cached_layers(osm_context ctx, const osm_moe_layer* layers, const uint32_t* cache_layers,
+                              uint32_t n_layers, osm_expert_cache cache, const float* x, uint32_t tokens,
+                              const uint32_t* pick_ids, const float* pick_weights, float* y) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !layers || !cache_layers || !cache || !x || !y || n_layers == 0 || tokens == 0 ||
+      (!pick_ids) != (!pick_weights))
+    return fail(OSM_E_INVALID, "invalid arguments");
+  const std::size_t D = layers[0] ? layers[0]->layer.config().geometry.hidden : 0;
+  std::vector<float> cur(x, x + static_cast<std::size_t>(tokens) * D);
+  for (uint32_t i = 0; i < n_layers; ++i) {
+    if (!layers[i] || layers[i]->layer.config().geometry.hidden != D)
+      return fail(OSM_E_INVALID, "layers must share one hidden size");
+    const std::size_t K = layers[i]->layer.config().top_k;
+    osm::HipMoePicks picks;
+    if (pick_ids) {
+      // Every layer's picks sit at the same stride, so the layers must agree on k.
+      if (K != layers[0]->layer.config().top_k) return fail(OSM_E_INVALID, "given picks need one top_k");
+      picks = {pick_ids + static_cast<std::size_t>(i) * tokens * K, pick_weights + static_cast<std::size_t>(i) * tokens * K};
+    }
+    auto r = osm::run_qwen_sparse_moe_hip(ctx->ctx, *cache->cache, layers[i]->layer, cache_layers[i], cur, true,
+                                          pick_ids ? &picks : nullptr);
+    if (!r.executed) return fail(OSM_E_INVALID, "layer " + std::to_string(i) + ": " + r.diagnostic);
+    cur = std::move(r.values);
+  }
+  std::memcpy(y, cur.data(), cur.size() * sizeof(float));
+  return ok();
+  OSM_GUARD_END
+}
+
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,
                                 uint32_t tokens, int sublayer) {

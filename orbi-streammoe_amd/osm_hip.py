@@ -150,6 +150,7 @@ _PROTOTYPES = {
     "osm_host_cache_destroy": (None, [_H]),
     "osm_host_cache_create_with_storage": (c_int, [_H, c_size_t, c_size_t, c_int, POINTER(_H)]),
     "osm_pread_storage_create": (c_int, [c_char_p, c_uint32, c_uint32, c_size_t, POINTER(_H)]),
+    "osm_moe_run_cached_layers": (c_int, [_H, c_void_p, c_void_p, c_uint32, _H, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p]),
     "osm_qpack_expert_repack": (c_int, [POINTER(Geometry), c_void_p, c_size_t, c_uint64, c_void_p, c_void_p, c_size_t, POINTER(c_int)]),
     "osm_expert_storage_destroy": (None, [_H]),
     "osm_expert_storage_stride": (c_size_t, [_H]),
@@ -855,6 +856,22 @@ class ExpertCache(_Handle):
     @property
     def bytes_filled(self) -> int:
         return load().osm_expert_cache_bytes_filled(self.h)
+
+
+def run_cached_layers(ctx, layers, cache_layers, cache, x, picks=None) -> np.ndarray:
+    """Chained sublayers through the capped cache in one native call. picks:
+    None (route on the device) or (ids [n][tokens][k], weights [n][tokens][k])."""
+    xv = _c(x, np.float32).reshape(-1, layers[0].g.hidden)
+    hs = (c_void_p * len(layers))(*[m.h.value if isinstance(m.h, c_void_p) else m.h for m in layers])
+    cl = _c(cache_layers, np.uint32)
+    y = np.empty_like(xv)
+    ids = w = None
+    if picks is not None:
+        ids, w = _c(picks[0], np.uint32), _c(picks[1], np.float32)
+    check(load().osm_moe_run_cached_layers(ctx.h, ctypes.cast(hs, c_void_p), _p(cl), len(layers), cache.h, _p(xv),
+                                           xv.shape[0], _p(ids) if ids is not None else None,
+                                           _p(w) if w is not None else None, _p(y)))
+    return y
 
 
 class CachePolicy(_Handle):

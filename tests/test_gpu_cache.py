@@ -194,3 +194,30 @@ def test_cached_decode_from_pread_storage(ctx, tmp_path):
         ref = moe.run_slab(slab, 0, x[t], sublayer=t % 2 == 0)
         assert np.array_equal(got["ids"], ref["ids"]) and np.array_equal(got["out"], ref["out"])
     assert cache.stats()["evictions"] > 0 and host.stats()["misses"] > 0
+
+
+def test_cached_layer_stack_matches_layer_calls(ctx):
+    # The native stack of cached sublayers against one call per layer: the
+    # same outputs bit for bit, with given picks and with device routing.
+    seed, D, I, G, E, k, layers = 25, 256, 128, 64, 32, 4, 3
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    store = osm_hip.ExpertStore(g, layers, E)
+    store.synthesize(ctx, seed)
+    moes = [osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, l, E, D), osm_hip.BF16,
+                             O.synth_shared_gate_bf16(seed, l, D), O.synth_norm_weight(seed, l, D),
+                             O.synth_expert_blob(seed, l, O.SHARED_EXPERT_ID, D, I, G), max_tokens=1)
+            for l in range(layers)]
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(layers)]).astype(np.uint32).reshape(layers, 1, k)
+    w = rng.random((layers, 1, k)).astype(np.float32)
+    x = O.synth_tokens(seed, 0, 1, D)
+    for picks in ((ids, w), None):
+        a = osm_hip.ExpertCache(ctx, 64 * store.stride, store=store)
+        b = osm_hip.ExpertCache(ctx, 64 * store.stride, store=store)
+        got = osm_hip.run_cached_layers(ctx, moes, list(range(layers)), a, x, picks)
+        ref = x
+        for l in range(layers):
+            p = (ids[l], w[l]) if picks is not None else None
+            ref = moes[l].run_cached(b, l, ref, sublayer=True, picks=p)["out"]
+        assert np.array_equal(got, ref)
+        assert a.stats()["misses"] == b.stats()["misses"] > 0
