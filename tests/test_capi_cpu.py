@@ -77,3 +77,19 @@ def test_generator_statistics_and_determinism():
     s_, b_ = secs[0][1], secs[0][2]
     assert np.all(s_ >= 0) and abs(np.mean(s_) - 0.02 * np.sqrt(2 / np.pi)) < 0.002
     assert abs(np.mean(b_ + 8 * s_)) < 0.001 and abs(np.std(b_ + 8 * s_) - 0.002) < 0.0005
+
+
+def test_argument_checks_before_any_device_work():
+    # Entry points that reject their arguments before touching a device: the
+    # native cached layer stack, the qpack binding and the pread storage.
+    import ctypes
+    lib = osm_hip.load()
+    st = lib.osm_moe_run_cached_layers(None, None, None, 0, None, None, 0, None, None, None)
+    assert st == osm_hip.OSM_E_INVALID and osm_hip.last_error()
+    g = osm_hip.geometry(256, 128, 64, osm_hip.BF16)
+    assert lib.osm_qpack_expert_repack(ctypes.byref(g), None, 3, 0, None, None, 0, None) == osm_hip.OSM_E_INVALID
+    h = ctypes.c_void_p()
+    assert lib.osm_pread_storage_create(None, 1, 1, 16, ctypes.byref(h)) == osm_hip.OSM_E_INVALID
+    assert lib.osm_pread_storage_create(b"/nonexistent", 0, 1, 16, ctypes.byref(h)) == osm_hip.OSM_E_INVALID
+    assert lib.osm_expert_storage_stride(None) == 0
+    assert lib.osm_host_cache_create_with_storage(None, 1 << 20, 1, 0, ctypes.byref(h)) == osm_hip.OSM_E_INVALID
