@@ -1380,8 +1380,23 @@ int osmd_moe_experts(const osmd_moe_args* a, osmd_stream s) {
   return r != 0 ? r : osmd_moe_down(a, s);
 }
 
+// From this many tokens on, the per-token decode selects in its own launch
+// (one workgroup per token) and gate/up reads the published slot pointers:
+// below, the launch costs more than the selection that every routed gate/up
+// workgroup repeats (µs per layer step, Qwen3-Next shape, integrated /
+// separate: 2 tokens 24.9 / 27.4, 8 tokens 54.6 / 55.8, 16 tokens 91-95 /
+// 87.1, 32 tokens 162 / 145). The selection code is the same, so are the bits.
+constexpr uint32_t kSeparateSelectMinTokens = 12;
+
 int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s) {
-  // With a complete expert table the selection runs inside gate_up.
+  if (a->expert_table && a->tokens >= kSeparateSelectMinTokens) {
+    const int r = osmd_moe_route(a, s);
+    if (r != 0) return r;
+    osmd_moe_args b = *a;
+    b.expert_table = nullptr;  // gate/up reads the slot pointers the selection published
+    return osmd_moe_experts(&b, s);
+  }
+  // Otherwise, with a complete expert table the selection runs inside gate_up.
   const int r = a->expert_table ? osmd_moe_router(a, s) : osmd_moe_route(a, s);
   return r != 0 ? r : osmd_moe_experts(a, s);
 }
