@@ -261,8 +261,8 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
 /* How decodes run (no counterpart in the reference, which pushes tokens
  * through the sublayer one at a time with 56 dispatches each,
  * src/session/greedy_token_session.cpp:170-192, routed_moe.cpp:254-430):
- * OSM_PATH_AUTO runs the three per-token kernels below 56 tokens and the
- * grouped GEMMs from 56 tokens on (group 32/64/128, hidden and intermediate
+ * OSM_PATH_AUTO runs the three per-token kernels below 40 tokens and the
+ * grouped GEMMs from 40 tokens on (group 32/64/128, hidden and intermediate
  * multiples of 128, 16-byte aligned input); OSM_PATH_PER_TOKEN always runs
  * the per-token kernels; OSM_PATH_GROUPED always buckets (token, slot) pairs
  * by expert and reads each expert once; OSM_PATH_SINGLE_LAUNCH runs one-token

@@ -50,7 +50,7 @@ constexpr uint32_t kBlockRows = 16;   // MFMA columns (weight rows)
 constexpr uint32_t kGroupedWaves = 4;
 constexpr uint32_t kGroupedThreads = kGroupedWaves * kWave;
 constexpr uint32_t kRouterSplit = 3;
-constexpr uint32_t kRouterGemmMinTokens = 64;
+constexpr uint32_t kRouterGemmMinTokens = 16;
 constexpr uint32_t kActSplit = 2;
 
 __device__ __forceinline__ uint16_t bf16_rne(float f) {
@@ -1008,9 +1008,11 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     xin = m.x_norm;
     xbf16 = false;
   }
-  // Up to 64 tokens the per-token router kernel (one wavefront per router
+  // Up to 16 tokens the per-token router kernel (one wavefront per router
   // row and token) has the shorter latency; beyond, the MFMA router GEMM,
-  // whose K-range planes the selection adds. One preparation serves both
+  // whose K-range planes the selection adds (grouped decode at 40 / 56 / 64
+  // tokens: 206 / 237 / 252 µs per layer step with the per-token router up
+  // to 64 tokens, 198 / 225 / 238 µs with the GEMM from 16). One preparation serves both
   // GEMMs: 3 bf16 terms per activation for the router, of which the expert
   // GEMMs read the first 2 (the group sums are of those 2).
   const bool router_gemm = m.router_dtype == OSM_META_BF16 && (xbf16 || T > kRouterGemmMinTokens);

@@ -679,11 +679,11 @@ struct HipMoeResult {
 // automatic takes the per-token kernels, and the grouped path from
 // kGroupedMinTokens tokens on, between the batch sizes where it was
 // measured to overtake the per-token kernels at the Qwen3-Next shape on
-// MI355X (us per layer, per-token vs grouped: 48 tokens 212 vs 220; 56: 236
-// vs 237; 64: 269 vs 254; 512: 2730 vs 387). single_launch with more than
-// one token runs the per-token kernels.
+// MI355X (us per layer, per-token vs grouped: 32 tokens 148-177 vs 176-182;
+// 40: 201-207 vs 198; 48: 213-218 vs 211; 64: 266-272 vs 239; 512: 2730 vs
+// 387). single_launch with more than one token runs the per-token kernels.
 enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2, single_launch = 3 };
-inline constexpr std::uint32_t kGroupedMinTokens = 56;
+inline constexpr std::uint32_t kGroupedMinTokens = 40;
 
 class HipMoeLayer {
  public:
