@@ -20,7 +20,9 @@ from test_gpu_moe import QwenLayer, assert_token_parity
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("tokens", [16, 48])
+# 37 tokens end in a ragged 5-token tile of the router GEMM (from 17 tokens)
+# and of the bucketed expert tiles.
+@pytest.mark.parametrize("tokens", [16, 37, 48])
 def test_grouped_decode_qwen_shape(ctx, tokens):
     seed = 41
     L = QwenLayer(ctx, seed, max_tokens=64)
@@ -103,11 +105,12 @@ def test_grouped_router_gemm_planes_no_shared(ctx):
         assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
 
 
-def test_prefill_bf16_chunk(ctx):
-    # A 256-token prefill chunk in bf16 at the Qwen3-Next shape: every token
-    # against the per-token kernels on the widened input, a sample of tokens
-    # against the oracle.
-    seed, T = 44, 256
+@pytest.mark.parametrize("T", [256, 77, 1])
+def test_prefill_bf16_chunk(ctx, T):
+    # A prefill chunk in bf16 at the Qwen3-Next shape: every token against the
+    # per-token kernels on the widened input, a sample of tokens against the
+    # oracle. 77 and 1 tokens leave the last 16-token router tile ragged.
+    seed = 44
     L = QwenLayer(ctx, seed, max_tokens=T)
     xf = O.synth_tokens(seed, 9000, T, L.D)
     bits = ((xf.view(np.uint32) + 0x7FFF + ((xf.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
