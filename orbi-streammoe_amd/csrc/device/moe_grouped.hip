@@ -867,7 +867,28 @@ __global__ void combine4_kernel(const float* __restrict__ partial, uint32_t nspl
   for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
     const uint32_t t = static_cast<uint32_t>(i / D4), r4 = static_cast<uint32_t>(i % D4);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t j = 0; j < nslot; ++j) {
+    uint32_t j = 0;
+    if (nsplit == 1u) {
+      // One K range (the usual case): four slots' positions, then their rows,
+      // are loaded before the adds, which keep slot order.
+      const float4* part4 = reinterpret_cast<const float4*>(partial);
+      for (; j + 4u <= nslot; j += 4u) {
+        size_t pos[4];
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) pos[q] = pair_pos[t * nslot + j + q];
+        float4 v[4];
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) v[q] = part4[pos[q] * D4 + r4];
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+          acc.x += v[q].x;
+          acc.y += v[q].y;
+          acc.z += v[q].z;
+          acc.w += v[q].w;
+        }
+      }
+    }
+    for (; j < nslot; ++j) {
       const size_t pos = pair_pos[t * nslot + j];
       for (uint32_t sp = 0; sp < nsplit; ++sp) {
         const float4 v = reinterpret_cast<const float4*>(partial + (static_cast<size_t>(sp) * P + pos) * D)[r4];
