@@ -906,7 +906,6 @@ __global__ void combine4_kernel(const float* __restrict__ partial, uint32_t nspl
   }
 }
 
-// Columns per K range: the largest of 512 / 256 / 128 that divides K.
 // Columns per K range of the router GEMM: the widest of 512 / 256 / 128 that
 // divides the hidden size (a multiple of 128 on the grouped path).
 uint32_t router_range(uint32_t D) { return D % 512u == 0 ? 512u : (D % 256u == 0 ? 256u : 128u); }

@@ -457,6 +457,12 @@ bool HipResidentExpertCache::contains(std::uint32_t layer, std::uint32_t expert)
   return impl_->policy.contains(layer, expert);
 }
 
+const std::uint8_t* HipResidentExpertCache::resident_blob(std::uint32_t layer, std::uint32_t expert) const noexcept {
+  const auto it = impl_->key_slot.find(LfuRecencyPolicy::make_key(layer, expert));
+  if (it == impl_->key_slot.end()) return nullptr;
+  return impl_->slab.as<const std::uint8_t>() + it->second * impl_->stride;
+}
+
 HipResidentExpertCacheStats HipResidentExpertCache::stats() const noexcept {
   const auto& p = impl_->policy;
   return {p.hits, p.misses, p.loads, p.evictions, p.resident_entries(), p.resident_bytes(),

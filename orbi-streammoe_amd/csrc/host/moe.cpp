@@ -694,7 +694,6 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
     // once for the copies, before the expert kernels (with given picks the
     // routing kernels run meanwhile: they read no expert slot).
     auto* host_ptrs = reinterpret_cast<const std::uint8_t**>(io + o_ptr);
-    std::unordered_set<std::uint64_t> needed;
     expert_cache.begin_fills();
     for (std::uint32_t t = 0; t < tokens; ++t) {
       for (std::size_t j = 0; j < K; ++j) {
@@ -712,11 +711,15 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
           r.diagnostic = "Qwen sparse MoE routed expert geometry mismatch";
           return r;
         }
-        host_ptrs[t * nslot + j] = e->device_blob();
-        needed.insert(LfuRecencyPolicy::make_key(layer, id));
       }
       if (nslot > K) host_ptrs[t * nslot + K] = m->shared_blob.as<const std::uint8_t>();
     }
+    // Every pick's slot from the final residency: a later miss of this batch
+    // can evict an expert admitted earlier in it and refill its slot (the
+    // expert, if picked again, was re-admitted elsewhere), so a pointer taken
+    // at the time of its get may name a slot that now holds another expert.
+    for (std::uint32_t t = 0; t < tokens; ++t)
+      for (std::size_t j = 0; j < K; ++j) host_ptrs[t * nslot + j] = expert_cache.resident_blob(layer, ids[t * K + j]);
     if (picks != nullptr) {
       rc = osmd_copy_d2d(dio, io, o_out, st);  // x, picks and slot pointers
       if (rc == 0) rc = osmd_moe_route(&ar, st);
@@ -729,8 +732,8 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
       r.diagnostic = hip_error("Qwen sparse MoE: routing or expert fills failed", rc);
       return r;
     }
-    for (const std::uint64_t key : needed)
-      if (!expert_cache.contains(layer, static_cast<std::uint32_t>(key & 0xFFFFFFFFU))) {
+    for (std::size_t i = 0; i < tokens * K; ++i)
+      if (host_ptrs[(i / K) * nslot + i % K] == nullptr) {
         r.diagnostic = "Qwen sparse MoE: the cache budget cannot hold every expert of this batch at once";
         return r;
       }

@@ -588,6 +588,8 @@ class HipResidentExpertCache {
   [[nodiscard]] HipValuesResult run(std::uint32_t layer, std::uint32_t expert,
                                     std::span<const float> x) noexcept;
   [[nodiscard]] bool contains(std::uint32_t layer, std::uint32_t expert) const noexcept;
+  // Device blob of a resident expert, or null; no tick, no policy update.
+  [[nodiscard]] const std::uint8_t* resident_blob(std::uint32_t layer, std::uint32_t expert) const noexcept;
   [[nodiscard]] HipResidentExpertCacheStats stats() const noexcept;
   // Fill batch: the misses of the gets between the two calls are copied
   // back to back on the side stream, which waits once (at the first miss)

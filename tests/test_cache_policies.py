@@ -113,6 +113,23 @@ def test_device_policy_reference_scenario():
         O.DeviceCachePolicy(4).get(0, 1, 5)
 
 
+def test_device_policy_batch_evicts_its_own_earlier_pick():
+    # One fill batch of two tokens picking [0, 1] and [1, 0] over a 4-expert
+    # budget warmed with 10-13 at frequency 2: 0 takes 10's place, 1 evicts 0
+    # (this batch's own frequency-1 fill), 1 hits, and 0 comes back in 11's
+    # place. Token 0's pick 0 is resident at the end, but not in the slot it
+    # was first copied to, which 1 now holds: a layer that runs every pick of
+    # the batch after all the gets must look its slot up again. Oracle and
+    # product policy agree on every step.
+    for p in (O.DeviceCachePolicy(4), osm_hip.CachePolicy(4)):
+        for _ in range(2):
+            for e in (10, 11, 12, 13):
+                p.get(0, e, 1)
+        steps = [p.get(0, e, 1) for e in (0, 1, 1, 0)]
+        assert steps == [(False, [10]), (False, [0]), (True, []), (False, [11])]
+        assert p.contains(0, 0) and p.contains(0, 1) and not p.contains(0, 10) and not p.contains(0, 11)
+
+
 # ---- product policies through the C ABI, against the oracle --------------------------------
 @pytest.mark.parametrize("seed", range(5))
 def test_product_policy_matches_oracle(seed):

@@ -167,6 +167,55 @@ def test_cached_batch_refills_its_own_slot(ctx):
     assert cache.stats()["evictions"] == 3  # both were all hits
 
 
+def test_cached_two_tokens_refill_an_earlier_pick(ctx):
+    # Two tokens in one call over a 4-expert budget warmed with 10-13 at
+    # frequency 2, picking [0, 1] and [1, 0]: 0 is copied into 10's slot,
+    # 1 evicts 0 and is copied into that same slot, 1 hits, and 0 is
+    # admitted again into 11's slot. Token 0's first pick must read 0's
+    # bytes from its final slot, not 1's from the slot it was first copied
+    # to. Both tokens against the oracle; counters against the restated
+    # policy.
+    seed, D, I, G, E, k = 26, 256, 128, 64, 16, 2
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    store = osm_hip.ExpertStore(g, 1, E)
+    store.synthesize(ctx, seed)
+    stride = store.stride
+    cache = osm_hip.ExpertCache(ctx, 4 * stride, store=store)
+    policy = O.DeviceCachePolicy(4 * stride)
+    sg_bits = O.synth_shared_gate_bf16(seed, 0, D)
+    shared = O.synth_expert_blob(seed, 0, O.SHARED_EXPERT_ID, D, I, G)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, 0, E, D), osm_hip.BF16, sg_bits, None, shared,
+                           max_tokens=2)
+    sg = O.bf16_bits_to_f32(sg_bits)
+
+    def run(ids, t0):
+        ids = np.array(ids, np.uint32)
+        n = ids.shape[0]
+        w = np.tile(np.array([0.625, 0.375], np.float32), (n, 1))
+        x = O.synth_tokens(seed, t0, n, D)
+        got = moe.run_cached(cache, 0, x.reshape(-1), picks=(ids, w))
+        for t in range(n):
+            for e in ids[t]:
+                policy.get(0, int(e), stride)
+            gate = float(got["shared_gate"][t])
+            ref_gate = 1.0 / (1.0 + np.exp(-np.dot(sg.astype(np.float64), x[t].astype(np.float64))))
+            assert abs(gate - ref_gate) <= 1e-6
+            ref = np.zeros(D, np.float64)
+            for j in range(k):
+                ref += float(w[t, j]) * O.expert_forward(store.blob_view(0, int(ids[t, j])), D, I, G, O.META_BF16, x[t])
+            ref += gate * O.expert_forward(shared, D, I, G, O.META_BF16, x[t])
+            assert rel_l2(got["out"][t], ref.astype(np.float32)) <= 1e-3, (ids.tolist(), t)
+
+    for t0 in range(2):
+        run([[10, 11]], 2 * t0)
+        run([[12, 13]], 2 * t0 + 1)
+    run([[0, 1], [1, 0]], 10)
+    st, po = cache.stats(), policy.stats()
+    for key in ("hits", "misses", "loads", "evictions", "resident_entries"):
+        assert st[key] == po[key], (key, st, po)
+    assert cache.contains(0, 0) and cache.contains(0, 1) and not cache.contains(0, 10)
+
+
 def test_cached_decode_from_pread_storage(ctx, tmp_path):
     # The whole miss path from files: pread storage -> pinned host L1 cache
     # -> HBM cache, against the all-resident decode (bit-identical outputs).

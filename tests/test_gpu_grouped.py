@@ -72,7 +72,7 @@ def test_grouped_small_f32_meta_f32_router_no_shared(ctx):
 
 
 def test_grouped_router_gemm_planes_no_shared(ctx):
-    # 96 fp32 tokens (more than 64: the router runs as the MFMA GEMM) with a
+    # 96 fp32 tokens (more than 16: the router runs as the MFMA GEMM) with a
     # bf16 router at hidden 768 (three 256-column K planes that the selection
     # adds) and no shared expert (the planes' shared-gate column is unused).
     # Ids, weights and logits against the per-token path (decode router
