@@ -258,6 +258,21 @@ int osm_moe_layer_run_cached_picks(osm_context ctx, osm_moe_layer l, osm_expert_
 int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                 uint32_t slab_layer, const float* x_dev, float* y_dev,
                                 uint32_t tokens, int sublayer);
+/* osm_moe_layer_decode_device without any device allocation. No counterpart
+ * in the reference; it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It runs the per-token kernels (same bits as
+ * osm_moe_layer_decode_device on OSM_PATH_PER_TOKEN) with their routing
+ * workspace in the library's fixed 4 MiB device array, one per GPU, held
+ * until the process ends, instead of the layer's. tokens must be in
+ * [1, osm_moe_layer_static_tokens_capacity(l)] (127 at the Qwen3-Next
+ * shape), else OSM_E_INVALID. Every call on one GPU shares that array, and
+ * the routing it leaves there is overwritten by the next call: calls that
+ * overlap in time on one GPU (several streams or contexts) race. */
+int osm_moe_layer_decode_device_static(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                                       uint32_t slab_layer, const float* x_dev, float* y_dev,
+                                       uint32_t tokens, int sublayer);
+uint32_t osm_moe_layer_static_tokens_capacity(osm_moe_layer l);
 /* How decodes run (no counterpart in the reference, which pushes tokens
  * through the sublayer one at a time with 56 dispatches each,
  * src/session/greedy_token_session.cpp:170-192, routed_moe.cpp:254-430):

@@ -653,6 +653,23 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
   return from_diag(r.executed, r.diagnostic);
 }
 
+int osm_moe_layer_decode_device_static(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
+                                       uint32_t slab_layer, const float* x_dev, float* y_dev,
+                                       uint32_t tokens, int sublayer) {
+  if (!ctx || !l || !slab) return fail(OSM_E_INVALID, "null argument");
+  const auto* table = slab->slab.device_table(slab_layer);
+  if (!table) return fail(OSM_E_INVALID, "slab layer out of range");
+  if (slab->slab.experts() != l->layer.config().expert_count)
+    return fail(OSM_E_INVALID, "slab expert count does not match the layer's router");
+  const char* diag = "";
+  const int rc = l->layer.decode_device_static(ctx->ctx, x_dev, y_dev, tokens, table, sublayer != 0, &diag);
+  return rc == OSM_OK ? ok() : fail(rc, diag);
+}
+
+uint32_t osm_moe_layer_static_tokens_capacity(osm_moe_layer l) {
+  return l ? l->layer.static_tokens_capacity() : 0U;
+}
+
 int osm_moe_layer_trace_single_launch(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                       uint32_t slab_layer, const float* x_dev, float* y_dev,
                                       uint64_t* trace_dev, uint32_t* shape) {

@@ -53,6 +53,14 @@ int osmd_event_synchronize(osmd_event e);
 int osmd_stream_wait_event(osmd_stream s, osmd_event e);
 int osmd_event_elapsed_ms(osmd_event start, osmd_event stop, float* ms);
 int osmd_device_synchronize(void);
+/* The fixed workspace of the decode entry point that allocates nothing: a
+ * file-scope device array of OSMD_STATIC_SCRATCH_BYTES, one copy per GPU,
+ * held until the process ends. _init looks its address up on `device`,
+ * which must be current (done at context creation); osmd_static_scratch
+ * returns it (looking it up then if _init did not run or failed). */
+#define OSMD_STATIC_SCRATCH_BYTES (4u << 20)
+int osmd_static_scratch_init(int device);
+int osmd_static_scratch(int device, void** out);
 /* Records what is enqueued on s between begin and end (nothing runs), then
  * instantiates it. A failed launch inside still needs the end call, which
  * then returns its error and no graph. Capture must not record memset nodes:

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "host_util.hpp"
+#include "osm_hip.h"
 #include "osm_hip.hpp"
 
 namespace osm {
@@ -364,6 +365,79 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
   r.executed = true;
   r.diagnostic = "HIP routed MoE decode enqueued";
   return r;
+}
+
+namespace {
+
+// The routing workspace of `tokens` rows, carved from the fixed array in
+// 256-byte aligned parts: logits, ids, weights, mass, shared gate,
+// normalised input, h, slot pointers.
+std::size_t static_workspace_bytes(const HipMoeLayerConfig& c, std::size_t tokens) {
+  auto al = [](std::size_t n) { return (n + 255U) & ~static_cast<std::size_t>(255U); };
+  const std::size_t nslot = c.top_k + (c.has_shared_expert ? 1U : 0U);
+  const std::size_t T = tokens;
+  return al(T * c.expert_count * 4U) + 2U * al(T * c.top_k * 4U) + 2U * al(T * 4U) +
+         al(T * c.geometry.hidden * 4U) + al(T * nslot * c.geometry.inter * 4U) + al(T * nslot * sizeof(void*));
+}
+
+}  // namespace
+
+std::uint32_t HipMoeLayer::static_tokens_capacity() const noexcept {
+  if (!valid()) return 0;
+  // One token's parts each round up to 256 bytes, so budget / (one token's
+  // bytes) is a lower bound; count up from it while the next one fits.
+  std::size_t t = OSMD_STATIC_SCRATCH_BYTES / static_workspace_bytes(impl_->cfg, 1U);
+  while (t < 65535U && static_workspace_bytes(impl_->cfg, t + 1U) <= OSMD_STATIC_SCRATCH_BYTES) ++t;
+  return static_cast<std::uint32_t>(t < 65535U ? t : 65535U);
+}
+
+int HipMoeLayer::decode_device_static(HipComputeContext& context, const float* x, float* y, std::uint32_t tokens,
+                                      const std::uint8_t* const* expert_table, bool sublayer,
+                                      const char** diagnostic) noexcept {
+  auto say = [&](const char* m) {
+    if (diagnostic) *diagnostic = m;
+  };
+  if (!valid()) return say("MoE layer is not valid"), OSM_E_INVALID;
+  if (!context.valid() || osmd_set_device(context.device()) != 0)
+    return say("HIP compute context is not valid or its device cannot be made current"), OSM_E_DEVICE;
+  if (context.device() != impl_->device) return say("MoE layer belongs to a different device"), OSM_E_INVALID;
+  if (x == nullptr || y == nullptr || expert_table == nullptr)
+    return say("MoE decode needs device input, output and expert table"), OSM_E_INVALID;
+  if (sublayer && impl_->norm_weight.get() == nullptr)
+    return say("MoE sublayer decode needs an RMSNorm weight"), OSM_E_INVALID;
+  if (tokens == 0 || tokens > static_tokens_capacity())
+    return say("MoE decode without allocation: token count must be in [1, static_tokens_capacity] "
+               "(the fixed 4 MiB workspace)"),
+           OSM_E_INVALID;
+  void* base = nullptr;
+  if (osmd_static_scratch(context.device(), &base) != 0 || base == nullptr)
+    return say("MoE decode without allocation: the fixed workspace's device address is unavailable"), OSM_E_DEVICE;
+  osmd_moe_args a = impl_->args(x, y, tokens, expert_table, sublayer);
+  auto al = [](std::size_t n) { return (n + 255U) & ~static_cast<std::size_t>(255U); };
+  const HipMoeLayerConfig& c = impl_->cfg;
+  const std::size_t T = tokens, nslot = impl_->nslot();
+  auto* p = static_cast<std::uint8_t*>(base);
+  a.logits = reinterpret_cast<float*>(p);
+  p += al(T * c.expert_count * 4U);
+  a.ids = reinterpret_cast<std::uint32_t*>(p);
+  p += al(T * c.top_k * 4U);
+  a.weights = reinterpret_cast<float*>(p);
+  p += al(T * c.top_k * 4U);
+  a.mass = reinterpret_cast<float*>(p);
+  p += al(T * 4U);
+  a.shared_gate = reinterpret_cast<float*>(p);
+  p += al(T * 4U);
+  a.x_norm = reinterpret_cast<float*>(p);
+  p += al(T * c.geometry.hidden * 4U);
+  a.h = reinterpret_cast<float*>(p);
+  p += al(T * nslot * c.geometry.inter * 4U);
+  a.slot_ptrs = reinterpret_cast<const std::uint8_t**>(p);
+  // Nothing here is read before this call writes it: the router writes the
+  // logits, shared gate and normalised input, the selection the picks and
+  // slot pointers, gate/up every slot's h.
+  if (osmd_moe_decode(&a, context.stream()) != 0) return say("MoE decode launch failed"), OSM_E_DEVICE;
+  say("");
+  return OSM_OK;
 }
 
 bool HipMoeLayer::set_path(HipMoePath path, std::string* diagnostic) noexcept {

@@ -718,6 +718,17 @@ class HipMoeLayer {
                                                 std::uint32_t tokens,
                                                 const std::uint8_t* const* expert_table,
                                                 bool sublayer) noexcept;
+  // decode_device through the per-token kernels with the routing workspace
+  // (logits, picks, normalised input, h, slot pointers) in the library's
+  // fixed per-device array instead of the layer's: no device memory is
+  // allocated or freed. Returns 0 or an osm_status; *diagnostic (static
+  // text) says why on failure, e.g. `tokens` beyond what the array holds
+  // (static_tokens_capacity). Calls on one device share the array, so calls
+  // that overlap in time on one device (two streams) race.
+  [[nodiscard]] int decode_device_static(HipComputeContext& context, const float* x, float* y,
+                                         std::uint32_t tokens, const std::uint8_t* const* expert_table,
+                                         bool sublayer, const char** diagnostic) noexcept;
+  [[nodiscard]] std::uint32_t static_tokens_capacity() const noexcept;
   // False (path unchanged) for single_launch on a layer whose shape cannot
   // run as one launch.
   bool set_path(HipMoePath path, std::string* diagnostic = nullptr) noexcept;

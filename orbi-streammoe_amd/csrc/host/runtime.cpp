@@ -112,6 +112,10 @@ std::optional<HipComputeContext> HipComputeContext::create(int device,
       set_diag(diagnostic, std::string("stream creation failed: ") + osmd_error_string(rc));
       return std::nullopt;
     }
+    // The no-allocation decode's fixed workspace: its address on this device,
+    // looked up once with the device current. A failure here is not fatal;
+    // that entry point looks it up again and reports the error itself.
+    (void)osmd_static_scratch_init(device);
     HipComputeContext ctx;
     ctx.impl_ = std::move(impl);
     set_diag(diagnostic, "HIP compute context created");

@@ -130,6 +130,8 @@ _PROTOTYPES = {
     "osm_moe_layer_run_cached": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_uint32, c_int, POINTER(MoeOutputs)]),
     "osm_moe_layer_run_cached_picks": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_uint32, c_int, c_void_p, c_void_p, POINTER(MoeOutputs)]),
     "osm_moe_layer_decode_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
+    "osm_moe_layer_decode_device_static": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int]),
+    "osm_moe_layer_static_tokens_capacity": (c_uint32, [_H]),
     "osm_moe_decode_layers": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_layer_launch_phase": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int, c_int]),
     "osm_moe_layer_set_path": (c_int, [_H, c_int]),
@@ -608,6 +610,16 @@ class MoeLayer(_Handle):
 
     def decode_device(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer=False):
         check(load().osm_moe_layer_decode_device(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0))
+
+    def decode_device_static(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer=False):
+        """decode_device with no device allocation: the per-token kernels with
+        their workspace in the library's fixed per-device array."""
+        check(load().osm_moe_layer_decode_device_static(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens,
+                                                        1 if sublayer else 0))
+
+    @property
+    def static_tokens_capacity(self) -> int:
+        return int(load().osm_moe_layer_static_tokens_capacity(self.h))
 
     def set_path(self, path):
         """PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED or PATH_SINGLE_LAUNCH."""
