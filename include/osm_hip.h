@@ -308,6 +308,16 @@ int osm_moe_layer_trace_single_launch(osm_context ctx, osm_moe_layer l, osm_expe
 int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                  uint32_t slab_layer, const uint16_t* x_bf16_dev, float* y_dev,
                                  uint32_t tokens);
+/* The routing of the layer's last call, for its first `tokens` rows: what
+ * QwenSparseMoeResult.routing and .shared_gate hold per token
+ * (include/orbi/streammoe/model/routed_moe.hpp:21-27) after the device-side
+ * calls above (decode_device, prefill_device, decode_layers, graphs), which
+ * return only y. ids, weights, mass, shared_gate, logits and normalized (the
+ * RMSNorm output of a sublayer decode, the input of a per-token MoE decode)
+ * are filled where non-NULL; out is ignored. Synchronises the context's
+ * stream. tokens must be in [1, max_tokens]. */
+int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens,
+                          const osm_moe_outputs* outputs);
 /* Enqueues n_layers decodes back to back, as the reference's decoder stack
  * runs its layers in order (src/model/checkpoint_decoder_stack.cpp:191-204).
  * chained != 0: sublayer form, layer i reads the output of layer i-1 (x_dev

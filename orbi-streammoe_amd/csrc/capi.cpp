@@ -799,6 +799,23 @@ int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_sl
   OSM_GUARD_END
 }
 
+int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens, const osm_moe_outputs* outputs) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !l || !outputs) return fail(OSM_E_INVALID, "null argument");
+  if (tokens == 0 || tokens > l->layer.max_tokens())
+    return fail(OSM_E_INVALID, "routing download: token count must be in [1, max_tokens]");
+  if (!ctx->ctx.activate(nullptr)) return fail(OSM_E_DEVICE, "HIP compute context cannot be made current");
+  osm::HipMoeResult r;
+  std::string d;
+  if (!l->layer.download_routing(ctx->ctx, tokens, r.routing, &d)) return fail(OSM_E_DEVICE, d);
+  if (outputs->normalized && !l->layer.download_normalized(ctx->ctx, tokens, r.normalized, &d))
+    return fail(OSM_E_DEVICE, d);
+  osm_moe_outputs o = *outputs;
+  o.out = nullptr;
+  return write_outputs(r, &o, true);
+  OSM_GUARD_END
+}
+
 int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                uint32_t slab_layer, const float* x_dev, float* y_dev, uint32_t tokens,
                                int sublayer, int phase) {

@@ -587,6 +587,22 @@ bool HipMoeLayer::download_routing(HipComputeContext& context, std::uint32_t tok
   }
 }
 
+bool HipMoeLayer::download_normalized(HipComputeContext& context, std::uint32_t tokens, std::vector<float>& out,
+                                      std::string* diagnostic) const noexcept {
+  try {
+    if (!valid() || tokens == 0 || tokens > impl_->max_tokens)
+      return set_diag(diagnostic, "normalised input download: invalid layer or token count"), false;
+    out.resize(static_cast<std::size_t>(tokens) * impl_->cfg.geometry.hidden);
+    const osmd_stream st = context.stream();
+    int rc = osmd_memcpy_d2h(out.data(), impl_->x_norm.get(), out.size() * sizeof(float), st);
+    if (rc == 0) rc = osmd_stream_synchronize(st);
+    if (rc != 0) return set_diag(diagnostic, hip_error("normalised input download failed", rc)), false;
+    return true;
+  } catch (const std::exception& e) {
+    return set_diag(diagnostic, std::string("normalised input download exception: ") + e.what()), false;
+  }
+}
+
 HipMoeResult HipMoeLayer::run(HipComputeContext& context, std::span<const float> hidden,
                               std::uint32_t tokens, const std::uint8_t* const* expert_table,
                               bool sublayer) noexcept {

@@ -766,6 +766,11 @@ class HipMoeLayer {
   [[nodiscard]] bool download_routing(HipComputeContext& context, std::uint32_t tokens,
                                       HipMoeRouting& out,
                                       std::string* diagnostic = nullptr) const noexcept;
+  // The RMSNorm output (sublayer form) or the input (MoE form) of the last
+  // per-token decode, or the normalised input of the last grouped sublayer.
+  [[nodiscard]] bool download_normalized(HipComputeContext& context, std::uint32_t tokens,
+                                         std::vector<float>& out,
+                                         std::string* diagnostic = nullptr) const noexcept;
 
  private:
   friend struct MoeLayerAccess;

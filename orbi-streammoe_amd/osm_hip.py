@@ -138,6 +138,7 @@ _PROTOTYPES = {
     "osm_moe_layer_wait_failures": (c_int, [_H, _H, POINTER(c_uint32)]),
     "osm_moe_layer_trace_single_launch": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_void_p, POINTER(c_uint32)]),
     "osm_moe_layer_prefill_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32]),
+    "osm_moe_layer_routing": (c_int, [_H, _H, c_uint32, POINTER(MoeOutputs)]),
     "osm_decode_graph_create": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int, POINTER(_H)]),
     "osm_graph_capture_begin": (c_int, [_H]),
     "osm_graph_capture_end": (c_int, [_H, POINTER(_H)]),
@@ -641,6 +642,16 @@ class MoeLayer(_Handle):
 
     def prefill_device(self, slab, slab_layer, x_bf16_ptr, y_ptr, tokens):
         check(load().osm_moe_layer_prefill_device(self.ctx.h, self.h, slab.h, slab_layer, x_bf16_ptr, y_ptr, tokens))
+
+    def routing(self, tokens, normalized=False) -> dict:
+        """Routing of the layer's last call (device-side decodes and prefill
+        return only y): ids, weights, mass, shared gate, logits and, when
+        asked, the normalised input."""
+        res, o = self._outputs(tokens, normalized)
+        del res["out"]
+        o.out = None
+        check(load().osm_moe_layer_routing(self.ctx.h, self.h, tokens, ctypes.byref(o)))
+        return res
 
     def launch_phase(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer, phase):
         check(load().osm_moe_layer_launch_phase(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0, phase))

@@ -2,6 +2,9 @@
 
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 META_F32, META_F16, META_BF16 = 0, 1, 2
@@ -137,3 +140,12 @@ def random_blob(rng, hidden, inter, group, meta):
              random_projection(rng, inter, hidden, group, meta),
              random_projection(rng, hidden, inter, group, meta)]
     return make_blob(projs, meta), projs
+
+
+def pmap(fn, items, workers=None):
+    """fn over items on a thread pool (the oracle's C calls release the GIL);
+    results in item order. At most 16 threads: the CPU share of one GPU."""
+    items = list(items)
+    n = workers or min(16, os.cpu_count() or 1, max(1, len(items)))
+    with ThreadPoolExecutor(max_workers=n) as ex:
+        return list(ex.map(fn, items))

@@ -14,15 +14,21 @@ import pytest
 
 import oracle as O
 import osm_hip
-from helpers import max_abs, random_blob, rel_l2
-from test_gpu_moe import QwenLayer, assert_token_parity
+from helpers import max_abs, pmap, random_blob, rel_l2
+from test_gpu_moe import QwenLayer, assert_token_parity, assert_weights
 
 pytestmark = pytest.mark.gpu
 
 
+def oracle_tokens(L, gpu, x, tokens, sublayer=False):
+    for e in {int(i) for i in gpu["ids"][:len(tokens)].ravel()}:
+        L.blob(e)  # fill the host blob cache before the oracle threads read it
+    return pmap(lambda t: L.oracle_token(x[t], sublayer=sublayer), tokens)
+
+
 # 37 tokens end in a ragged 5-token tile of the router GEMM (from 17 tokens)
-# and of the bucketed expert tiles.
-@pytest.mark.parametrize("tokens", [16, 37, 48])
+# and of the bucketed expert tiles; 64 is the largest decode batch measured.
+@pytest.mark.parametrize("tokens", [16, 37, 48, 64])
 def test_grouped_decode_qwen_shape(ctx, tokens):
     seed = 41
     L = QwenLayer(ctx, seed, max_tokens=64)
@@ -33,18 +39,23 @@ def test_grouped_decode_qwen_shape(ctx, tokens):
     per_token = L.moe.run_slab(L.slab, 0, x)
     assert np.array_equal(gpu["ids"], per_token["ids"])
     assert rel_l2(gpu["out"], per_token["out"]) <= 2e-5
+    oras = oracle_tokens(L, gpu, x, range(tokens))
     for t in range(tokens):
-        assert_token_parity(gpu, t, L.oracle_token(x[t]))
+        assert_token_parity(gpu, t, oras[t])
 
 
-def test_grouped_sublayer(ctx):
+# 16 tokens take the per-token router kernel after the RMSNorm; 48 take the
+# router GEMM on the normalised input.
+@pytest.mark.parametrize("tokens", [16, 48])
+def test_grouped_sublayer(ctx, tokens):
     seed = 42
-    L = QwenLayer(ctx, seed, max_tokens=16, norm=True)
-    x = O.synth_tokens(seed, 0, 16, L.D) * np.float32(2.0)
+    L = QwenLayer(ctx, seed, max_tokens=48, norm=True)
+    x = O.synth_tokens(seed, 0, tokens, L.D) * np.float32(2.0)
     L.moe.set_path(osm_hip.PATH_GROUPED)
     gpu = L.moe.run_slab(L.slab, 0, x, sublayer=True)
-    for t in range(16):
-        assert_token_parity(gpu, t, L.oracle_token(x[t], sublayer=True), sublayer=True)
+    oras = oracle_tokens(L, gpu, x, range(tokens), sublayer=True)
+    for t in range(tokens):
+        assert_token_parity(gpu, t, oras[t], sublayer=True)
 
 
 def test_grouped_small_f32_meta_f32_router_no_shared(ctx):
@@ -105,11 +116,14 @@ def test_grouped_router_gemm_planes_no_shared(ctx):
         assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
 
 
-@pytest.mark.parametrize("T", [256, 77, 1])
+@pytest.mark.parametrize("T", [512, 256, 77, 1])
 def test_prefill_bf16_chunk(ctx, T):
-    # A prefill chunk in bf16 at the Qwen3-Next shape: every token against the
-    # per-token kernels on the widened input, a sample of tokens against the
-    # oracle. 77 and 1 tokens leave the last 16-token router tile ragged.
+    # A prefill chunk in bf16 at the Qwen3-Next shape (512 tokens: the chunk
+    # that is measured): the prefill's own routing of every token against the
+    # oracle's router (ids bit-exact, weights and shared gate within 1e-6),
+    # every output against the per-token kernels on the widened input, and a
+    # sample of outputs against the oracle. 77 and 1 tokens leave the last
+    # 16-token router tile ragged.
     seed = 44
     L = QwenLayer(ctx, seed, max_tokens=T)
     xf = O.synth_tokens(seed, 9000, T, L.D)
@@ -119,11 +133,25 @@ def test_prefill_bf16_chunk(ctx, T):
     xb.upload(bits)
     L.moe.prefill_device(L.slab, 0, xb.ptr, y.ptr, T)
     got = y.download(np.float32, T * L.D).reshape(T, L.D)
+    routing = L.moe.routing(T)
+    router = O.bf16_bits_to_f32(L.router_bits)
+    sg = O.bf16_bits_to_f32(L.sg_bits)
+    picks = pmap(lambda t: O.route_qwen_top_k(xw[t], router, L.D, L.E, L.k, True), range(T))
+    for t in range(T):
+        if not np.array_equal(routing["ids"][t], picks[t]["ids"]):
+            pytest.fail(f"token {t}: prefill ids {list(routing['ids'][t])} oracle {list(picks[t]['ids'])}")
+        assert_weights(routing["weights"][t], routing["logits"][t], routing["ids"][t], picks[t]["weights"],
+                       picks[t]["logits"])
+        gate = O.sigmoid(float(np.dot(sg.astype(np.float64), xw[t].astype(np.float64))))
+        assert abs(routing["shared_gate"][t] - gate) <= 1e-6, t
+    assert rel_l2(routing["logits"], np.stack([p["logits"] for p in picks])) <= 1e-5
     L.moe.set_path(osm_hip.PATH_PER_TOKEN)
     ref = L.moe.run_slab(L.slab, 0, xw)
+    assert np.array_equal(ref["ids"], routing["ids"])
     for t in range(T):
         assert rel_l2(got[t], ref["out"][t]) <= 2e-5, t
-    for t in range(0, T, 32):
-        ora = L.oracle_token(xw[t])
+    sample = list(range(0, T, 32))
+    oras = oracle_tokens(L, ref, xw, sample)
+    for t, ora in zip(sample, oras):
         assert np.array_equal(ref["ids"][t], ora["ids"])
         assert rel_l2(got[t], ora["out"]) <= 1e-3
