@@ -82,6 +82,16 @@ def build_model(ctx, layers, seed):
     return g, slab, moes
 
 
+def routing_counts(moes, reset=False):
+    """The layers' routing counters summed (selections, exact-path
+    selections, exact paths over every expert, unresolved adjacent picks)."""
+    tot = {}
+    for m in moes:
+        for k, v in m.routing_stats(reset=reset).items():
+            tot[k] = tot.get(k, 0) + v
+    return tot
+
+
 def time_steps(ctx, n, fn):
     start, stop = ctx.event(), ctx.event()
     ctx.synchronize()
@@ -426,7 +436,9 @@ def main():
 
     for i in range(warm):
         step_graph(i)
+    routing_counts(moes, reset=True)
     ms = time_steps(ctx, steps, lambda i: step_graph(warm + i))
+    route_indep = routing_counts(moes)
     ms_per_step = ms / steps
     us_per_token_layer = ms_per_step * 1000.0 / L
     hbm_gbps = bytes_per_token_layer / (us_per_token_layer * 1e-6) / 1e9
@@ -454,7 +466,10 @@ def main():
 
     for i in range(warm):
         step_chained(i)
+    routing_counts(moes, reset=True)
     us_chained = time_steps(ctx, steps, lambda i: step_chained(warm + i)) / steps * 1000.0 / L
+    route_chained = routing_counts(moes)
+    log(f"[bench] routing counters, independent / chained: {route_indep} / {route_chained}")
     log(f"[bench] chained sublayers, graph: {us_chained:.2f} us/token-layer")
 
     # Per-kernel timing: L launches of one phase, captured into a graph and
@@ -524,6 +539,10 @@ def main():
         "bytes_per_token_layer": bytes_per_token_layer,
         "chained_sublayer_us_per_token_layer": round(us_chained, 3),
         "stream_launch_us_per_token_layer": round(us_eager, 3),
+        "routing_exact_path": {
+            "what": "selections whose order the per-logit bounds did not prove, recomputed in the reference's order",
+            "independent": route_indep, "chained": route_chained,
+        },
         "kernels": kernels,
         "roofline": {
             "kernel": dominant,

@@ -265,7 +265,7 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
  * osm_moe_layer_decode_device on OSM_PATH_PER_TOKEN) with their routing
  * workspace in the library's fixed 4 MiB device array, one per GPU, held
  * until the process ends, instead of the layer's. tokens must be in
- * [1, osm_moe_layer_static_tokens_capacity(l)] (127 at the Qwen3-Next
+ * [1, osm_moe_layer_static_tokens_capacity(l)] (119 at the Qwen3-Next
  * shape), else OSM_E_INVALID. Every call on one GPU shares that array, and
  * the routing it leaves there is overwritten by the next call: calls that
  * overlap in time on one GPU (several streams or contexts) race. */
@@ -280,28 +280,9 @@ uint32_t osm_moe_layer_static_tokens_capacity(osm_moe_layer l);
  * grouped GEMMs from 40 tokens on (group 32/64/128, hidden and intermediate
  * multiples of 128, 16-byte aligned input); OSM_PATH_PER_TOKEN always runs
  * the per-token kernels; OSM_PATH_GROUPED always buckets (token, slot) pairs
- * by expert and reads each expert once; OSM_PATH_SINGLE_LAUNCH runs one-token
- * decodes as one launch (more tokens: the per-token kernels) where the shape
- * allows it (hidden <= 2048, intermediate in (64, 512], <= 512 experts,
- * top_k + shared <= 12, f32 or bf16 router; set_path fails otherwise). The
- * single launch and the per-token kernels give the same bits; on MI355X at
- * the Qwen3-Next shape the single launch is the slower of the two. */
-enum osm_moe_path { OSM_PATH_AUTO = 0, OSM_PATH_PER_TOKEN = 1, OSM_PATH_GROUPED = 2, OSM_PATH_SINGLE_LAUNCH = 3 };
+ * by expert and reads each expert once. */
+enum osm_moe_path { OSM_PATH_AUTO = 0, OSM_PATH_PER_TOKEN = 1, OSM_PATH_GROUPED = 2 };
 int osm_moe_layer_set_path(osm_moe_layer l, int path);
-/* The single launch's workgroups wait on each other with bounded spins; a
- * wait that ran out sets a sticky flag, read here (0 = every launch of this
- * layer completed its handshakes). Synchronises the context's stream. */
-int osm_moe_layer_wait_failures(osm_context ctx, osm_moe_layer l, uint32_t* out);
-/* Tracing (the reference times phases with steady_clock around each step,
- * greedy_token_session.cpp:171-183; this is the device-side counterpart for
- * the single launch): one single-launch decode of one token (MoE form) that
- * also stamps each workgroup's timeline into trace_dev (device, [grid][8]
- * u64: steady-clock ticks at its phase boundaries, slot 7 its compute unit's
- * hardware id). shape[4] gets the router, gate/up and down workgroup counts
- * and the grid (blocks: router, gate/up, down). */
-int osm_moe_layer_trace_single_launch(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
-                                      uint32_t slab_layer, const float* x_dev, float* y_dev,
-                                      uint64_t* trace_dev, uint32_t* shape);
 /* A prefill chunk: bf16 x [tokens, D] (device, 16-byte aligned) through the
  * grouped path, MoE form, y fp32 [tokens, D]; needs a bf16 router. Routing
  * per token is that of run_qwen_sparse_moe_vulkan_accum on the widened x. */
@@ -318,6 +299,19 @@ int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_sl
  * stream. tokens must be in [1, max_tokens]. */
 int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens,
                           const osm_moe_outputs* outputs);
+/* Routing exactness counters of the layer since its creation or the last
+ * reset (no counterpart in the reference, whose router always sums on the
+ * host in one order, src/cpu/reference_ops.cpp:85-93). The device sums
+ * logits in other orders and bounds each one's distance from the
+ * reference's; a selection whose order the bounds do not prove recomputes
+ * its candidates' logits in the reference's order. out[0] selections (one
+ * per token per call), out[1] selections that took that exact path, out[2]
+ * exact paths that recomputed every expert (picks near exp underflow),
+ * out[3] adjacent picks whose reference probabilities could tie only
+ * through the last bit of exp (order taken from the exps; 0 in every run
+ * so far). Synchronises the context's stream; reset != 0 zeroes them
+ * afterwards. */
+int osm_moe_layer_routing_stats(osm_context ctx, osm_moe_layer l, uint32_t out[4], int reset);
 /* Enqueues n_layers decodes back to back, as the reference's decoder stack
  * runs its layers in order (src/model/checkpoint_decoder_stack.cpp:191-204).
  * chained != 0: sublayer form, layer i reads the output of layer i-1 (x_dev

@@ -670,17 +670,6 @@ uint32_t osm_moe_layer_static_tokens_capacity(osm_moe_layer l) {
   return l ? l->layer.static_tokens_capacity() : 0U;
 }
 
-int osm_moe_layer_trace_single_launch(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
-                                      uint32_t slab_layer, const float* x_dev, float* y_dev,
-                                      uint64_t* trace_dev, uint32_t* shape) {
-  if (!ctx || !l || !slab || !shape) return fail(OSM_E_INVALID, "null argument");
-  const auto* table = slab->slab.device_table(slab_layer);
-  if (!table) return fail(OSM_E_INVALID, "slab layer out of range");
-  if (slab->slab.experts() != l->layer.config().expert_count)
-    return fail(OSM_E_INVALID, "slab expert count does not match the layer's router");
-  auto r = l->layer.trace_single_launch(ctx->ctx, x_dev, y_dev, table, trace_dev, shape);
-  return from_diag(r.executed, r.diagnostic);
-}
 
 // Builds the facade's decode step from C handles, checking each layer
 // against the slab.
@@ -775,16 +764,11 @@ extern "C" {
 
 int osm_moe_layer_set_path(osm_moe_layer l, int path) {
   if (!l) return fail(OSM_E_INVALID, "null layer");
-  if (path < OSM_PATH_AUTO || path > OSM_PATH_SINGLE_LAUNCH) return fail(OSM_E_INVALID, "unknown MoE path");
+  if (path < OSM_PATH_AUTO || path > OSM_PATH_GROUPED) return fail(OSM_E_INVALID, "unknown MoE path");
   std::string d;
   return l->layer.set_path(static_cast<osm::HipMoePath>(path), &d) ? ok() : fail(OSM_E_INVALID, d);
 }
 
-int osm_moe_layer_wait_failures(osm_context ctx, osm_moe_layer l, uint32_t* out) {
-  if (!ctx || !l || !out) return fail(OSM_E_INVALID, "invalid arguments");
-  std::string d;
-  return l->layer.single_launch_failures(ctx->ctx, out, &d) ? ok() : fail(OSM_E_DEVICE, d);
-}
 
 int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_slab slab, uint32_t slab_layer,
                                  const uint16_t* x_bf16_dev, float* y_dev, uint32_t tokens) {
@@ -814,6 +798,15 @@ int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens, con
   o.out = nullptr;
   return write_outputs(r, &o, true);
   OSM_GUARD_END
+}
+
+int osm_moe_layer_routing_stats(osm_context ctx, osm_moe_layer l, uint32_t out[4], int reset) {
+  if (!ctx || !l || !out) return fail(OSM_E_INVALID, "null argument");
+  std::uint32_t v[4] = {0, 0, 0, 0};
+  std::string d;
+  if (!l->layer.routing_stats(ctx->ctx, v, reset != 0, &d)) return fail(OSM_E_DEVICE, d);
+  std::memcpy(out, v, sizeof(v));
+  return ok();
 }
 
 int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,

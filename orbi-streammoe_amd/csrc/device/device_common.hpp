@@ -97,6 +97,31 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
+// Inclusive prefix sum over the 64 lanes in lane order. row_shr 1, 2 and 3
+// (lanes without a source add 0) give each lane the sum of up to four lanes
+// ending at it, row_shr 4 and 8 extend that to the start of its 16-lane row,
+// and row_bcast 15 / 31 add the totals of the rows before it.
+__device__ __forceinline__ float wave_incl_scan(float v) {
+  float s = v + dpp<0x111>(0.0f, v);
+  s += dpp<0x112>(0.0f, v);
+  s += dpp<0x113>(0.0f, v);
+  s += dpp<0x114>(0.0f, s);
+  s += dpp<0x118>(0.0f, s);
+  s += dpp<kDppRowBcast15, 0xA>(0.0f, s);
+  s += dpp<kDppRowBcast31, 0xC>(0.0f, s);
+  return s;
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Float bits as an unsigned key that orders like the value (-0 below +0).
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // Sum over aligned groups of `width` lanes (width a power of two <= 64).
 __device__ __forceinline__ float group_sum(float v, int width) {
   for (int m = width >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);

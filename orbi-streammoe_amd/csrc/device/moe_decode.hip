@@ -8,10 +8,12 @@
 //                   -> logits, sigmoid shared gate, normalised x.
 //   gate_up_kernel  top-k selection (src/cpu/reference_ops.cpp:130-212,
 //                   src/model/qwen_router.cpp:11-94), recomputed from the
-//                   logits by one wavefront of every routed workgroup so no
-//                   workgroup waits on another, then the gate and up q4 GEMVs
-//                   of every pick and of the shared expert with SwiGLU fused
-//                   in the epilogue (shaders/q4_gemv.comp + shaders/swiglu.comp).
+//                   logits by every routed workgroup so no workgroup waits on
+//                   another, proven equal to the reference's from per-logit
+//                   error bounds or else recomputed in the reference's order,
+//                   then the gate and up q4 GEMVs of every pick and of the
+//                   shared expert with SwiGLU fused in the epilogue
+//                   (shaders/q4_gemv.comp + shaders/swiglu.comp).
 //   down_kernel     down q4 GEMV of every pick and of the shared expert with
 //                   the routing weights and the sigmoid shared gate folded in,
 //                   plus the optional residual add
@@ -23,8 +25,9 @@
 // reference GEMV's: scale * sum(q * x) + bias * sum(x).
 //
 // When residency is decided on the host (a capped expert cache), a
-// one-wavefront select kernel runs after route_kernel instead, the host reads
-// the ids and writes the slot pointers, and gate_up_kernel reads those.
+// one-workgroup-per-token select kernel runs after route_kernel instead, the
+// host reads the ids and writes the slot pointers, and gate_up_kernel reads
+// those.
 #include "device_common.hpp"
 
 namespace {
@@ -44,10 +47,15 @@ struct SlotSource {
   }
 };
 
-// What a routed wavefront needs to select its expert from the logits.
+
+// What a routed workgroup needs to select its token's experts: the logits
+// and their bounds (or the router GEMM's planes), and, for the exact path,
+// the router and the input it was applied to.
 struct RouteView {
   const float* logits;                // [B, E]
+  const float* bounds;                // [B, E] bound of each logit, or null (no bound: exact path)
   const float* planes;                // null, or `parts` planes [B][E + 1] of partial sums
+  const float* bound_planes;          // with planes: [parts][2][B][E + 1] bound parts, or null
   uint32_t parts, tokens;
   float* logits_out;                  // [B, E]  with planes: the summed logits
   float* gate_out;                    // [B]     with planes: the shared gate
@@ -59,6 +67,15 @@ struct RouteView {
   float* weights;                     // [B, k]
   float* mass;                        // [B]
   const uint8_t** slot_ptrs;          // [B, nslot]
+  uint32_t* stats;                    // null, or the four routing counters
+  // The exact path: router [E, D] (router_dtype), the router's input x
+  // [B, D] (fp32, or bf16 when x_bf16), RMS-normalised first when rms.
+  const void* router;
+  uint32_t router_dtype, router_group, hidden;
+  const void* x;
+  uint32_t x_bf16, rms;
+  const float* norm_weight;
+  float rms_eps;
 };
 
 struct GateUpParams {
@@ -81,222 +98,11 @@ struct DownParams {
   float* y;                  // [B, D]
 };
 
-// Top-k selection on one 256-thread workgroup. Thread i owns experts
-// [i*PER, i*PER+PER). Probabilities are the reference's: exp(logit - max) /
-// sum over all experts (reference_ops.cpp:130-160); the max and the sum
-// combine the four wavefronts' reductions in a fixed order. The order is the
-// reference's too: probability descending, lower expert id first among
-// equals (reference_ops.cpp:170-196: strict > on insertion, stable sort by
-// probability). A probability is >= 0, so its bits order like its value; the
-// key is (bits + 1, ~id), unique per expert, and 0 for experts past E and
-// popped entries (below every real expert, even one whose probability is
-// +0). Each wavefront takes the top-k of its 64 * PER experts in k rounds
-// (the largest lane head over the wavefront, the lowest lane holding it:
-// lanes own ascending id ranges, so that is the lowest id). The 4k
-// candidates are then ranked in one pass: as (key << 32) | ~id they are
-// unique and order exactly as probability descending, id ascending, so a
-// candidate's place is the number of candidates above it. With a table,
-// each thread parks its experts' blob pointers in LDS, so a pick's blob
-// costs no dependent global load.
-constexpr uint32_t kSelThreads = 256;
-constexpr uint32_t kSelWaves = kSelThreads / kWave;
-
-// Result of one token's selection, in LDS: ids and probabilities in pick
-// order, the blob of every expert, and the workgroup's reduction scratch.
-template <int PER>
-struct Selection {
-  uint32_t id[OSMD_MAX_TOP_K];
-  float p[OSMD_MAX_TOP_K];
-  const uint8_t* blob[kSelThreads * PER];
-  float red[2][kSelWaves];
-  uint64_t cand[kSelWaves * OSMD_MAX_TOP_K];  // (key << 32) | ~id, wavefront-major
-};
-
-__device__ __forceinline__ void sort_step(uint32_t* k, uint32_t* n, int a, int b) {
-  // Descending on (k, n): swap when (k[b], n[b]) > (k[a], n[a]).
-  const uint64_t ka = (static_cast<uint64_t>(k[a]) << 32) | n[a];
-  const uint64_t kb = (static_cast<uint64_t>(k[b]) << 32) | n[b];
-  const bool swap = kb > ka;
-  const uint32_t k0 = k[a], n0 = n[a];
-  k[a] = swap ? k[b] : k0;
-  n[a] = swap ? n[b] : n0;
-  k[b] = swap ? k0 : k[b];
-  n[b] = swap ? n0 : n[b];
-}
-
-template <int PER>
-__device__ __forceinline__ void sort_lane(uint32_t* k, uint32_t* n) {
-  // Odd-even transposition (PER is 2 or 4).
-#pragma unroll
-  for (int round = 0; round < PER; ++round) {
-#pragma unroll
-    for (int j = round & 1; j + 1 < PER; j += 2) sort_step(k, n, j, j + 1);
-  }
-}
-
-// Selection from this thread's logits p[j] of experts tid*PER + j (entries
-// past E are ignored) and their table pointers. Every thread of the
-// workgroup calls it; it ends with a barrier, after which out is complete.
-template <int PER>
-__device__ __forceinline__ void select_values(const RouteView& rv, float (&p)[PER],
-                                              const uint8_t* const (&tab)[PER], Selection<PER>& out,
-                                              uint64_t* mark = nullptr) {
-  const uint32_t E = rv.expert_count;
-  const uint32_t k = rv.top_k;
-  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const uint32_t base = tid * PER;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    if (base + j >= E) p[j] = -INFINITY;
-    mx = fmaxf(mx, p[j]);
-  }
-  mx = wave_max(mx);
-  if (lane == 0) out.red[0][wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
-  float sum = 0.0f;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    p[j] = (base + j < E) ? expf(p[j] - mx) : 0.0f;
-    sum += p[j];
-  }
-  sum = wave_sum(sum);
-  if (lane == 0) out.red[1][wave] = sum;
-  __syncthreads();
-  sum = ((out.red[1][0] + out.red[1][1]) + out.red[1][2]) + out.red[1][3];
-  if (mark != nullptr && threadIdx.x == 0) mark[5] = static_cast<uint64_t>(wall_clock64());
-  uint32_t key[PER], nid[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    key[j] = (base + j < E) ? __float_as_uint(p[j] / sum) + 1u : 0u;
-    nid[j] = ~(base + j);
-    if (base + j < E) out.blob[base + j] = tab[j];
-  }
-  sort_lane<PER>(key, nid);
-
-  // This wavefront's top-k. Each round is branch-free (the pop is a select
-  // on every lane) and lane r keeps round r's result, written out after the
-  // last round. The loop stays rolled: one body, fetched once, instead of
-  // k copies that each start with instruction-cache misses (the selection
-  // runs on one workgroup, so its code is cold).
-  uint32_t rk = 0u, ri = 0u;
-#pragma unroll 1
-  for (uint32_t r = 0; r < k; ++r) {
-    {
-      const uint32_t m = wave_max_u32(key[0]);
-      const int wl = __ffsll(__ballot(key[0] == m)) - 1;  // never empty: m is some lane's key
-      const uint32_t sid = ~static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(nid[0]), wl));
-      rk = lane == r ? m : rk;
-      ri = lane == r ? sid : ri;
-      const bool won = static_cast<int>(lane) == wl;  // pop the head
-#pragma unroll
-      for (int j = 0; j + 1 < PER; ++j) {
-        key[j] = won ? key[j + 1] : key[j];
-        nid[j] = won ? nid[j + 1] : nid[j];
-      }
-      key[PER - 1] = won ? 0u : key[PER - 1];
-      nid[PER - 1] = won ? 0u : nid[PER - 1];
-    }
-  }
-  if (lane < k) out.cand[wave * k + lane] = (static_cast<uint64_t>(rk) << 32) | ~ri;
-  __syncthreads();
-  if (mark != nullptr && threadIdx.x == 0) mark[6] = static_cast<uint64_t>(wall_clock64());
-
-  // Wavefront 0: each lane ranks one candidate against all of them (LDS
-  // broadcast reads); the k best write their place. Candidates of key 0
-  // (fewer than k experts in a wavefront) always have k real ones above.
-  if (wave == 0) {
-    const uint32_t nc = kSelWaves * k;
-    const uint64_t mine = lane < nc ? out.cand[lane] : 0u;
-    uint32_t rank = 0;
-#pragma unroll 4
-    for (uint32_t c = 0; c < nc; ++c) rank += out.cand[c] > mine ? 1u : 0u;
-    if (lane < nc && rank < k) {
-      const uint32_t id = ~static_cast<uint32_t>(mine);
-      out.id[rank] = id < E ? id : E - 1u;  // a blob lookup always stays in the table
-      out.p[rank] = __uint_as_float(static_cast<uint32_t>(mine >> 32) - 1u);
-    }
-  }
-  __syncthreads();
-}
-
-// Loads token t's logits (and table pointers) and selects; every thread of
-// the workgroup calls it.
-template <int PER>
-__device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out) {
-  const uint32_t E = rv.expert_count;
-  const float* lg = rv.logits + static_cast<size_t>(t) * E;
-  const uint32_t base = threadIdx.x * PER;
-  float p[PER];
-  const uint8_t* tab[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const uint32_t e = (base + j < E) ? base + j : E - 1u;  // clamped: every load in bounds
-    if (rv.planes != nullptr) {
-      // Partial sums of the router GEMM's K ranges, added in plane order.
-      const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
-      const float* pl = rv.planes + static_cast<size_t>(t) * (E + 1u) + e;
-      float v = pl[0];
-      for (uint32_t part = 1; part < rv.parts; ++part) v += pl[part * ps];
-      p[j] = v;
-      if (base + j < E) rv.logits_out[static_cast<size_t>(t) * E + e] = v;
-    } else {
-      p[j] = lg[e];
-    }
-    tab[j] = rv.expert_table ? rv.expert_table[e] : nullptr;
-  }
-  if (rv.planes != nullptr && rv.has_shared && threadIdx.x == 0) {
-    const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
-    const float* pl = rv.planes + static_cast<size_t>(t) * (E + 1u) + E;
-    float g = pl[0];
-    for (uint32_t part = 1; part < rv.parts; ++part) g += pl[part * ps];
-    rv.gate_out[t] = 1.0f / (1.0f + expf(-g));  // reference_ops.cpp:214-216
-  }
-  select_values<PER>(rv, p, tab, out);
-}
-
-template <int PER>
-__device__ __forceinline__ const uint8_t* pick_blob(const RouteView& rv, const Selection<PER>& s,
-                                                    uint32_t r) {
-  const uint8_t* b = rv.expert_table ? s.blob[s.id[r]] : nullptr;
-  return b ? b : rv.fallback;
-}
-
-// Writes the selection of token t: ids and weights in pick order, the
-// selected mass summed in pick order and the optional renormalisation
-// (qwen_router.cpp:72-91), and each slot's blob (shared expert last).
-// Threads tid <= k of the workgroup take part.
-template <int PER>
-__device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t t, uint32_t tid,
-                                                  const Selection<PER>& s) {
-  const uint32_t k = rv.top_k;
-  const uint32_t nslot = k + rv.has_shared;
-  if (tid == 0) {
-    float mass = 0.0f;
-    for (uint32_t r = 0; r < k; ++r) mass = mass + s.p[r];
-    for (uint32_t r = 0; r < k; ++r) {
-      rv.ids[static_cast<size_t>(t) * k + r] = s.id[r];
-      rv.weights[static_cast<size_t>(t) * k + r] = rv.norm_topk_prob ? s.p[r] / mass : s.p[r];
-    }
-    rv.mass[t] = mass;
-  }
-  if (tid < k)
-    rv.slot_ptrs[static_cast<size_t>(t) * nslot + tid] = pick_blob(rv, s, tid);
-  else if (tid == k && nslot > k)
-    rv.slot_ptrs[static_cast<size_t>(t) * nslot + k] = rv.shared_expert;
-}
-
-template <int PER>
-__global__ __launch_bounds__(kSelThreads) void select_kernel(RouteView rv) {
-  __shared__ Selection<PER> sel;
-  select_block<PER>(rv, blockIdx.x, sel);
-  publish_selection(rv, blockIdx.x, threadIdx.x, sel);
-}
 
 // ---------------------------------------------------------------------------
-// Router GEMV. A wavefront owns one router row; lane l reads elements
-// l*8 + 512u .. +8 (u = 0, 1, ...), kept as loaded until the FMA.
+// Router elements as loaded. A wavefront of the router GEMV owns one router
+// row; lane l reads elements l*8 + 512u .. +8 (u = 0, 1, ...), kept as
+// loaded until the FMA.
 constexpr int kRouteWaves = 4;
 
 template <int RD>
@@ -374,6 +180,561 @@ __device__ __forceinline__ float raw8_get(const Raw8<RD>& r, int j) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Routing that is the reference's, bit for bit.
+//
+// The reference ranks experts by softmax probability, the lower id first
+// among equal probabilities (reference_ops.cpp:130-212), over logits that it
+// sums sequentially in fp32 (reference_ops.cpp:85-93) on the input that
+// rms_norm_inplace normalised (reference_ops.cpp:96-128). The device sums in
+// other orders, so its logits differ from the reference's by rounding. Every
+// device logit l therefore comes with a bound b >= |l - L|, L the
+// reference's logit (route_block, the router GEMM), and the selection ranks
+// on the device logits only where the bounds prove the reference's order:
+//
+//  - adjacent picks i, i+1: l_i - l_{i+1} > s (b_i + b_{i+1}), plus kappa
+//    when the lower logit has the lower id;
+//  - every expert e outside the picks: l_e + s b_e + kappa(e) < l_k - s b_k;
+//  - the k-th pick within 80 of the largest logit.
+//
+// s = 1 + 2^-9 covers a common factor 1 + eta by which the device's
+// RMS-normalised input can differ from the reference's (eta <= n u for a
+// width n <= 8192 and u = 2^-24, from the two sums of squares) and the
+// rounding of the bounds themselves. kappa = 2^-20 + 2^-23 (m - l + 1), m
+// the largest logit: a gap in L larger than that keeps the two
+// probabilities exp(fl(L - m)) / S at least four ulps apart whatever the
+// rounding of the subtraction, the exp (within one ulp) and the division, so
+// the reference's probabilities cannot tie where the device's logits do not.
+// Within 80 of m no exp underflows.
+//
+// Otherwise (a near tie, equal device logits, or a missing bound) the
+// selection takes the exact path: every expert whose interval can reach the
+// picks' lowest lower bound is recomputed in the reference's order, and the
+// candidates are ranked by exp(fl(L - m)) with ties to the lower id, the
+// reference's key. When the k-th candidate is more than 80 below m (exps
+// near or at underflow, where probabilities tie at 0 and the lowest ids win
+// whatever their logits) every expert is recomputed. Two adjacent picks
+// whose logits differ but whose exps lie within 5 ulps of each other are
+// counted as unresolved: there the order rests on the exp's last bit and on
+// the rounding of the sum, which the device cannot reproduce exactly.
+//
+// The probabilities of the picks (their weights) come from the device
+// logits in both paths: exp(l - max) / sum over every expert.
+constexpr uint32_t kSelThreads = 256;
+constexpr uint32_t kSelWaves = kSelThreads / kWave;
+constexpr float kBoundSlack = 1.0f + 0x1p-9f;
+constexpr float kUnderflowGap = 80.0f;
+
+// The exact path recomputes logits in the reference's order. The additions
+// of one logit form a chain that cannot be split, so the workgroup stages
+// everything else: kExactCols columns at a time, all threads load the
+// candidates' router elements and the input, round each product w * x into
+// LDS, and one thread per candidate then adds its row's products in column
+// order. The next chunk's loads are issued before the additions start.
+constexpr uint32_t kExactCols = 256;
+constexpr uint32_t kExactRows = 16;  // candidates per pass
+constexpr uint32_t kExactStride = kExactCols + 1u;  // LDS row stride: the adders' rows in distinct banks
+
+__device__ __forceinline__ float tie_margin(float mx, float l) { return 0x1p-20f + 0x1p-23f * (mx - l + 1.0f); }
+
+// Result of one token's selection, in LDS: ids, device logits and bounds and
+// probabilities in pick order, the blob, device logit and bound of every
+// expert, and the workgroup's scratch.
+template <int PER>
+struct Selection {
+  uint32_t id[OSMD_MAX_TOP_K];
+  float lg[OSMD_MAX_TOP_K];
+  float bd[OSMD_MAX_TOP_K];
+  float p[OSMD_MAX_TOP_K];
+  const uint8_t* blob[kSelThreads * PER];
+  float val[kSelThreads * PER];   // device logit of every expert
+  float aux[kSelThreads * PER];   // its bound; on the exact path, its exp(fl(L - m)) (-1: no candidate)
+  float ex[kSelThreads * PER];    // exact path: the reference's logit of a candidate
+  float red[2][kSelWaves];
+  uint64_t cand[kSelWaves * OSMD_MAX_TOP_K];  // (key << 32) | ~id, wavefront-major
+  uint32_t fid[OSMD_MAX_TOP_K + 1];           // exact path: candidates by rank
+  float scal[2];
+  uint32_t nunresolved, ncand, wcount[kSelWaves];
+  uint16_t cl[kSelThreads * PER];             // exact path: candidate list
+  float xe[kExactCols];                       // exact path: the input of one chunk of columns
+  float prod[kExactRows][kExactStride];       // exact path: rounded products of one chunk
+  float pad[32];                              // chain_sum reads up to 24 past a row
+};
+static_assert(kExactCols == kSelThreads && kExactRows * 16u == kSelThreads, "exact-path chunk mapping");
+
+__device__ __forceinline__ void sort_step(uint32_t* k, uint32_t* n, int a, int b) {
+  // Descending on (k, n): swap when (k[b], n[b]) > (k[a], n[a]).
+  const uint64_t ka = (static_cast<uint64_t>(k[a]) << 32) | n[a];
+  const uint64_t kb = (static_cast<uint64_t>(k[b]) << 32) | n[b];
+  const bool swap = kb > ka;
+  const uint32_t k0 = k[a], n0 = n[a];
+  k[a] = swap ? k[b] : k0;
+  n[a] = swap ? n[b] : n0;
+  k[b] = swap ? k0 : k[b];
+  n[b] = swap ? n0 : n[b];
+}
+
+template <int PER>
+__device__ __forceinline__ void sort_lane(uint32_t* k, uint32_t* n) {
+  // Odd-even transposition (PER is 2 or 4).
+#pragma unroll
+  for (int round = 0; round < PER; ++round) {
+#pragma unroll
+    for (int j = round & 1; j + 1 < PER; j += 2) sort_step(k, n, j, j + 1);
+  }
+}
+
+// acc + v[0] + v[1] + ... + v[n-1] (SQUARE: + v[i] * v[i]) in order, each
+// operation rounded to fp32, v in LDS, n a multiple of 8. Three register
+// blocks of 8 rotate: the reads of a block are issued two blocks before its
+// additions (sched_barrier keeps the compiler from moving them later), so
+// the chain of additions, which cannot be shortened, is what is waited on.
+// The reads run up to 24 elements past n (the LDS arrays are padded for
+// it); those values are never added.
+template <bool SQUARE>
+__device__ __forceinline__ void chain_read8(const float* v, float (&r)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = v[j];
+  __builtin_amdgcn_sched_barrier(0);
+}
+template <bool SQUARE>
+__device__ __forceinline__ float chain_add8(const float (&r)[8], float acc) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc = SQUARE ? acc + r[j] * r[j] : acc + r[j];
+  __builtin_amdgcn_sched_barrier(0);
+  return acc;
+}
+template <bool SQUARE>
+__device__ __forceinline__ float chain_sum(const float* v, uint32_t n, float acc) {
+  float a[8], b[8], c[8];
+  chain_read8<SQUARE>(v, a);
+  chain_read8<SQUARE>(v + 8, b);
+  for (uint32_t i = 0;; i += 24) {
+    chain_read8<SQUARE>(v + i + 16, c);
+    acc = chain_add8<SQUARE>(a, acc);
+    if (i + 8 >= n) break;
+    chain_read8<SQUARE>(v + i + 24, a);
+    acc = chain_add8<SQUARE>(b, acc);
+    if (i + 16 >= n) break;
+    chain_read8<SQUARE>(v + i + 32, b);
+    acc = chain_add8<SQUARE>(c, acc);
+    if (i + 24 >= n) break;
+  }
+  return acc;
+}
+
+// x[c] of the router's input, as the reference reads it (0 past the row).
+__device__ __forceinline__ float load_x1(const RouteView& rv, uint32_t t, uint32_t c) {
+  if (c >= rv.hidden) return 0.0f;
+  const size_t o = static_cast<size_t>(t) * rv.hidden + c;
+  return rv.x_bf16 ? bf16_to_f32(ldg<uint16_t>(static_cast<const uint16_t*>(rv.x) + o))
+                   : ldg<float>(static_cast<const float*>(rv.x) + o);
+}
+
+// The reference's RMSNorm scale of token t: the squares summed in order,
+// then 1 / sqrt(sum / D + eps), each operation rounded to fp32
+// (reference_ops.cpp:113-121). Every thread calls it; x is staged in LDS
+// kExactRows * kExactStride columns at a time for thread 0's chain.
+template <int PER>
+__device__ float exact_rms_scale(const RouteView& rv, uint32_t t, Selection<PER>& out) {
+#pragma clang fp contract(off)
+  constexpr uint32_t kCols = kExactRows * kExactStride;
+  float* stage = &out.prod[0][0];
+  float ss = 0.0f;
+  for (uint32_t c0 = 0; c0 < rv.hidden; c0 += kCols) {
+    for (uint32_t i = threadIdx.x; i < kCols; i += kSelThreads) stage[i] = load_x1(rv, t, c0 + i);
+    __syncthreads();
+    if (threadIdx.x == 0) ss = chain_sum<true>(stage, rv.hidden - c0 < kCols ? rv.hidden - c0 : kCols, ss);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0)
+    out.scal[1] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, static_cast<float>(rv.hidden)) + rv.rms_eps));
+  __syncthreads();
+  return out.scal[1];
+}
+
+// The reference's logits of candidates out.cl[first .. first + nr), nr <=
+// kExactRows, for token t: acc + w[c] * x[c] for c = 0 .. D-1, every product
+// and sum rounded to fp32 (reference_ops.cpp:85-93), on x scaled as
+// rms_norm_inplace does, x * (scale * weight) (reference_ops.cpp:123-126).
+// Every thread calls it; candidate r's logit lands in out.ex.
+template <int RD, int PER>
+__device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>& out, uint32_t first, uint32_t nr,
+                                float scale) {
+#pragma clang fp contract(off)
+  const uint32_t D = rv.hidden, tid = threadIdx.x;
+  // This thread's products: row r, 16 columns from seg. The 16 rows of one
+  // segment sit in 16 lanes, so their LDS writes land in 16 banks.
+  const uint32_t r = tid % 16u, seg = (tid / 16u) * 16u;
+  const uint32_t e = r < nr ? out.cl[first + r] : out.cl[first];
+  Q8Row qr{};
+  const uint8_t* row = nullptr;
+  if constexpr (RD == OSM_ROUTER_AFFINE_Q8)
+    qr = q8_row(rv.router, rv.expert_count, e, D, rv.router_group);
+  else
+    row = static_cast<const uint8_t*>(rv.router) + static_cast<size_t>(e) * D * (RD == OSM_META_F32 ? 4u : 2u);
+  Raw8<RD> w0, w1;
+  float xv = 0.0f, nwv = 1.0f;
+  auto fetch = [&](uint32_t c0) {
+    const uint32_t c = c0 + seg;
+    if (r < nr && c < D) {
+      if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c, w0); else load_raw8<RD>(row, c, w0);
+    }
+    if (r < nr && c + 8u < D) {
+      if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c + 8u, w1); else load_raw8<RD>(row, c + 8u, w1);
+    }
+    xv = load_x1(rv, t, c0 + tid);
+    if (rv.rms && c0 + tid < D) nwv = ldg<float>(rv.norm_weight + c0 + tid);
+  };
+  float acc = 0.0f;
+  fetch(0);
+  for (uint32_t c0 = 0; c0 < D; c0 += kExactCols) {
+    out.xe[tid] = rv.rms ? xv * (scale * nwv) : xv;
+    __syncthreads();
+    if (r < nr) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        out.prod[r][seg + j] = raw8_get<RD>(w0, j) * out.xe[seg + j];
+        out.prod[r][seg + 8 + j] = raw8_get<RD>(w1, j) * out.xe[seg + 8 + j];
+      }
+    }
+    __syncthreads();
+    if (c0 + kExactCols < D) fetch(c0 + kExactCols);
+    if (tid < nr) acc = chain_sum<false>(out.prod[tid], D - c0 < kExactCols ? D - c0 : kExactCols, acc);
+    __syncthreads();
+  }
+  if (tid < nr) out.ex[out.cl[first + tid]] = acc;
+}
+
+template <int PER>
+__device__ void exact_logits(const RouteView& rv, uint32_t t, Selection<PER>& out, uint32_t first, uint32_t nr,
+                             float scale) {
+  switch (rv.router_dtype) {
+    case OSM_META_F32: exact_logits_rd<OSM_META_F32>(rv, t, out, first, nr, scale); break;
+    case OSM_META_F16: exact_logits_rd<OSM_META_F16>(rv, t, out, first, nr, scale); break;
+    case OSM_ROUTER_AFFINE_Q8: exact_logits_rd<OSM_ROUTER_AFFINE_Q8>(rv, t, out, first, nr, scale); break;
+    default: exact_logits_rd<OSM_META_BF16>(rv, t, out, first, nr, scale); break;
+  }
+}
+
+// The exact path (every thread of the workgroup; out.id/lg/bd hold the
+// device ranking). Rewrites out.id and out.lg; returns whether every expert
+// was recomputed. out.nunresolved gets the unresolved adjacent pairs.
+template <int PER>
+__device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[PER], const float (&b)[PER],
+                             Selection<PER>& out, float mx) {
+  const uint32_t E = rv.expert_count, k = rv.top_k;
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const uint32_t base = tid * PER;
+  if (tid == 0) {
+    float th = INFINITY;
+    for (uint32_t i = 0; i < k; ++i) th = fminf(th, out.lg[i] - kBoundSlack * out.bd[i]);
+    out.scal[0] = th;
+  }
+  const float scale = rv.rms ? exact_rms_scale<PER>(rv, t, out) : 1.0f;  // its barriers publish scal[0]
+  if (!rv.rms) __syncthreads();
+  const float th = out.scal[0];
+  bool full = false;
+  float m = -INFINITY;
+  for (;;) {
+    // Candidates: a compact list in out.cl, wavefront by wavefront.
+    bool member[PER];
+    uint32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const uint32_t e = base + j;
+      // A bound that is not finite admits the expert (NaN comparisons fail).
+      member[j] = e < E && (full || !(l[j] + kBoundSlack * b[j] + tie_margin(mx, l[j]) < th));
+      mine += member[j] ? 1u : 0u;
+    }
+    const float incl = wave_incl_scan(static_cast<float>(mine));  // small integers: exact
+    if (lane == kWave - 1) out.wcount[wave] = static_cast<uint32_t>(incl);
+    __syncthreads();
+    uint32_t pos = static_cast<uint32_t>(incl) - mine;
+    for (uint32_t w = 0; w < wave; ++w) pos += out.wcount[w];
+    const uint32_t nc = out.wcount[0] + out.wcount[1] + out.wcount[2] + out.wcount[3];
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (member[j]) out.cl[pos++] = static_cast<uint16_t>(base + j);
+    __syncthreads();
+    for (uint32_t first = 0; first < nc; first += kExactRows)
+      exact_logits<PER>(rv, t, out, first, nc - first < kExactRows ? nc - first : kExactRows, scale);
+    __syncthreads();
+    float lm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (member[j]) lm = fmaxf(lm, out.ex[base + j]);
+    lm = wave_max(lm);
+    if (lane == 0) out.red[0][wave] = lm;
+    __syncthreads();
+    m = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
+    // The reference's key: exp(fl(L - m)) (reference_ops.cpp:141-145).
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (base + j < E) out.aux[base + j] = member[j] ? expf(out.ex[base + j] - m) : -1.0f;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      if (!member[j]) continue;
+      const uint32_t e = base + j;
+      const float v = out.aux[e];
+      uint32_t rk = 0;
+      for (uint32_t i = 0; i < nc; ++i) {
+        const uint32_t o = out.cl[i];
+        const float w = out.aux[o];
+        rk += (w > v || (w == v && o < e)) ? 1u : 0u;
+      }
+      if (rk <= k) out.fid[rk] = e;
+    }
+    __syncthreads();
+    // Beyond 80 below m the exps near underflow: rank every expert.
+    const bool again = !full && !(out.ex[out.fid[k - 1]] - m >= -kUnderflowGap);
+    if (!again) {
+      if (tid == 0) out.ncand = nc;
+      break;
+    }
+    full = true;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    // Adjacent pairs among the first k + 1 ranked candidates (there are at
+    // least k: the device's picks are candidates).
+    const uint32_t n = out.ncand < k + 1u ? out.ncand : k + 1u;
+    uint32_t unresolved = 0;
+    for (uint32_t i = 0; i + 1 < n; ++i) {
+      const uint32_t a = out.fid[i], c = out.fid[i + 1];
+      if (out.ex[a] == out.ex[c]) continue;  // equal logits, equal keys: the lower id first, certainly
+      const float ea = out.aux[a], ec = out.aux[c];
+      const bool zeros = ea == 0.0f && ec == 0.0f && out.ex[a] - m < -104.0f && out.ex[c] - m < -104.0f;
+      if (!zeros && fabsf(ea - ec) <= 5.0f * 0x1p-23f * fmaxf(ea, ec) + 5.0f * 0x1p-149f) ++unresolved;
+    }
+    out.nunresolved = unresolved;
+    for (uint32_t i = 0; i < k; ++i) {
+      out.id[i] = out.fid[i];
+      out.lg[i] = out.val[out.fid[i]];
+    }
+  }
+  __syncthreads();
+  return full;
+}
+
+// Selection from this thread's device logits l[j] and bounds b[j] of experts
+// tid*PER + j (entries past E are ignored) and their table pointers. Every
+// thread of the workgroup calls it; it ends with a barrier, after which
+// out.id and out.p are complete. `count`: add this selection to the
+// routing counters (one workgroup per token does).
+template <int PER>
+__device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, const float (&l)[PER],
+                                              const float (&b)[PER], const uint8_t* const (&tab)[PER],
+                                              Selection<PER>& out, bool count) {
+  const uint32_t E = rv.expert_count;
+  const uint32_t k = rv.top_k;
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const uint32_t base = tid * PER;
+  uint32_t key[PER], nid[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const bool valid = base + j < E;
+    key[j] = valid ? ordered_key(l[j]) : 0u;  // above 0 for every real logit
+    nid[j] = ~(base + j);
+    if (valid) {
+      out.blob[base + j] = tab[j];
+      out.val[base + j] = l[j];
+      out.aux[base + j] = b[j];
+      mx = fmaxf(mx, l[j]);
+    }
+  }
+  mx = wave_max(mx);
+  if (lane == 0) out.red[0][wave] = mx;
+  sort_lane<PER>(key, nid);
+
+  // This wavefront's top-k by (logit, lower id). Each round is branch-free
+  // (the pop is a select on every lane) and lane r keeps round r's result,
+  // written out after the last round. The loop stays rolled: one body,
+  // fetched once (the selection runs on one workgroup, so its code is cold).
+  uint32_t rk = 0u, ri = 0u;
+#pragma unroll 1
+  for (uint32_t r = 0; r < k; ++r) {
+    const uint32_t mk = wave_max_u32(key[0]);
+    const int wl = __ffsll(__ballot(key[0] == mk)) - 1;  // never empty: mk is some lane's key
+    const uint32_t sid = ~static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(nid[0]), wl));
+    rk = lane == r ? mk : rk;
+    ri = lane == r ? sid : ri;
+    const bool won = static_cast<int>(lane) == wl;  // pop the head
+#pragma unroll
+    for (int j = 0; j + 1 < PER; ++j) {
+      key[j] = won ? key[j + 1] : key[j];
+      nid[j] = won ? nid[j + 1] : nid[j];
+    }
+    key[PER - 1] = won ? 0u : key[PER - 1];
+    nid[PER - 1] = won ? 0u : nid[PER - 1];
+  }
+  if (lane < k) out.cand[wave * k + lane] = (static_cast<uint64_t>(rk) << 32) | ~ri;
+  __syncthreads();
+  mx = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
+
+  // The softmax denominator over every expert (reference_ops.cpp:135-151),
+  // its four wavefront sums combined in a fixed order.
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sum += (base + j < E) ? expf(l[j] - mx) : 0.0f;
+  sum = wave_sum(sum);
+  if (lane == 0) out.red[1][wave] = sum;
+
+  // Wavefront 0: each lane ranks one candidate against all of them (LDS
+  // broadcast reads); the k best write their place. Candidates of key 0
+  // (fewer than k experts in a wavefront) always have k real ones above.
+  if (wave == 0) {
+    const uint32_t nc = kSelWaves * k;
+    const uint64_t mine = lane < nc ? out.cand[lane] : 0u;
+    uint32_t rank = 0;
+#pragma unroll 4
+    for (uint32_t c = 0; c < nc; ++c) rank += out.cand[c] > mine ? 1u : 0u;
+    if (lane < nc && rank < k) {
+      const uint32_t id0 = ~static_cast<uint32_t>(mine);
+      const uint32_t id = id0 < E ? id0 : E - 1u;  // a table lookup always stays in the table
+      out.id[rank] = id;
+      out.lg[rank] = out.val[id];
+      out.bd[rank] = out.aux[id];
+    }
+  }
+  __syncthreads();
+  sum = ((out.red[1][0] + out.red[1][1]) + out.red[1][2]) + out.red[1][3];
+
+  // The certificate: every expert outside the picks below the k-th's lower
+  // bound, and (thread 0) the picks in order and far from underflow.
+  const float lk = out.lg[k - 1];
+  const float low = lk - kBoundSlack * out.bd[k - 1];
+  const uint64_t kth = (static_cast<uint64_t>(ordered_key(lk)) << 32) | ~out.id[k - 1];
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t e = base + j;
+    const uint64_t c = (static_cast<uint64_t>(ordered_key(l[j])) << 32) | ~e;
+    if (e < E && c < kth && !(l[j] + kBoundSlack * b[j] + tie_margin(mx, l[j]) < low)) bad = true;
+  }
+  if (tid == 0) {
+    for (uint32_t i = 0; i + 1 < k; ++i) {
+      const float need = kBoundSlack * (out.bd[i] + out.bd[i + 1]) +
+                         (out.id[i] > out.id[i + 1] ? tie_margin(mx, out.lg[i + 1]) : 0.0f);
+      if (!(out.lg[i] - out.lg[i + 1] > need)) bad = true;
+    }
+    if (!(lk - mx >= -kUnderflowGap)) bad = true;
+  }
+  bad = __syncthreads_or(bad) != 0;
+  bool full = false;
+  if (bad) full = select_exact<PER>(rv, t, l, b, out, mx);
+  if (tid < k) out.p[tid] = expf(out.lg[tid] - mx) / sum;
+  if (count && tid == 0 && rv.stats != nullptr) {
+    atomicAdd(rv.stats + 0, 1u);
+    if (bad) atomicAdd(rv.stats + 1, 1u);
+    if (full) atomicAdd(rv.stats + 2, 1u);
+    if (bad && out.nunresolved != 0u) atomicAdd(rv.stats + 3, out.nunresolved);
+  }
+  __syncthreads();
+}
+
+// Loads token t's logits and their bounds (and table pointers) and selects;
+// every thread of the workgroup calls it.
+template <int PER>
+__device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out, bool count) {
+  const uint32_t E = rv.expert_count;
+  const uint32_t D = rv.hidden;
+  const float* lg = rv.logits + static_cast<size_t>(t) * E;
+  const uint32_t base = threadIdx.x * PER;
+  float p[PER], bnd[PER];
+  const uint8_t* tab[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t e = (base + j < E) ? base + j : E - 1u;  // clamped: every load in bounds
+    if (rv.planes != nullptr) {
+      // Partial sums of the router GEMM's K ranges, added in plane order.
+      // Range r of R columns starts at the running sum P_r, so its prefix
+      // sums are bounded by R |P_r| plus the plane's own part.
+      const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
+      const size_t o = static_cast<size_t>(t) * (E + 1u) + e;
+      const float* pl = rv.planes + o;
+      float v = pl[0];
+      float rs = 0.0f, as = 0.0f;
+      const float cols = static_cast<float>(D / rv.parts);
+      if (rv.bound_planes != nullptr) {
+        rs = rv.bound_planes[o];
+        as = rv.bound_planes[ps + o];
+      }
+      for (uint32_t part = 1; part < rv.parts; ++part) {
+        if (rv.bound_planes != nullptr) {
+          rs += rv.bound_planes[2u * part * ps + o] + cols * fabsf(v);
+          as += rv.bound_planes[(2u * part + 1u) * ps + o];
+        }
+        v += pl[part * ps];
+      }
+      p[j] = v;
+      // Per plane: rs bounds the sum of |prefix sums| in the reference's
+      // order, as bounds the sum of |w x|, which the GEMM's own rounding
+      // and the reference's products are proportional to.
+      const float cA = 112.0f + static_cast<float>(D) * static_cast<float>(D) * 0x1p-24f;
+      bnd[j] = rv.bound_planes != nullptr ? kBoundSlack * 0x1p-24f * (rs + cA * as) : INFINITY;
+      if (base + j < E) rv.logits_out[static_cast<size_t>(t) * E + e] = v;
+    } else {
+      p[j] = lg[e];
+      bnd[j] = rv.bounds != nullptr ? rv.bounds[static_cast<size_t>(t) * E + e] : INFINITY;
+    }
+    tab[j] = rv.expert_table ? rv.expert_table[e] : nullptr;
+  }
+  if (rv.planes != nullptr && rv.has_shared && threadIdx.x == 0) {
+    const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
+    const float* pl = rv.planes + static_cast<size_t>(t) * (E + 1u) + E;
+    float g = pl[0];
+    for (uint32_t part = 1; part < rv.parts; ++part) g += pl[part * ps];
+    rv.gate_out[t] = 1.0f / (1.0f + expf(-g));  // reference_ops.cpp:214-216
+  }
+  select_values<PER>(rv, t, p, bnd, tab, out, count);
+}
+
+template <int PER>
+__device__ __forceinline__ const uint8_t* pick_blob(const RouteView& rv, const Selection<PER>& s,
+                                                    uint32_t r) {
+  const uint8_t* b = rv.expert_table ? s.blob[s.id[r]] : nullptr;
+  return b ? b : rv.fallback;
+}
+
+// Writes the selection of token t: ids and weights in pick order, the
+// selected mass summed in pick order and the optional renormalisation
+// (qwen_router.cpp:72-91), and each slot's blob (shared expert last).
+// Threads tid <= k of the workgroup take part.
+template <int PER>
+__device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t t, uint32_t tid,
+                                                  const Selection<PER>& s) {
+  const uint32_t k = rv.top_k;
+  const uint32_t nslot = k + rv.has_shared;
+  if (tid == 0) {
+    float mass = 0.0f;
+    for (uint32_t r = 0; r < k; ++r) mass = mass + s.p[r];
+    for (uint32_t r = 0; r < k; ++r) {
+      rv.ids[static_cast<size_t>(t) * k + r] = s.id[r];
+      rv.weights[static_cast<size_t>(t) * k + r] = rv.norm_topk_prob ? s.p[r] / mass : s.p[r];
+    }
+    rv.mass[t] = mass;
+  }
+  if (tid < k)
+    rv.slot_ptrs[static_cast<size_t>(t) * nslot + tid] = pick_blob(rv, s, tid);
+  else if (tid == k && nslot > k)
+    rv.slot_ptrs[static_cast<size_t>(t) * nslot + k] = rv.shared_expert;
+}
+
+template <int PER>
+__global__ __launch_bounds__(kSelThreads) void select_kernel(RouteView rv) {
+  __shared__ Selection<PER> sel;
+  select_block<PER>(rv, blockIdx.x, sel, true);
+  publish_selection(rv, blockIdx.x, threadIdx.x, sel);
+}
+
+// ---------------------------------------------------------------------------
+// Router GEMV. A wavefront owns one router row; lane l reads elements
+// l*8 + 512u .. +8 (u = 0, 1, ...), kept as loaded until the FMA.
+
 // Token t's input, RMS-normalised when the flags ask for it
 // (reference_ops.cpp:96-128), into xs[D] in LDS; write_norm also stores it to
 // x_norm. Every workgroup that needs x normalises its own copy: the values
@@ -433,9 +794,30 @@ __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, floa
 // vector): logits, or the sigmoid shared gate (reference_ops.cpp:214-216).
 // RCH loads of 8 elements per lane cover hidden <= 512 * RCH.
 // also(row, value) runs on lane 0 after each row's store (row E: the gate).
-template <int RD, int RCH, typename Also>
-__device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, uint32_t blk, float* xs,
-                                            Also&& also) {
+
+// Router rows blk*4 .. blk*4+3 of token t (row E is the shared-expert gate
+// vector): logits, or the sigmoid shared gate (reference_ops.cpp:214-216).
+// RCH loads of 8 elements per lane cover hidden <= 512 * RCH.
+//
+// Each logit also gets its bound (when a.logit_bounds is set). With u =
+// 2^-24 and p_c = w_c x_c:
+//  - the reference sums acc = acc + p_c in column order, rounding each
+//    product and sum, so its error is at most u (sum_c |p_c| + sum_c |S_c|),
+//    S_c its partial sums; |S_c| <= |P_c| + (a second-order term), P_c the
+//    exact prefix sums;
+//  - this kernel's sum (an FMA chain over each lane's 8-column chunk, the
+//    lane's chunks in order, then the wavefront tree) has error at most
+//    (8 + chunks per lane + 6) u sum_c |p_c|;
+//  - an RMS-normalised input differs from the reference's by a common factor
+//    (handled by the selection) and per element by at most 4 u.
+// sum_c |P_c| is taken over the chunks in column order: chunk (u, lane)
+// starts at the exclusive prefix of the chunk sums (a wavefront scan per u
+// plus the totals of the u before), and its 8 prefix sums are at most
+// 8 |start| + the sum of |its own partial sums|. The bound written is
+// (1 + 2^-9) u (sum |P_c| + (32 + chunks + n^2 u) sum |p_c|), n the width,
+// which the bound's own rounding leaves above the true one.
+template <int RD, int RCH>
+__device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, uint32_t blk, float* xs) {
   const uint32_t D = a.geom.hidden;
   const uint32_t E = a.expert_count;
   const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -465,20 +847,53 @@ __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, 
   }
   stage_x(a, t, xs, blk == 0);
   if (row < nrows) {
-    float acc = 0.0f;
+    const bool bound = row < E && a.logit_bounds != nullptr;
+    float cs[RCH], qa[RCH];
+    float acc = 0.0f, aa = 0.0f;
 #pragma unroll
     for (int u = 0; u < RCH; ++u) {
       const uint32_t c = lane * 8u + u * 8u * kWave;
+      cs[u] = 0.0f;
+      qa[u] = 0.0f;
       if (c < D) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf(raw8_get<RD>(w[u], j), xs[c + j], acc);
+        for (int j = 0; j < 8; ++j) {
+          const float v = raw8_get<RD>(w[u], j), xv = xs[c + j];
+          cs[u] = fmaf(v, xv, cs[u]);
+          aa = fmaf(fabsf(v), fabsf(xv), aa);
+          qa[u] += fabsf(cs[u]);
+        }
       }
+      acc += cs[u];
+    }
+    float rsum = 0.0f;
+    if (bound) {
+      float carry = 0.0f;
+#pragma unroll
+      for (int u = 0; u < RCH; ++u) {
+        if (u * 8u * kWave < D) {  // wavefront-uniform
+          const float incl = wave_incl_scan(cs[u]);
+          const uint32_t c = lane * 8u + u * 8u * kWave;
+          if (c < D) rsum += 8.0f * fabsf(carry + (incl - cs[u])) + qa[u];
+          carry += readlane_f(incl, 63);
+        }
+      }
+      rsum = wave_sum(rsum);
+      aa = wave_sum(aa);
     }
     acc = wave_sum(acc);
     if (lane == 0) {
-      const float v = row < E ? acc : 1.0f / (1.0f + expf(-acc));
-      *(row < E ? a.logits + static_cast<size_t>(t) * E + row : a.shared_gate + t) = v;
-      also(row, v);
+      if (row < E) {
+        a.logits[static_cast<size_t>(t) * E + row] = acc;
+        if (bound) {
+          const float n = static_cast<float>(D);
+          const float chunks = static_cast<float>((D + 8u * kWave - 1u) / (8u * kWave));
+          a.logit_bounds[static_cast<size_t>(t) * E + row] =
+              kBoundSlack * 0x1p-24f * (rsum + (32.0f + chunks + n * n * 0x1p-24f) * aa);
+        }
+      } else {
+        a.shared_gate[t] = 1.0f / (1.0f + expf(-acc));
+      }
     }
   }
 }
@@ -486,7 +901,7 @@ __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, 
 template <int RD>
 __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
   extern __shared__ __align__(16) float xs[];  // [D] normalised input of this token
-  route_block<RD, 16>(a, blockIdx.y, blockIdx.x, xs, [](uint32_t, float) {});
+  route_block<RD, 16>(a, blockIdx.y, blockIdx.x, xs);
 }
 
 // ---------------------------------------------------------------------------
@@ -532,21 +947,13 @@ __device__ __forceinline__ void load_xr(const float* x, uint32_t nch, uint32_t l
 // store(index, value): h[t, j, row] at index (t * nslot + j) * I + row.
 template <int META, int CPL, int ROWS, typename Store>
 __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, uint32_t j, uint32_t blk,
-                                             const uint8_t* blob, const float (&xr)[CPL][32], Store&& store) {
+                                             const uint8_t* blob, float (&xr)[CPL][32], Store&& store) {
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = threadIdx.x / kWave;
   const uint32_t D = p.g.hidden, I = p.g.inter, G = p.g.group;
   const uint32_t nch = D / 32u;  // 16-byte chunks per row
   const uint32_t gpr = D / G;    // groups per row
   const osm_expert_offsets off = osm_expert_layout(p.g);
-  float xsum[CPL];
-#pragma unroll
-  for (int ci = 0; ci < CPL; ++ci) {
-    xsum[ci] = 0.0f;
-#pragma unroll
-    for (int v = 0; v < 32; ++v) xsum[ci] += xr[ci][v];
-  }
-
   const uint32_t r0 = (blk * kGuWaves + wave) * ROWS;
   uint4 qg[ROWS][CPL], qu[ROWS][CPL];
   uint32_t sg[ROWS][CPL], bg[ROWS][CPL];
@@ -567,6 +974,15 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
       su[i][ci] = meta_bits<META>(blob + off.up_s, gi);
       bu[i][ci] = meta_bits<META>(blob + off.up_b, gi);
     }
+  }
+  // The lane's slices of x (and their sums), loaded while the weights are in flight.
+  load_xr<CPL>(p.x + static_cast<size_t>(t) * D, nch, lane, xr);
+  float xsum[CPL];
+#pragma unroll
+  for (int ci = 0; ci < CPL; ++ci) {
+    xsum[ci] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 32; ++v) xsum[ci] += xr[ci][v];
   }
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
@@ -591,17 +1007,15 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
   const uint32_t t = blockIdx.z;
   const uint32_t j = blockIdx.y;
   const uint32_t D = p.g.hidden;
-  float xr[CPL][32];
-  load_xr<CPL>(p.x + static_cast<size_t>(t) * D, D / 32u, lane, xr);
 
   const uint8_t* blob;
   if constexpr (PER > 0) {
-    // Routed slot: the workgroup selects with its x slices loaded; block
-    // (0, 0) also publishes the selection.
+    // Routed slot: the workgroup selects first; block (0, 0) also publishes
+    // the selection and counts it.
     const RouteView& rv = p.rv;
     __shared__ Selection<PER> sel;
     if (j < rv.top_k) {
-      select_block<PER>(rv, t, sel);
+      select_block<PER>(rv, t, sel, blockIdx.x == 0 && j == 0);
       if (blockIdx.x == 0 && j == 0) publish_selection(rv, t, threadIdx.x, sel);
       blob = pick_blob(rv, sel, j);
     } else {
@@ -611,6 +1025,9 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
     blob = p.src.blob(t, j);
   }
   if (blob == nullptr) blob = p.rv.fallback;  // never dereference a null slot
+  // x is read with the weights, after the selection, so its slices are not
+  // held in registers through it; both loads are in flight together.
+  float xr[CPL][32];
   gate_up_rows<META, CPL, ROWS>(p, t, j, blockIdx.x, blob, xr, [&](size_t i, float v) { p.h[i] = v; });
 }
 
@@ -638,164 +1055,10 @@ size_t down_lds_bytes(uint32_t inter, uint32_t nslot, uint32_t rows_per_block) {
   return (chunks * (kChunkStride + 1u) + 2u * rows_per_block) * sizeof(float);
 }
 
-// ---------------------------------------------------------------------------
-// Single-launch decode: how its workgroups hand data to each other.
-//
-// A one-token decode with every expert resident runs as one grid: router
-// workgroups (4 router rows each), one selector, gate/up workgroups (the
-// shared expert's first), down workgroups. A workgroup waits only on
-// workgroups with lower indices, which the dispatcher starts first.
-//
-// Everything handed from one workgroup to another -- the logits and shared
-// gate, the selection, h -- travels as 8-byte elements that carry the launch
-// number next to the value, each written with one agent-scope atomic store
-// and read with agent-scope atomic loads (coherent across the XCDs' separate
-// L2 caches; no L2 write-back or invalidate is involved). A reader re-reads
-// an element until its tag is this launch's number: the read is the wait.
-// The selector writes one record per slot (tag, expert id, weight), in eight
-// copies, so the readers on the XCD that workgroup b runs on (b % 8) share
-// one copy. h is 22 KB that every down workgroup reads, too much to re-read
-// while waiting: each gate/up workgroup, once its h stores are complete
-// (s_waitcnt vmcnt(0) in every wavefront, then a barrier), adds 1 to its
-// slot's done counter, and down workgroups poll the slot counters (one lane
-// each) before reading h, whose tags they still check. h rotates through
-// four buffers (launch number mod 4) and is first read with ordinary loads,
-// served by the reader's L2 after one miss per XCD: each 128-byte line of it
-// is written whole by one workgroup with write-through stores, so a miss
-// fetches it complete, and a line some L2 still holds from four launches
-// back carries an old tag and is read again with coherent loads.
-//
-// Launch numbers come from a per-workgroup counter, read and advanced once
-// per launch, so nothing is reset between launches. Every wait gives up after
-// kSpinLimit re-reads and sets the sticky error word; the workgroup then
-// goes on with what it read.
-constexpr uint32_t kSpinLimit = 1u << 20;
-constexpr uint32_t kRecordCopies = 8;
-constexpr uint32_t kRecordSlots = 16;
-constexpr uint32_t kSharedId = 0xFFFFu;  // record id of the shared expert
-constexpr uint32_t kHBuffers = 4;        // h buffers, by launch number mod 4
-
-__device__ __forceinline__ void store_tagged(uint64_t* p, uint32_t epoch, float v) {
-  __hip_atomic_store(p, (static_cast<uint64_t>(epoch) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t load_tagged(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool tag_current(uint64_t v, uint32_t epoch) {
-  return static_cast<uint32_t>(v >> 32) == epoch;
-}
-__device__ __forceinline__ float tagged_value(uint64_t v) { return __uint_as_float(static_cast<uint32_t>(v)); }
-// Selection record: tag (low 16 bits of the launch number), expert id, weight.
-__device__ __forceinline__ uint64_t record_of(uint32_t epoch, uint32_t id, float w) {
-  return (static_cast<uint64_t>(epoch & 0xFFFFu) << 48) | (static_cast<uint64_t>(id & 0xFFFFu) << 32) |
-         __float_as_uint(w);
-}
-__device__ __forceinline__ bool record_current(uint64_t v, uint32_t epoch) {
-  return static_cast<uint32_t>(v >> 48) == (epoch & 0xFFFFu);
-}
-
-// Byte offsets of the handshake buffer's parts (the error word is at 0).
-struct FusedLayout {
-  size_t launch, logits, record, done, h, bytes;
-};
-__host__ __device__ inline size_t round_up128(size_t n) { return (n + 127u) & ~static_cast<size_t>(127u); }
-__host__ __device__ inline FusedLayout fused_layout(uint32_t grid, uint32_t experts, uint32_t nslot,
-                                                    uint32_t inter) {
-  FusedLayout l;
-  l.launch = 128u;
-  l.logits = l.launch + round_up128(static_cast<size_t>(grid) * 4u);
-  l.record = l.logits + round_up128((static_cast<size_t>(experts) + 1u) * 8u);
-  l.done = l.record + static_cast<size_t>(kRecordCopies) * kRecordSlots * 8u;
-  l.h = l.done + static_cast<size_t>(kRecordSlots) * 128u;  // one counter per slot, 128 bytes apart
-  l.bytes = l.h + kHBuffers * round_up128(static_cast<size_t>(nslot) * inter * 8u);
-  return l;
-}
-
-struct FusedWaits {
-  uint32_t* err;
-  uint32_t epoch;
-  const uint64_t* record;  // this workgroup's copy
-  const uint64_t* h;       // this launch's tagged h [nslot][I]
-  const uint32_t* done;    // per-slot gate/up done counters, 128 bytes apart
-  uint32_t gu_per_slot;    // gate/up workgroups per slot
-  uint64_t* mark;          // this workgroup's timeline slots, or null
-  const RouteView* rv;
-  const uint8_t** s_blob;  // LDS: blob of each slot
-  float* s_w;              // LDS: weight of each slot
-};
-
-// Optional timeline of a single launch: thread 0 stamps the steady clock into
-// slot i of its workgroup's 8 (slot 7: the hardware id of its compute unit).
-__device__ __forceinline__ void stamp(uint64_t* mark, int i) {
-  if (mark != nullptr && threadIdx.x == 0) mark[i] = static_cast<uint64_t>(wall_clock64());
-}
-
-// Whether a wait should stop: out of spins, or another wait already gave up.
-__device__ __forceinline__ bool give_up(uint32_t spin, uint32_t* err) {
-  if (spin >= kSpinLimit ||
-      ((spin & 255u) == 255u && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)) {
-    __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return true;
-  }
-  return false;
-}
-
-// Lanes r < n of the calling wavefront read record slot r until it is this
-// launch's; returns the lane's record.
-__device__ __forceinline__ uint64_t read_record(const FusedWaits& fw, uint32_t n) {
-  const uint32_t lane = threadIdx.x % kWave;
-  uint64_t v = 0;
-  for (uint32_t spin = 0;; ++spin) {
-    bool ok = true;
-    if (lane < n) {
-      v = load_tagged(fw.record + lane);
-      ok = record_current(v, fw.epoch);
-    }
-    if (__all(ok)) break;
-    if (give_up(spin, fw.err)) break;
-    __builtin_amdgcn_s_sleep(2);
-  }
-  return v;
-}
-
-// s_waitcnt immediate with vmcnt = 0 and the other counters not waited on
-// (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
-constexpr int kWaitVmcnt0 = 0x0F70;
-
-// Lanes c < n of the calling wavefront poll counter c (128 bytes apart from
-// `first`) until it reaches `target`; the others wait with them.
-__device__ __forceinline__ void wait_counters(const uint32_t* first, uint32_t n, uint32_t target, uint32_t* err) {
-  const uint32_t lane = threadIdx.x % kWave;
-  for (uint32_t spin = 0;; ++spin) {
-    bool ok = true;
-    if (lane < n) {
-      const uint32_t v = __hip_atomic_load(const_cast<uint32_t*>(first) + lane * 32u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      ok = static_cast<int32_t>(v - target) >= 0;
-    }
-    if (__all(ok)) break;
-    if (give_up(spin, err)) break;
-    __builtin_amdgcn_s_sleep(4);
-  }
-}
-
-// Blob of a record: the table entry of its expert (the fallback for a null
-// entry or an id out of range), or the shared expert.
-__device__ __forceinline__ const uint8_t* record_blob(const RouteView& rv, uint64_t rec) {
-  const uint32_t id = static_cast<uint32_t>(rec >> 32) & 0xFFFFu;
-  if (id == kSharedId) return rv.shared_expert;
-  const uint8_t* b = id < rv.expert_count ? rv.expert_table[id] : nullptr;
-  return b ? b : rv.fallback;
-}
 
 // down + weighted accumulate for rows blk * rows_per_block ... of token t.
-// FUSED: the slot pointers and weights are read once the selection is out,
-// and h once every gate/up workgroup is done; the down weights are already
-// in flight while h is awaited.
-template <int META, int LPR, int MAXS, bool FUSED>
-__device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint32_t blk, float* hs,
-                                           const FusedWaits& fw) {
+template <int META, int LPR, int MAXS>
+__device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint32_t blk, float* hs) {
   constexpr uint32_t kRowsPerGroup = kWave / LPR;
   constexpr uint32_t kRowsPerBlock = down_rows_per_block<LPR>();
   constexpr int kSlotsPerWave = (MAXS + 1) / 2;
@@ -823,63 +1086,13 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   constexpr int kH4PerThread = 8;
   float4 hv[kH4PerThread];
   auto load_h = [&](uint32_t pass) {
-    if constexpr (FUSED) {
-      // h comes from the gate/up workgroups of this launch: an ordinary
-      // read first, then coherent re-reads until every element this thread
-      // stages carries the launch number.
-      for (uint32_t spin = 0;; ++spin) {
-        bool ok = true;
 #pragma unroll
-        for (int u = 0; u < kH4PerThread; ++u) {
-          const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
-          if (f < n4) {
-            const uint64_t* src = fw.h + static_cast<size_t>(t) * nslot * I + static_cast<size_t>(f) * 4u;
-            uint64_t v0, v1, v2, v3;
-            if (spin == 0) {
-              const uint4 a = *reinterpret_cast<const uint4*>(src);
-              const uint4 c = *reinterpret_cast<const uint4*>(src + 2);
-              v0 = (static_cast<uint64_t>(a.y) << 32) | a.x;
-              v1 = (static_cast<uint64_t>(a.w) << 32) | a.z;
-              v2 = (static_cast<uint64_t>(c.y) << 32) | c.x;
-              v3 = (static_cast<uint64_t>(c.w) << 32) | c.z;
-            } else {
-              v0 = load_tagged(src);
-              v1 = load_tagged(src + 1);
-              v2 = load_tagged(src + 2);
-              v3 = load_tagged(src + 3);
-            }
-            ok = ok && tag_current(v0, fw.epoch) && tag_current(v1, fw.epoch) && tag_current(v2, fw.epoch) &&
-                 tag_current(v3, fw.epoch);
-            hv[u] = make_float4(tagged_value(v0), tagged_value(v1), tagged_value(v2), tagged_value(v3));
-          } else {
-            hv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-          }
-        }
-        if (ok || give_up(spin, fw.err)) break;
-        if (spin > 0) __builtin_amdgcn_s_sleep(2);
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < kH4PerThread; ++u) {
-        const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
-        hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+    for (int u = 0; u < kH4PerThread; ++u) {
+      const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
+      hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  if constexpr (FUSED) {
-    // Each slot's blob and weight from this launch's selection record.
-    if (wave == 0) {
-      const uint64_t rec = read_record(fw, nslot);
-      if (lane < nslot) {
-        fw.s_blob[lane] = record_blob(*fw.rv, rec);
-        fw.s_w[lane] = __uint_as_float(static_cast<uint32_t>(rec));
-      }
-    }
-    __syncthreads();
-    stamp(fw.mark, 1);
-  } else {
-    load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
-  }
+  load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
 
   // This wavefront's slots: pointers and weights (uniform loads), then the
   // packed chunk and metadata of each, with no branch between them. Slots
@@ -890,16 +1103,11 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   for (int i = 0; i < kSlotsPerWave; ++i) {
     const uint32_t j = half + 2u * i;
     const uint32_t js = j < nslot ? j : 0u;
-    if constexpr (FUSED) {
-      bp[i] = fw.s_blob[js];
-      w[i] = fw.s_w[js];
-    } else {
-      bp[i] = p.src.blob(t, js);
-      if (js < p.top_k)
-        w[i] = p.weights ? p.weights[static_cast<size_t>(t) * p.top_k + js] : 1.0f;
-      else
-        w[i] = p.shared_gate ? p.shared_gate[t] : 1.0f;
-    }
+    bp[i] = p.src.blob(t, js);
+    if (js < p.top_k)
+      w[i] = p.weights ? p.weights[static_cast<size_t>(t) * p.top_k + js] : 1.0f;
+    else
+      w[i] = p.shared_gate ? p.shared_gate[t] : 1.0f;
     if (j >= nslot || bp[i] == nullptr) w[i] = 0.0f;
     if (bp[i] == nullptr) bp[i] = p.fallback;
   }
@@ -912,13 +1120,6 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
     q[i] = ldg16(bp[i] + off.down_q + qo);
     sb[i] = meta_bits<META>(bp[i] + off.down_s, gi);
     bb[i] = meta_bits<META>(bp[i] + off.down_b, gi);
-  }
-  if constexpr (FUSED) {
-    stamp(fw.mark, 2);
-    if (wave == 0) wait_counters(fw.done, nslot, fw.epoch * fw.gu_per_slot, fw.err);
-    __syncthreads();
-    load_h(0);
-    stamp(fw.mark, 3);
   }
 
   // Stage h and its per-chunk sums: 8 consecutive threads hold one 32-float
@@ -966,162 +1167,14 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
       p.y[o] = p.residual ? p.residual[o] + v : v;
     }
   }
-  if constexpr (FUSED) stamp(fw.mark, 4);
 }
 
 template <int META, int LPR, int MAXS>
 __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   extern __shared__ __align__(16) float hs[];  // chunks, then chunk sums, then [2][rows] halves
-  down_block<META, LPR, MAXS, false>(p, blockIdx.y, blockIdx.x, hs, FusedWaits{});
+  down_block<META, LPR, MAXS>(p, blockIdx.y, blockIdx.x, hs);
 }
 
-// ---------------------------------------------------------------------------
-// The single-launch decode kernel (one token, every expert resident). Blocks
-// [0, nr) route, then ngu gate/up blocks (the shared expert's first), then
-// the down blocks. Each phase runs the code of the three-kernel decode above,
-// so both give the same bits.
-constexpr int kFusedRouteLoads = 4;  // hidden <= 2048
-constexpr int kFusedMaxSlots = 12;
-constexpr int kFusedPer = 2;  // experts <= 512
-
-struct FusedParams {
-  osmd_moe_args a;
-  GateUpParams gp;
-  DownParams dp;
-  uint32_t* sync;   // handshake buffer (fused_layout)
-  uint64_t* trace;  // [grid][8] timeline, or null
-  uint32_t nr, ngu, gu_blocks_per_slot, grid;
-};
-
-template <int RD, int META, int LPR>
-__global__ __launch_bounds__(256) void fused_decode_kernel(FusedParams f) {
-  extern __shared__ __align__(16) float lds[];  // x of the token, or the down staging
-  __shared__ uint32_t s_epoch;
-  __shared__ Selection<kFusedPer> sel;
-  __shared__ const uint8_t* s_blob[kFusedMaxSlots];
-  __shared__ float s_w[kFusedMaxSlots];
-  const uint32_t b = blockIdx.x;
-  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  uint8_t* base = reinterpret_cast<uint8_t*>(f.sync);
-  const FusedLayout lay = fused_layout(f.grid, f.a.expert_count, f.gp.src.nslot, f.a.geom.inter);
-  uint32_t* err = f.sync;
-  uint32_t* launch = reinterpret_cast<uint32_t*>(base + lay.launch);
-  uint64_t* tl = reinterpret_cast<uint64_t*>(base + lay.logits);  // tagged logits, then the gate
-  uint64_t* rec = reinterpret_cast<uint64_t*>(base + lay.record);
-  uint64_t* th = reinterpret_cast<uint64_t*>(base + lay.h);  // then + (e % 4) buffers, below
-  uint32_t* done = reinterpret_cast<uint32_t*>(base + lay.done);
-  uint64_t* mark = f.trace ? f.trace + static_cast<size_t>(b) * 8u : nullptr;
-  stamp(mark, 0);
-  if (mark != nullptr && tid == 0) mark[7] = __smid();
-  // This launch's number, from the workgroup's own launch counter.
-  if (tid == 0) {
-    const uint32_t e = __hip_atomic_load(launch + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    __hip_atomic_store(launch + b, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_epoch = e;
-  }
-  const RouteView& rv = f.gp.rv;
-  const uint32_t k = f.a.top_k, E = f.a.expert_count;
-  const uint32_t nslot = f.gp.src.nslot;
-
-  if (b < f.nr) {
-    // Router rows; stage_x's barrier makes s_epoch visible before the stores.
-    route_block<RD, kFusedRouteLoads>(f.a, 0u, b, lds,
-                                      [&](uint32_t row, float v) { store_tagged(tl + row, s_epoch, v); });
-    stamp(mark, 1);
-    return;
-  }
-  __syncthreads();
-  const uint32_t e = s_epoch;
-  th += static_cast<size_t>(e % kHBuffers) * (round_up128(static_cast<size_t>(nslot) * f.a.geom.inter * 8u) / 8u);
-  if (b == f.nr) {
-    // The selector: every thread reads its experts' tagged logits (thread 0
-    // also the gate) until the whole workgroup has this launch's, selects,
-    // and threads r < nslot write the records.
-    const uint32_t bs = tid * kFusedPer;
-    float pv[kFusedPer];
-    const uint8_t* tab[kFusedPer];
-#pragma unroll
-    for (int j = 0; j < kFusedPer; ++j) {
-      tab[j] = rv.expert_table[(bs + j < E) ? bs + j : E - 1u];
-      // Loaded here, while the logits are still being computed: left alone,
-      // the compiler issues these loads after the wait below.
-      asm volatile("" : : "v"(tab[j]));
-    }
-    const bool has_shared = nslot > k;
-    for (uint32_t spin = 0;; ++spin) {
-      bool ok = true;
-#pragma unroll
-      for (int j = 0; j < kFusedPer; ++j) {
-        const uint64_t v = load_tagged(tl + ((bs + j < E) ? bs + j : E - 1u));
-        ok = ok && tag_current(v, e);
-        pv[j] = tagged_value(v);
-      }
-      if (has_shared && tid == 0) {
-        const uint64_t v = load_tagged(tl + E);
-        ok = ok && tag_current(v, e);
-        s_w[0] = tagged_value(v);
-      }
-      // Both exits are decided for the whole workgroup (the loop holds barriers).
-      if (__syncthreads_and(ok)) break;
-      if (__syncthreads_or(tid == 0 && give_up(spin, err))) break;
-      __builtin_amdgcn_s_sleep(2);
-    }
-    const float gate = s_w[0];
-    stamp(mark, 1);
-    select_values<kFusedPer>(rv, pv, tab, sel, mark);
-    stamp(mark, 2);
-    // Records: weights as the per-token kernels publish them (p / mass in
-    // pick order when renormalised), the shared expert last with its gate.
-    if (tid < nslot) {
-      float mass = 0.0f;
-      for (uint32_t r = 0; r < k; ++r) mass = mass + sel.p[r];
-      const uint64_t my = tid < k ? record_of(e, sel.id[tid], rv.norm_topk_prob ? sel.p[tid] / mass : sel.p[tid])
-                                  : record_of(e, kSharedId, gate);
-#pragma unroll
-      for (uint32_t c = 0; c < kRecordCopies; ++c)
-        __hip_atomic_store(rec + c * kRecordSlots + tid, my, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    stamp(mark, 3);
-    publish_selection(rv, 0u, tid, sel);  // ids, weights, mass, slot pointers for the host
-    stamp(mark, 4);
-    return;
-  }
-  FusedWaits fw{err, e, rec + (b % kRecordCopies) * kRecordSlots, th, done, f.gu_blocks_per_slot, mark, &rv,
-                s_blob, s_w};
-  const uint32_t g = b - f.nr - 1u;
-  if (g < f.ngu) {
-    const uint32_t si = g / f.gu_blocks_per_slot, blk = g % f.gu_blocks_per_slot;
-    const uint32_t j = (f.a.flags & OSMD_MOE_SHARED) ? (si == 0 ? k : si - 1u) : si;
-    stage_x(f.a, 0u, lds, false);
-    stamp(mark, 1);
-    float xr[1][32];
-    load_xr<1>(lds, f.a.geom.hidden / 32u, lane, xr);
-    const uint8_t* blob;
-    if (j < k) {
-      if (wave == 0) {
-        FusedWaits one = fw;
-        one.record += j;
-        const uint64_t r = read_record(one, 1u);
-        if (lane == 0) s_blob[0] = record_blob(rv, r);
-      }
-      __syncthreads();
-      blob = s_blob[0];
-    } else {
-      blob = f.a.shared_expert;
-    }
-    if (blob == nullptr) blob = f.a.fallback_blob;
-    stamp(mark, 2);
-    gate_up_rows<META, 1, kGuRowsOneToken>(f.gp, 0u, j, blk, blob, xr,
-                                           [&](size_t i, float v) { store_tagged(th + i, e, v); });
-    stamp(mark, 3);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this wavefront's h stores are complete
-    __syncthreads();
-    if (tid == 0) __hip_atomic_fetch_add(done + j * 32u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    stamp(mark, 4);
-    return;
-  }
-  down_block<META, LPR, kFusedMaxSlots, true>(f.dp, 0u, g - f.ngu, lds, fw);
-}
 
 // ---------------------------------------------------------------------------
 // Host-side launchers.
@@ -1211,10 +1264,10 @@ int launch_down(const DownParams& dp, uint32_t tokens, hipStream_t st) {
   }
 }
 
-// Experts per lane of a selection: 8 up to 512 experts, 16 beyond. One width
+// Experts per lane of a selection: 2 up to 512 experts, 4 beyond. One width
 // for every expert count in a range keeps the order of the wavefront sums of
-// the softmax the same in every kernel that selects (the per-token kernels,
-// the select kernel, the single launch), so they publish the same bits.
+// the softmax the same in every kernel that selects (the per-token kernels
+// and the select kernel), so they publish the same bits.
 int selection_per(uint32_t experts) { return experts <= 2u * kSelThreads ? 2 : 4; }
 
 template <int RD>
@@ -1245,6 +1298,18 @@ RouteView route_view(const osmd_moe_args& a) {
   rv.weights = a.weights;
   rv.mass = a.mass;
   rv.slot_ptrs = a.slot_ptrs;
+  rv.bounds = a.logit_bounds;
+  rv.bound_planes = a.bound_planes;
+  rv.stats = a.route_stats;
+  rv.router = a.router;
+  rv.router_dtype = a.router_dtype;
+  rv.router_group = a.router_group;
+  rv.hidden = a.geom.hidden;
+  rv.x = a.x;
+  rv.x_bf16 = a.x_bf16;
+  rv.rms = (a.flags & OSMD_MOE_RMSNORM) ? 1u : 0u;
+  rv.norm_weight = a.norm_weight;
+  rv.rms_eps = a.rms_eps;
   return rv;
 }
 
@@ -1255,60 +1320,6 @@ int launch_select(const osmd_moe_args& a, hipStream_t st) {
     default: select_kernel<4><<<a.tokens, kSelThreads, 0, st>>>(rv); break;
   }
   return launch_status();
-}
-
-// Shape of the single-launch grid.
-struct FusedShape {
-  uint32_t nr, bps, ngu, nd, grid, lpr;
-  size_t lds;
-};
-
-FusedShape fused_shape(const osmd_moe_args& a) {
-  FusedShape f;
-  const uint32_t shared = (a.flags & OSMD_MOE_SHARED) ? 1u : 0u;
-  const uint32_t nslot = a.top_k + shared;
-  const uint32_t D = a.geom.hidden, I = a.geom.inter;
-  f.nr = (a.expert_count + shared + kRouteWaves - 1) / kRouteWaves;
-  const uint32_t gu_rows = kGuWaves * kGuRowsOneToken;
-  f.bps = (I + gu_rows - 1) / gu_rows;
-  f.ngu = nslot * f.bps;
-  f.lpr = static_cast<uint32_t>(pow2_at_least(I / 32u));
-  const uint32_t rows = 2u * (kWave / f.lpr);
-  f.nd = (D + rows - 1) / rows;
-  f.grid = f.nr + 1u + f.ngu + f.nd;
-  const size_t down = down_lds_bytes(I, nslot, rows);
-  f.lds = down > D * sizeof(float) ? down : D * sizeof(float);
-  return f;
-}
-
-bool fused_supported(const osmd_moe_args& a) {
-  const uint32_t nslot = a.top_k + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  const uint32_t D = a.geom.hidden, I = a.geom.inter;
-  const uint32_t lpr = static_cast<uint32_t>(pow2_at_least(I / 32u));
-  return a.tokens == 1u && a.expert_table != nullptr && a.slot_ptrs != nullptr &&
-         (a.router_dtype == OSM_META_BF16 || a.router_dtype == OSM_META_F32) && D % 32u == 0u &&
-         D <= 512u * kFusedRouteLoads && I % 32u == 0u && (lpr == 4u || lpr == 8u || lpr == 16u) &&
-         a.expert_count <= kSelThreads * kFusedPer && nslot <= static_cast<uint32_t>(kFusedMaxSlots) &&
-         fused_shape(a).lds <= 65536u;
-}
-
-template <int RD, int META>
-int launch_fused_meta(const FusedParams& f, const FusedShape& sh, hipStream_t st) {
-  switch (sh.lpr) {
-    case 4: fused_decode_kernel<RD, META, 4><<<sh.grid, 256, sh.lds, st>>>(f); break;
-    case 8: fused_decode_kernel<RD, META, 8><<<sh.grid, 256, sh.lds, st>>>(f); break;
-    default: fused_decode_kernel<RD, META, 16><<<sh.grid, 256, sh.lds, st>>>(f); break;
-  }
-  return launch_status();
-}
-
-template <int RD>
-int launch_fused_rd(const FusedParams& f, const FusedShape& sh, hipStream_t st) {
-  switch (f.a.geom.meta_dtype) {
-    case OSM_META_F32: return launch_fused_meta<RD, OSM_META_F32>(f, sh, st);
-    case OSM_META_F16: return launch_fused_meta<RD, OSM_META_F16>(f, sh, st);
-    default: return launch_fused_meta<RD, OSM_META_BF16>(f, sh, st);
-  }
 }
 
 GateUpParams gate_up_params(const osmd_moe_args& a) {
@@ -1401,41 +1412,6 @@ int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s) {
   return r != 0 ? r : osmd_moe_experts(a, s);
 }
 
-int osmd_moe_fused_supported(const osmd_moe_args* a) { return fused_supported(*a) ? 1 : 0; }
-
-size_t osmd_moe_fused_sync_bytes(const osmd_moe_args* a) {
-  const uint32_t nslot = a->top_k + ((a->flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  return fused_layout(fused_shape(*a).grid, a->expert_count, nslot, a->geom.inter).bytes;
-}
-
-size_t osmd_moe_fused_error_offset(void) { return 0u; }
-
-int osmd_moe_fused_shape(const osmd_moe_args* a, uint32_t* out4) {
-  const FusedShape sh = fused_shape(*a);
-  out4[0] = sh.nr;
-  out4[1] = sh.ngu;
-  out4[2] = sh.nd;
-  out4[3] = sh.grid;
-  return 0;
-}
-
-int osmd_moe_decode_fused(const osmd_moe_args* a, uint32_t* sync, uint64_t* trace, osmd_stream s) {
-  if (!fused_supported(*a) || sync == nullptr) return static_cast<int>(hipErrorInvalidValue);
-  const FusedShape sh = fused_shape(*a);
-  FusedParams f;
-  f.a = *a;
-  f.gp = gate_up_params(*a);
-  f.dp = down_params(*a);
-  f.sync = sync;
-  f.trace = trace;
-  f.nr = sh.nr;
-  f.ngu = sh.ngu;
-  f.gu_blocks_per_slot = sh.bps;
-  f.grid = sh.grid;
-  const hipStream_t st = static_cast<hipStream_t>(s);
-  return a->router_dtype == OSM_META_F32 ? launch_fused_rd<OSM_META_F32>(f, sh, st)
-                                         : launch_fused_rd<OSM_META_BF16>(f, sh, st);
-}
 
 int osmd_expert_forward(const uint8_t* blob, osm_expert_geometry g, const float* x, float* h,
                         float* out, osmd_stream s) {

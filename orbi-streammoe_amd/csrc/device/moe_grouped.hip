@@ -1058,6 +1058,7 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   }
   int r = 0;
   osmd_moe_args ms = m;
+  ms.x_bf16 = a->x_bf16 != 0 ? 1u : 0u;  // the exact path reads the input as given
   if (router_gemm) {
     const uint32_t nrows = m.expert_count + has_shared;
     const uint32_t rcols = router_range(D);

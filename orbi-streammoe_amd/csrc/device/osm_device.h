@@ -145,6 +145,20 @@ typedef struct osmd_moe_args {
    * shared_gate itself; when null, logits and shared_gate are final. */
   const float* logit_planes;
   uint32_t logit_parts;
+  /* Routing exactness. logit_bounds [B, E]: the router writes, for every
+   * logit, a bound on its distance from the reference's sequentially summed
+   * fp32 logit; with logit_planes, bound_planes holds the router GEMM's
+   * per-plane parts of it, [logit_parts][2][B][E + 1]. The selection ranks on
+   * the device logits only where the bounds prove the reference's order, and
+   * otherwise recomputes the candidates' logits in the reference's order from
+   * x (fp32, or bf16 when x_bf16; RMS-normalised first in the sublayer form).
+   * route_stats (null, or 4 counters, added to): selections, selections that
+   * took the exact path, exact paths that ranked every expert, and adjacent
+   * picks whose order rests on exp rounding within 5 ulps. */
+  float* logit_bounds;
+  const float* bound_planes;
+  uint32_t* route_stats;
+  uint32_t x_bf16;
 } osmd_moe_args;
 
 /* Largest top-k and expert count the fused decode kernels accept. */
@@ -153,13 +167,13 @@ typedef struct osmd_moe_args {
 
 /* decode (every expert resident, expert_table set): three kernels --
  *   route:   RMSNorm (optional) + router GEMV + shared-gate dot -> logits
- *   gate_up: top-k selection from the logits (recomputed by one wavefront
- *            of every routed workgroup; one publishes ids/weights/mass/
- *            slot_ptrs), then the gate/up GEMVs with fused SwiGLU -> h
+ *   gate_up: top-k selection from the logits (recomputed by every routed
+ *            workgroup; one publishes ids/weights/mass/slot_ptrs), then the
+ *            gate/up GEMVs with fused SwiGLU -> h
  *   down:    down GEMVs + weighted accumulate (+ residual) -> y
  * Host-driven residency (expert_table null): osmd_moe_route runs route and a
- * one-wavefront select kernel, so the host can read ids and write slot_ptrs
- * before osmd_moe_experts (gate_up then reads slot_ptrs). */
+ * one-workgroup-per-token select kernel, so the host can read ids and write
+ * slot_ptrs before osmd_moe_experts (gate_up then reads slot_ptrs). */
 int osmd_moe_route(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_experts(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s);
@@ -168,24 +182,6 @@ int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_router(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s);
 int osmd_moe_down(const osmd_moe_args* a, osmd_stream s);
-
-/* Single-launch decode of one token with every expert resident: routing,
- * selection, gate/up and down in one grid whose workgroups signal each other
- * through `sync` (osmd_moe_fused_sync_bytes(a) bytes, zeroed once before the
- * first launch and never again; one per layer, launches of one layer in
- * stream order). A wait that exceeded its spin limit sets the sticky u32 at
- * byte osmd_moe_fused_error_offset() of sync. osmd_moe_fused_supported tells
- * whether a (tokens, shape, router dtype, table) can run this way; the
- * results are the bits of osmd_moe_decode. */
-int osmd_moe_fused_supported(const osmd_moe_args* a);
-size_t osmd_moe_fused_sync_bytes(const osmd_moe_args* a);
-size_t osmd_moe_fused_error_offset(void);
-/* trace: null, or [grid][8] u64 per-workgroup timeline (steady-clock stamps
- * at phase boundaries, slot 7 the compute unit's hardware id); the grid is
- * router, gate/up, down blocks, counts from osmd_moe_fused_shape
- * (router, gate/up, down, grid). */
-int osmd_moe_decode_fused(const osmd_moe_args* a, uint32_t* sync, uint64_t* trace, osmd_stream s);
-int osmd_moe_fused_shape(const osmd_moe_args* a, uint32_t* out4);
 
 /* The selection kernel alone: top-k of a->logits for a->tokens tokens into
  * ids / weights / mass (and slot_ptrs from expert_table when set). */

@@ -49,7 +49,8 @@ struct HipMoeLayer::Impl {
   DeviceBytes zero_blob;  // fallback blob when there is no shared expert
   // workspace
   DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs;
-  DeviceBytes fused_sync;  // single-launch handshake words (zeroed once)
+  DeviceBytes logit_bounds;  // [T, E] bound of each logit's distance from the reference's
+  DeviceBytes route_stats;   // 4 routing counters (osmd_moe_args::route_stats)
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
   PinnedBytes host_io;    // cache-driven path: pinned staging of inputs and outputs (grown on use)
   DeviceBytes dev_io;     // its device mirror: one copy in, one copy out per call
@@ -90,7 +91,7 @@ struct HipMoeLayer::Impl {
            g.inter % 128U == 0U && reinterpret_cast<std::uintptr_t>(x) % 16U == 0U;
   }
   bool use_grouped(std::uint32_t tokens, const void* x) const {
-    if (path == HipMoePath::per_token || path == HipMoePath::single_launch) return false;
+    if (path == HipMoePath::per_token) return false;
     if (path == HipMoePath::grouped) return true;
     return tokens >= kGroupedMinTokens && grouped_ok(x);
   }
@@ -137,6 +138,8 @@ struct HipMoeLayer::Impl {
     a.expert_table = table;
     a.fallback_blob = shared_blob.get() ? shared_blob.as<const std::uint8_t>() : zero_blob.as<const std::uint8_t>();
     a.logits = logits.as<float>();
+    a.logit_bounds = logit_bounds.as<float>();
+    a.route_stats = route_stats.as<std::uint32_t>();
     a.ids = ids.as<std::uint32_t>();
     a.weights = weights.as<float>();
     a.shared_gate = shared_gate.as<float>();
@@ -145,11 +148,6 @@ struct HipMoeLayer::Impl {
     a.h = h.as<float>();
     a.slot_ptrs = slot_ptrs.as<const std::uint8_t*>();
     return a;
-  }
-
-  bool use_single_launch(const osmd_moe_args& a) const {
-    if (path != HipMoePath::single_launch) return false;
-    return fused_sync.get() != nullptr && osmd_moe_fused_supported(&a) != 0;
   }
 };
 
@@ -264,6 +262,9 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
     if (rc == 0) rc = impl->x_in.allocate(T * D * sizeof(float));
     if (rc == 0) rc = impl->y_out.allocate(T * D * sizeof(float));
     if (rc == 0) rc = impl->logits.allocate(T * E * sizeof(float));
+    if (rc == 0) rc = impl->logit_bounds.allocate(T * E * sizeof(float));
+    if (rc == 0) rc = impl->route_stats.allocate(4U * sizeof(std::uint32_t));
+    if (rc == 0) rc = osmd_zero(impl->route_stats.get(), 4U * sizeof(std::uint32_t), st);
     if (rc == 0) rc = impl->ids.allocate(T * K * sizeof(std::uint32_t));
     if (rc == 0) rc = impl->weights.allocate(T * K * sizeof(float));
     if (rc == 0) rc = impl->mass.allocate(T * sizeof(float));
@@ -274,17 +275,6 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
     // Slot pointers start null (read as the fallback blob until a selection
     // writes them).
     if (rc == 0) rc = osmd_zero(impl->slot_ptrs.get(), impl->slot_ptrs.size(), st);
-    if (rc == 0) {
-      // The single-launch decode's handshake words, when the shape allows it
-      // (a stand-in table pointer: only its presence is checked).
-      const osmd_moe_args probe =
-          impl->args(nullptr, nullptr, 1U, reinterpret_cast<const std::uint8_t* const*>(impl->slot_ptrs.get()), false);
-      if (osmd_moe_fused_supported(&probe) != 0) {
-        const std::size_t bytes = osmd_moe_fused_sync_bytes(&probe);
-        rc = impl->fused_sync.allocate(bytes);
-        if (rc == 0) rc = osmd_zero(impl->fused_sync.get(), bytes, st);
-      }
-    }
     if (rc == 0) rc = osmd_zero(impl->shared_gate.get(), T * sizeof(float), st);
     if (rc == 0) rc = impl->host_ptrs.allocate(T * nslot * sizeof(void*));
     if (rc == 0) rc = osmd_stream_synchronize(st);
@@ -353,8 +343,6 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
       const osmd_moe_grouped_args ga = impl_->grouped_args(a, false);
       rc = osmd_moe_grouped(&ga, context.stream());
     }
-  } else if (impl_->use_single_launch(a)) {
-    rc = osmd_moe_decode_fused(&a, impl_->fused_sync.as<std::uint32_t>(), nullptr, context.stream());
   } else {
     rc = osmd_moe_decode(&a, context.stream());
   }
@@ -370,13 +358,13 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
 namespace {
 
 // The routing workspace of `tokens` rows, carved from the fixed array in
-// 256-byte aligned parts: logits, ids, weights, mass, shared gate,
-// normalised input, h, slot pointers.
+// 256-byte aligned parts: logits, their bounds, ids, weights, mass, shared
+// gate, normalised input, h, slot pointers.
 std::size_t static_workspace_bytes(const HipMoeLayerConfig& c, std::size_t tokens) {
   auto al = [](std::size_t n) { return (n + 255U) & ~static_cast<std::size_t>(255U); };
   const std::size_t nslot = c.top_k + (c.has_shared_expert ? 1U : 0U);
   const std::size_t T = tokens;
-  return al(T * c.expert_count * 4U) + 2U * al(T * c.top_k * 4U) + 2U * al(T * 4U) +
+  return 2U * al(T * c.expert_count * 4U) + 2U * al(T * c.top_k * 4U) + 2U * al(T * 4U) +
          al(T * c.geometry.hidden * 4U) + al(T * nslot * c.geometry.inter * 4U) + al(T * nslot * sizeof(void*));
 }
 
@@ -419,6 +407,8 @@ int HipMoeLayer::decode_device_static(HipComputeContext& context, const float* x
   auto* p = static_cast<std::uint8_t*>(base);
   a.logits = reinterpret_cast<float*>(p);
   p += al(T * c.expert_count * 4U);
+  a.logit_bounds = reinterpret_cast<float*>(p);
+  p += al(T * c.expert_count * 4U);
   a.ids = reinterpret_cast<std::uint32_t*>(p);
   p += al(T * c.top_k * 4U);
   a.weights = reinterpret_cast<float*>(p);
@@ -433,8 +423,9 @@ int HipMoeLayer::decode_device_static(HipComputeContext& context, const float* x
   p += al(T * nslot * c.geometry.inter * 4U);
   a.slot_ptrs = reinterpret_cast<const std::uint8_t**>(p);
   // Nothing here is read before this call writes it: the router writes the
-  // logits, shared gate and normalised input, the selection the picks and
-  // slot pointers, gate/up every slot's h.
+  // logits, their bounds, the shared gate and the normalised input, the
+  // selection the picks and slot pointers, gate/up every slot's h. The
+  // routing counters are the layer's own.
   if (osmd_moe_decode(&a, context.stream()) != 0) return say("MoE decode launch failed"), OSM_E_DEVICE;
   say("");
   return OSM_OK;
@@ -442,56 +433,13 @@ int HipMoeLayer::decode_device_static(HipComputeContext& context, const float* x
 
 bool HipMoeLayer::set_path(HipMoePath path, std::string* diagnostic) noexcept {
   if (!impl_) return set_diag(diagnostic, "MoE layer is not valid"), false;
-  if (path == HipMoePath::single_launch && impl_->fused_sync.get() == nullptr)
-    return set_diag(diagnostic,
-                    "single-launch decode needs hidden <= 2048, intermediate in (64, 512], <= 512 experts, "
-                    "top_k + shared <= 12 and an f32 or bf16 router"),
-           false;
+  if (path != HipMoePath::automatic && path != HipMoePath::per_token && path != HipMoePath::grouped)
+    return set_diag(diagnostic, "unknown MoE path"), false;
   impl_->path = path;
   return true;
 }
 
 HipMoePath HipMoeLayer::path() const noexcept { return impl_ ? impl_->path : HipMoePath::automatic; }
-
-HipDispatchResult HipMoeLayer::trace_single_launch(HipComputeContext& context, const float* x, float* y,
-                                                  const std::uint8_t* const* expert_table, std::uint64_t* trace,
-                                                  std::uint32_t* shape) noexcept {
-  HipDispatchResult r;
-  if (!valid() || !context.activate(&r.diagnostic)) {
-    if (r.diagnostic.empty()) r.diagnostic = "MoE layer is not valid";
-    return r;
-  }
-  if (x == nullptr || y == nullptr || expert_table == nullptr || trace == nullptr || shape == nullptr) {
-    r.diagnostic = "single-launch trace: invalid arguments";
-    return r;
-  }
-  const osmd_moe_args a = impl_->args(x, y, 1U, expert_table, false);
-  if (impl_->fused_sync.get() == nullptr || osmd_moe_fused_supported(&a) == 0) {
-    r.diagnostic = "single-launch decode is not available for this layer";
-    return r;
-  }
-  osmd_moe_fused_shape(&a, shape);
-  const int rc = osmd_moe_decode_fused(&a, impl_->fused_sync.as<std::uint32_t>(), trace, context.stream());
-  if (rc != 0) {
-    r.diagnostic = hip_error("single-launch trace launch failed", rc);
-    return r;
-  }
-  r.executed = true;
-  return r;
-}
-
-bool HipMoeLayer::single_launch_failures(HipComputeContext& context, std::uint32_t* out,
-                                         std::string* diagnostic) const noexcept {
-  if (!valid() || out == nullptr) return set_diag(diagnostic, "invalid layer or output"), false;
-  *out = 0;
-  if (impl_->fused_sync.get() == nullptr) return true;
-  if (!context.activate(diagnostic)) return false;
-  const osmd_stream st = context.stream();
-  int rc = osmd_memcpy_d2h(out, impl_->fused_sync.as<std::uint8_t>() + osmd_moe_fused_error_offset(), 4, st);
-  if (rc == 0) rc = osmd_stream_synchronize(st);
-  if (rc != 0) return set_diag(diagnostic, hip_error("single-launch status download failed", rc)), false;
-  return true;
-}
 
 HipDispatchResult HipMoeLayer::prefill_device_bf16(HipComputeContext& context, const std::uint16_t* x_bf16,
                                                    float* y, std::uint32_t tokens,
@@ -585,6 +533,18 @@ bool HipMoeLayer::download_routing(HipComputeContext& context, std::uint32_t tok
   } catch (const std::exception& e) {
     return set_diag(diagnostic, std::string("routing download exception: ") + e.what()), false;
   }
+}
+
+bool HipMoeLayer::routing_stats(HipComputeContext& context, std::uint32_t (&out)[4], bool reset,
+                                std::string* diagnostic) noexcept {
+  if (!valid()) return set_diag(diagnostic, "MoE layer is not valid"), false;
+  if (!context.activate(diagnostic)) return false;
+  const osmd_stream st = context.stream();
+  int rc = osmd_memcpy_d2h(out, impl_->route_stats.get(), sizeof(out), st);
+  if (rc == 0 && reset) rc = osmd_zero(impl_->route_stats.get(), sizeof(out), st);
+  if (rc == 0) rc = osmd_stream_synchronize(st);
+  if (rc != 0) return set_diag(diagnostic, hip_error("routing counters download failed", rc)), false;
+  return true;
 }
 
 bool HipMoeLayer::download_normalized(HipComputeContext& context, std::uint32_t tokens, std::vector<float>& out,

@@ -673,18 +673,14 @@ struct HipMoeResult {
 // vector [D] (bf16 or f32), optional RMSNorm weight, the shared expert, and
 // scratch for up to max_tokens tokens.
 // How a decode runs: the per-token kernels (router, gate/up, down; every
-// token reads its picks' weights), grouped GEMMs (tokens bucketed by expert,
-// each expert's weights read once for all its tokens), or, for one token,
-// the single-launch kernel (the per-token kernels' work in one grid whose
-// workgroups hand data to each other; same bits, measured slower than the
-// three kernels at the Qwen3-Next shape, so only taken when asked for).
-// automatic takes the per-token kernels, and the grouped path from
+// token reads its picks' weights) or grouped GEMMs (tokens bucketed by
+// expert, each expert's weights read once for all its tokens). automatic takes the per-token kernels, and the grouped path from
 // kGroupedMinTokens tokens on, between the batch sizes where it was
 // measured to overtake the per-token kernels at the Qwen3-Next shape on
 // MI355X (us per layer, per-token vs grouped: 32 tokens 148-177 vs 176-182;
 // 40: 201-207 vs 198; 48: 213-218 vs 211; 64: 266-272 vs 239; 512: 2730 vs
-// 387). single_launch with more than one token runs the per-token kernels.
-enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2, single_launch = 3 };
+// 387).
+enum class HipMoePath { automatic = 0, per_token = 1, grouped = 2 };
 inline constexpr std::uint32_t kGroupedMinTokens = 40;
 
 class HipMoeLayer {
@@ -729,20 +725,9 @@ class HipMoeLayer {
                                          std::uint32_t tokens, const std::uint8_t* const* expert_table,
                                          bool sublayer, const char** diagnostic) noexcept;
   [[nodiscard]] std::uint32_t static_tokens_capacity() const noexcept;
-  // False (path unchanged) for single_launch on a layer whose shape cannot
-  // run as one launch.
+  // False (path unchanged) for a value that names no path.
   bool set_path(HipMoePath path, std::string* diagnostic = nullptr) noexcept;
   [[nodiscard]] HipMoePath path() const noexcept;
-  // Waits of the single-launch kernel that ran out of spins since the layer
-  // was created (0 when every launch completed its handshakes).
-  [[nodiscard]] bool single_launch_failures(HipComputeContext& context, std::uint32_t* out,
-                                            std::string* diagnostic = nullptr) const noexcept;
-  // One single-launch decode (MoE form) that also records each workgroup's
-  // timeline into trace (device, [grid][8] u64); shape gets the router,
-  // gate/up and down workgroup counts and the grid size.
-  [[nodiscard]] HipDispatchResult trace_single_launch(HipComputeContext& context, const float* x, float* y,
-                                                      const std::uint8_t* const* expert_table,
-                                                      std::uint64_t* trace, std::uint32_t* shape) noexcept;
   // A prefill chunk in bf16 ([tokens, D], device) through the grouped path:
   // bf16 router, MoE form (no RMSNorm / residual), y fp32 [tokens, D].
   [[nodiscard]] HipDispatchResult prefill_device_bf16(HipComputeContext& context,
@@ -766,6 +751,12 @@ class HipMoeLayer {
   [[nodiscard]] bool download_routing(HipComputeContext& context, std::uint32_t tokens,
                                       HipMoeRouting& out,
                                       std::string* diagnostic = nullptr) const noexcept;
+  // The routing counters of every selection since creation or the last
+  // reset: selections, selections that took the exact path, exact paths that
+  // recomputed every expert, and unresolved adjacent picks. Synchronises the
+  // context's stream; reset zeroes them afterwards.
+  [[nodiscard]] bool routing_stats(HipComputeContext& context, std::uint32_t (&out)[4], bool reset,
+                                   std::string* diagnostic = nullptr) noexcept;
   // The RMSNorm output (sublayer form) or the input (MoE form) of the last
   // per-token decode, or the normalised input of the last grouped sublayer.
   [[nodiscard]] bool download_normalized(HipComputeContext& context, std::uint32_t tokens,

@@ -22,7 +22,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libosm_hip.so")
 
 OSM_OK, OSM_E_INVALID, OSM_E_RUNTIME, OSM_E_DEVICE = 0, 1, 2, 3
-PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED, PATH_SINGLE_LAUNCH = 0, 1, 2, 3
+PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED = 0, 1, 2
 F32, F16, BF16 = 0, 1, 2
 AFFINE_Q8 = 3  # router / shared-gate dtype: MLX affine 8-bit (osm_affine_q8_c)
 
@@ -135,10 +135,9 @@ _PROTOTYPES = {
     "osm_moe_decode_layers": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int]),
     "osm_moe_layer_launch_phase": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32, c_int, c_int]),
     "osm_moe_layer_set_path": (c_int, [_H, c_int]),
-    "osm_moe_layer_wait_failures": (c_int, [_H, _H, POINTER(c_uint32)]),
-    "osm_moe_layer_trace_single_launch": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_void_p, POINTER(c_uint32)]),
     "osm_moe_layer_prefill_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32]),
     "osm_moe_layer_routing": (c_int, [_H, _H, c_uint32, POINTER(MoeOutputs)]),
+    "osm_moe_layer_routing_stats": (c_int, [_H, _H, POINTER(c_uint32), c_int]),
     "osm_decode_graph_create": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int, POINTER(_H)]),
     "osm_graph_capture_begin": (c_int, [_H]),
     "osm_graph_capture_end": (c_int, [_H, POINTER(_H)]),
@@ -623,22 +622,8 @@ class MoeLayer(_Handle):
         return int(load().osm_moe_layer_static_tokens_capacity(self.h))
 
     def set_path(self, path):
-        """PATH_AUTO, PATH_PER_TOKEN, PATH_GROUPED or PATH_SINGLE_LAUNCH."""
+        """PATH_AUTO, PATH_PER_TOKEN or PATH_GROUPED."""
         check(load().osm_moe_layer_set_path(self.h, path))
-
-    def trace_single_launch(self, slab, slab_layer, x_ptr, y_ptr, trace_ptr):
-        """One traced single-launch decode; returns (router, gate/up, down, grid)
-        workgroup counts. trace_ptr: device [grid][8] u64."""
-        shape = (c_uint32 * 4)()
-        check(load().osm_moe_layer_trace_single_launch(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr,
-                                                       trace_ptr, shape))
-        return tuple(shape)
-
-    def wait_failures(self) -> int:
-        """Single-launch waits that ran out of spins since creation (0 = none)."""
-        v = c_uint32(0)
-        check(load().osm_moe_layer_wait_failures(self.ctx.h, self.h, ctypes.byref(v)))
-        return v.value
 
     def prefill_device(self, slab, slab_layer, x_bf16_ptr, y_ptr, tokens):
         check(load().osm_moe_layer_prefill_device(self.ctx.h, self.h, slab.h, slab_layer, x_bf16_ptr, y_ptr, tokens))
@@ -652,6 +637,13 @@ class MoeLayer(_Handle):
         o.out = None
         check(load().osm_moe_layer_routing(self.ctx.h, self.h, tokens, ctypes.byref(o)))
         return res
+
+    def routing_stats(self, reset=False) -> dict:
+        """Selections, those that took the exact path, exact paths over every
+        expert, and unresolved adjacent picks, since creation or a reset."""
+        v = (c_uint32 * 4)()
+        check(load().osm_moe_layer_routing_stats(self.ctx.h, self.h, v, 1 if reset else 0))
+        return dict(zip(("selections", "exact", "exact_all", "unresolved"), list(v)))
 
     def launch_phase(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer, phase):
         check(load().osm_moe_layer_launch_phase(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0, phase))
