@@ -107,14 +107,15 @@ __global__ void widen_bf16_kernel(const uint16_t* __restrict__ x, size_t n, floa
 // by butterfly.
 template <bool XBF16, int NS>
 __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t K, uint32_t G,
-                               uint16_t* __restrict__ terms, float* __restrict__ sums) {
+                               uint16_t* __restrict__ terms, float* __restrict__ sums,
+                               float* __restrict__ norms) {
   static_assert(NS >= kActSplit, "the expert GEMMs read the first two terms");
   const uint32_t words = K / 8u, wpg = G / 8u;
   const size_t n = static_cast<size_t>(R) * words;  // a multiple of wpg, so groups never straddle waves
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
   for (size_t i0 = static_cast<size_t>(blockIdx.x) * blockDim.x; i0 < n; i0 += stride) {
     const size_t i = i0 + threadIdx.x;
-    float total = 0.0f;
+    float total = 0.0f, sq = 0.0f;
     if (i < n) {
       const uint32_t r = static_cast<uint32_t>(i / words), wd = static_cast<uint32_t>(i % words);
       float v[8];
@@ -132,6 +133,8 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
       }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sq += v[k] * v[k];
       float rep[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -157,6 +160,15 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
     // Sum of the group's G/8 words, then written by its first lane.
     for (uint32_t m = 1; m < wpg; m <<= 1) total += __shfl_xor(total, static_cast<int>(m), kWave);
     if (i < n && (i % wpg) == 0u) sums[i / wpg] = total;
+    if (norms != nullptr) {
+      // Euclidean norm of each 32-column chunk (4 words), rounded up: the
+      // router GEMM's error bounds take |w . x| <= |w| |x| per chunk. The
+      // fp32 sum of 32 squares is within 32 u of the true one, so 1 + 2^-20
+      // covers it and the square root's rounding.
+      sq += __shfl_xor(sq, 1, kWave);
+      sq += __shfl_xor(sq, 2, kWave);
+      if (i < n && (i % 4u) == 0u) norms[i / 4u] = sqrtf(sq) * (1.0f + 0x1p-20f);
+    }
   }
 }
 
@@ -171,10 +183,28 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
 // (48 KB of terms, 64 KB of router rows at R = 512) and the grid large; a
 // wave that read its own copy of the terms, over all of K, moved 4x more
 // bytes through L2 than the tile holds.
+//
+// Every logit plane also gets the parts of its bound on the distance from
+// the reference's sequentially summed logit (bplanes, when set;
+// reference_ops.cpp:85-93). Per 32-column step the MFMAs start from zero
+// (smallest term first) and the step sums are added in fp32, so with u =
+// 2^-24 and a the step's sum |w| |x| (at most |w_chunk| |x_chunk|, the
+// norms of the router rows and inputs, rnorm and xnorm):
+//  - the MFMAs form each bf16 product exactly and add 33 operands per
+//    instruction; in any order, with each addition faithful (or with all
+//    operands aligned to the largest and truncated), that errs by at most
+//    66 u of the operands' absolute sum, about 70 u a per step;
+//  - adding the step sums errs by at most u |running sum| per step;
+//  - the reference's 32 partial sums within the step are at most
+//    32 (|running sum before it| + a).
+// Plane 2p + 0 gets the sum over steps of 32 (|before| + a) + |after|,
+// plane 2p + 1 the sum of a; the selection adds R |start of the range| for
+// each range and scales the total.
 template <int NS, int NSTEP>
 __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
     const uint16_t* __restrict__ terms, uint32_t T, uint32_t D, const uint16_t* __restrict__ router,
-    const uint16_t* __restrict__ shared_gate_vec, uint32_t E, float* __restrict__ planes) {
+    const uint16_t* __restrict__ shared_gate_vec, uint32_t E, float* __restrict__ planes,
+    const float* __restrict__ rnorm, const float* __restrict__ xnorm, float* __restrict__ bplanes) {
   constexpr uint32_t R = 32u * NSTEP;
   constexpr uint32_t RS = R + 8u;  // LDS row stride (bf16), padded against bank conflicts
   constexpr uint32_t kUnitCols = R / 8u;
@@ -195,6 +225,19 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
   uint4 raw[NSTEP];
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) raw[st] = ldg16(wrow + 32u * st + 8u * q);
+  const bool bounds = bplanes != nullptr;
+  __shared__ float xn_lds[kTileTokens][NSTEP];
+  float wn[NSTEP];
+  if (bounds) {
+    const float* rn = rnorm + static_cast<size_t>(rr) * (D / 32u) + k0 / 32u;
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) wn[st] = rn[st];
+    if (tid < kTileTokens * NSTEP) {
+      const uint32_t r = tid / NSTEP, st = tid % NSTEP;
+      const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
+      xn_lds[r][st] = xnorm[static_cast<size_t>(tok) * (D / 32u) + k0 / 32u + st];
+    }
+  }
   uint4 stage[kUnitsPerThread];
 #pragma unroll
   for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
@@ -212,8 +255,10 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
   __syncthreads();
 
   // 2. MFMAs: A = token m's terms at k0 + 32 st + 8q (word order), B = 8
-  // router values of row rr reordered to word order.
+  // router values of row rr reordered to word order. Each step starts from
+  // zero, smallest term first; its sum joins the running sums in fp32.
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float rp[4] = {0.f, 0.f, 0.f, 0.f}, ap[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) {
     const uint32_t h4[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
@@ -229,9 +274,20 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
     bv.z = h[word_k(4)] | (static_cast<uint32_t>(h[word_k(5)]) << 16);
     bv.w = h[word_k(6)] | (static_cast<uint32_t>(h[word_k(7)]) << 16);
     const bf16x8 b = as_operand(bv);
+    f32x4 part = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < NS; ++t)
-      acc = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * st + 8u * q])), b, acc);
+    for (int t = NS - 1; t >= 0; --t)
+      part = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * st + 8u * q])), b, part);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float before = acc[j];
+      acc[j] = before + part[j];
+      if (bounds) {
+        const float a = wn[st] * xn_lds[4u * q + j][st];
+        rp[j] += 32.0f * (fabsf(before) + a) + fabsf(acc[j]);
+        ap[j] += a;
+      }
+    }
   }
 
   // 3. Plane blockIdx.z, [T][E + 1] (column E: the shared gate, when there is
@@ -239,7 +295,14 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t t = t0 + 4u * q + j;
-    if (t < T && row < nrows) planes[(static_cast<size_t>(blockIdx.z) * T + t) * (E + 1u) + row] = acc[j];
+    if (t < T && row < nrows) {
+      planes[(static_cast<size_t>(blockIdx.z) * T + t) * (E + 1u) + row] = acc[j];
+      if (bounds) {
+        const size_t ps = static_cast<size_t>(T) * (E + 1u);
+        bplanes[2u * blockIdx.z * ps + static_cast<size_t>(t) * (E + 1u) + row] = rp[j];
+        bplanes[(2u * blockIdx.z + 1u) * ps + static_cast<size_t>(t) * (E + 1u) + row] = ap[j];
+      }
+    }
   }
 }
 
@@ -794,7 +857,7 @@ __global__ void swiglu_terms_kernel(const float* __restrict__ part, uint32_t nsp
   const size_t plane = static_cast<size_t>(P) * I;
   for (size_t i0 = static_cast<size_t>(blockIdx.x) * blockDim.x; i0 < n; i0 += stride) {
     const size_t i = i0 + threadIdx.x;
-    float total = 0.0f;
+    float total = 0.0f, sq = 0.0f;
     if (i < n) {
       const size_t pair = i / words, wd = i % words;
       const float* gp = part + pair * I + wd * 8u;
@@ -1044,17 +1107,26 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     xbf16 = false;
   }
   const uint32_t x_term_count = router_gemm ? kRouterSplit : kActSplit;
+  // Error bounds of the GEMM's logits need the router's and the input's
+  // 32-column norms.
+  const bool gemm_bounds = router_gemm && a->router_norms != nullptr && a->x_norms != nullptr &&
+                           a->bound_planes != nullptr;
+  float* xnorms = gemm_bounds ? a->x_norms : nullptr;
   const size_t words = static_cast<size_t>(T) * (D / 8u);
   if (router_gemm) {
     if (xbf16)
-      prepare_kernel<true, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+      prepare_kernel<true, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums,
+                                                                                xnorms);
     else
-      prepare_kernel<false, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+      prepare_kernel<false, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums,
+                                                                                xnorms);
   } else {
     if (xbf16)
-      prepare_kernel<true, kActSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+      prepare_kernel<true, kActSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums,
+                                                                                xnorms);
     else
-      prepare_kernel<false, kActSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums);
+      prepare_kernel<false, kActSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums,
+                                                                                xnorms);
   }
   int r = 0;
   osmd_moe_args ms = m;
@@ -1069,19 +1141,23 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     switch (rcols) {
       case 512:
         router_gemm_kernel<kRouterSplit, 16><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
-                                                                              m.expert_count, a->logit_planes);
+                                                                              m.expert_count, a->logit_planes, a->router_norms, xnorms,
+                                               gemm_bounds ? a->bound_planes : nullptr);
         break;
       case 256:
         router_gemm_kernel<kRouterSplit, 8><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
-                                                                             m.expert_count, a->logit_planes);
+                                                                             m.expert_count, a->logit_planes, a->router_norms, xnorms,
+                                               gemm_bounds ? a->bound_planes : nullptr);
         break;
       default:
         router_gemm_kernel<kRouterSplit, 4><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
-                                                                             m.expert_count, a->logit_planes);
+                                                                             m.expert_count, a->logit_planes, a->router_norms, xnorms,
+                                               gemm_bounds ? a->bound_planes : nullptr);
         break;
     }
     ms.logit_planes = a->logit_planes;
     ms.logit_parts = D / rcols;
+    ms.bound_planes = gemm_bounds ? a->bound_planes : nullptr;
   } else {
     // The decode router kernel, one token per grid row (fp32 input).
     osmd_moe_args ra = m;

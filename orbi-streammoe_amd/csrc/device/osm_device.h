@@ -218,6 +218,13 @@ typedef struct osmd_moe_grouped_args {
   float* h_sums;
   float* partial;
   float* logit_planes;
+  /* Error bounds of the router GEMM's logits (any null: no bounds, every
+   * selection takes the exact path): the router's 32-column norms
+   * [E + 1][D/32] (row E the shared-gate vector), the input's [T][D/32],
+   * and the bound planes [router_parts][2][T][E + 1]. */
+  const float* router_norms;
+  float* x_norms;
+  float* bound_planes;
 } osmd_moe_grouped_args;
 size_t osmd_moe_grouped_max_tiles(uint32_t tokens, uint32_t nslot, uint32_t experts);
 uint32_t osmd_moe_grouped_splits(const osm_expert_geometry* g, uint32_t cols);

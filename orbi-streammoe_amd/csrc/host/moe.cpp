@@ -3,6 +3,7 @@
 // routed_moe.cpp:254-430).
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <string>
 #include <unordered_set>
 #include <utility>
@@ -50,6 +51,7 @@ struct HipMoeLayer::Impl {
   // workspace
   DeviceBytes x_in, y_out, logits, ids, weights, mass, shared_gate, x_norm, h, slot_ptrs;
   DeviceBytes logit_bounds;  // [T, E] bound of each logit's distance from the reference's
+  DeviceBytes router_norms;  // bf16 router: [E + 1][D/32] norms of its 32-column chunks (row E: shared gate)
   DeviceBytes route_stats;   // 4 routing counters (osmd_moe_args::route_stats)
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
   PinnedBytes host_io;    // cache-driven path: pinned staging of inputs and outputs (grown on use)
@@ -58,7 +60,7 @@ struct HipMoeLayer::Impl {
   HipMoePath path = HipMoePath::automatic;
   bool grouped_ready = false;
   DeviceBytes g_x_terms, g_x_sums, g_pair_pos, g_pair_w, g_tiles, g_tile_count, g_gu_part, g_h_terms,
-      g_h_sums, g_partial, g_logit_planes;
+      g_h_sums, g_partial, g_logit_planes, g_x_norms, g_bound_planes;
 
   int ensure_grouped(osmd_stream st) {
     if (grouped_ready) return 0;
@@ -76,9 +78,10 @@ struct HipMoeLayer::Impl {
     if (rc == 0) rc = g_h_terms.allocate(P * 2U * I * 2U);
     if (rc == 0) rc = g_h_sums.allocate(P * (I / G) * 4U);
     if (rc == 0) rc = g_partial.allocate(osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(I)) * P * D * 4U);
-    if (rc == 0)
-      rc = g_logit_planes.allocate(osmd_moe_grouped_router_parts(static_cast<std::uint32_t>(D)) * T *
-                                   (cfg.expert_count + 1U) * 4U);
+    const std::size_t parts = osmd_moe_grouped_router_parts(static_cast<std::uint32_t>(D));
+    if (rc == 0) rc = g_logit_planes.allocate(parts * T * (cfg.expert_count + 1U) * 4U);
+    if (rc == 0) rc = g_x_norms.allocate(T * (D / 32U) * 4U);
+    if (rc == 0) rc = g_bound_planes.allocate(parts * 2U * T * (cfg.expert_count + 1U) * 4U);
     if (rc == 0) rc = osmd_zero(g_tile_count.get(), 4U, st);
     if (rc == 0) grouped_ready = true;
     return rc;
@@ -111,6 +114,9 @@ struct HipMoeLayer::Impl {
     ga.h_sums = g_h_sums.as<float>();
     ga.partial = g_partial.as<float>();
     ga.logit_planes = g_logit_planes.as<float>();
+    ga.router_norms = router_norms.as<const float>();
+    ga.x_norms = g_x_norms.as<float>();
+    ga.bound_planes = g_bound_planes.as<float>();
     return ga;
   }
 
@@ -254,6 +260,30 @@ std::optional<HipMoeLayer> HipMoeLayer::create(HipComputeContext& context, const
     if (rc == 0 && config.has_shared_expert)
       rc = q8 ? up_q8(impl->shared_gate_vec, *sq, 1U) : up(impl->shared_gate_vec, shared_gate_vec, D * esz);
     if (rc == 0 && !norm_weight.empty()) rc = up(impl->norm_weight, norm_weight.data(), norm_weight.size_bytes());
+    if (rc == 0 && router_dtype == OSM_META_BF16) {
+      // Norms of the bf16 router's 32-column chunks (and of the shared-gate
+      // vector as row E), each rounded up, for the router GEMM's error bounds.
+      const std::size_t chunks = D / 32U;
+      std::vector<float> nrm((E + 1U) * chunks, 0.0F);
+      auto widen = [](std::uint16_t b) {
+        const std::uint32_t u = static_cast<std::uint32_t>(b) << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        return static_cast<double>(f);
+      };
+      for (std::size_t r = 0; r <= E; ++r) {
+        const std::uint16_t* w = r < E ? static_cast<const std::uint16_t*>(router) + r * D
+                                       : static_cast<const std::uint16_t*>(shared_gate_vec);
+        if (w == nullptr) continue;
+        for (std::size_t c = 0; c < chunks; ++c) {
+          double ss = 0.0;
+          for (std::size_t j = 0; j < 32U; ++j) ss += widen(w[c * 32U + j]) * widen(w[c * 32U + j]);
+          nrm[r * chunks + c] = std::nextafter(static_cast<float>(std::sqrt(ss) * (1.0 + 1e-12)),
+                                               std::numeric_limits<float>::infinity());
+        }
+      }
+      rc = up(impl->router_norms, nrm.data(), nrm.size() * sizeof(float));
+    }
     if (rc == 0 && config.has_shared_expert) rc = up(impl->shared_blob, shared_blob.data(), shared_blob.size());
     if (rc == 0 && !config.has_shared_expert) {
       rc = impl->zero_blob.allocate(expert_blob_bytes(g));

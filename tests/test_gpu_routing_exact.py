@@ -152,3 +152,26 @@ def test_ties_within_exp_rounding_are_counted(ctx):
     assert np.array_equal(gpu["ids"][0], ora["ids"]), (list(gpu["ids"][0]), list(ora["ids"]))
     st = moe.routing_stats()
     assert st["exact"] == 1 and st["unresolved"] >= 1, st
+
+
+def test_router_gemm_bounds_prove_most_tokens(ctx):
+    # The grouped path's router GEMM bounds its logits too (per-step MFMA
+    # sums, 32-column norms): most tokens of a 128-token bf16 chunk are
+    # proven without the exact path, and every token's ids are the oracle's.
+    from test_gpu_moe import QwenLayer
+    T = 128
+    L = QwenLayer(ctx, 92, max_tokens=T)
+    xf = O.synth_tokens(92, 7000, T, L.D)
+    bits = ((xf.view(np.uint32) + 0x7FFF + ((xf.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    xw = (bits.astype(np.uint32) << 16).view(np.float32)
+    xb, y = ctx.alloc(T * L.D * 2), ctx.alloc(T * L.D * 4)
+    xb.upload(bits)
+    L.moe.routing_stats(reset=True)
+    L.moe.prefill_device(L.slab, 0, xb.ptr, y.ptr, T)
+    routing = L.moe.routing(T)
+    st = L.moe.routing_stats()
+    assert st["selections"] == T and st["exact"] <= T // 3, st
+    router = O.bf16_bits_to_f32(L.router_bits)
+    for t in range(T):
+        ora = O.route_qwen_top_k(xw[t], router, L.D, L.E, L.k, True)
+        assert np.array_equal(routing["ids"][t], ora["ids"]), t
