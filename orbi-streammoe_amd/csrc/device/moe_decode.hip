@@ -233,7 +233,7 @@ constexpr float kUnderflowGap = 80.0f;
 // order. The next chunk's loads are issued before the additions start.
 constexpr uint32_t kExactCols = 256;
 constexpr uint32_t kExactRows = 16;  // candidates per pass
-constexpr uint32_t kExactStride = kExactCols + 1u;  // LDS row stride: the adders' rows in distinct banks
+constexpr uint32_t kExactStride = kExactCols + 4u;  // LDS row stride: 16-byte aligned rows, adders' reads in distinct banks
 
 __device__ __forceinline__ float tie_margin(float mx, float l) { return 0x1p-20f + 0x1p-23f * (mx - l + 1.0f); }
 
@@ -257,8 +257,7 @@ struct Selection {
   uint32_t nunresolved, ncand, wcount[kSelWaves];
   uint16_t cl[kSelThreads * PER];             // exact path: candidate list
   float xe[kExactCols];                       // exact path: the input of one chunk of columns
-  float prod[kExactRows][kExactStride];       // exact path: rounded products of one chunk
-  float pad[32];                              // chain_sum reads up to 24 past a row
+  __attribute__((aligned(16))) float prod[kExactRows][kExactStride];  // exact path: rounded products of one chunk
 };
 static_assert(kExactCols == kSelThreads && kExactRows * 16u == kSelThreads, "exact-path chunk mapping");
 
@@ -284,42 +283,29 @@ __device__ __forceinline__ void sort_lane(uint32_t* k, uint32_t* n) {
   }
 }
 
-// acc + v[0] + v[1] + ... + v[n-1] (SQUARE: + v[i] * v[i]) in order, each
-// operation rounded to fp32, v in LDS, n a multiple of 8. Three register
-// blocks of 8 rotate: the reads of a block are issued two blocks before its
-// additions (sched_barrier keeps the compiler from moving them later), so
-// the chain of additions, which cannot be shortened, is what is waited on.
-// The reads run up to 24 elements past n (the LDS arrays are padded for
-// it); those values are never added.
-template <bool SQUARE>
-__device__ __forceinline__ void chain_read8(const float* v, float (&r)[8]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = v[j];
-  __builtin_amdgcn_sched_barrier(0);
-}
-template <bool SQUARE>
-__device__ __forceinline__ float chain_add8(const float (&r)[8], float acc) {
+// acc + v[0] + v[1] + ... + v[n-1] in order, each addition rounded to fp32,
+// v in LDS (16-byte aligned), n a multiple of 8. Runs of 256 are
+// straight-line code of 16-byte reads, which the compiler issues well ahead
+// of the additions, so the chain of additions, which cannot be shortened, is
+// what is waited on; the rest goes 8 at a time.
+__device__ __forceinline__ float chain_add4(float4 q, float acc) {
 #pragma clang fp contract(off)
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc = SQUARE ? acc + r[j] * r[j] : acc + r[j];
-  __builtin_amdgcn_sched_barrier(0);
+  acc = acc + q.x;
+  acc = acc + q.y;
+  acc = acc + q.z;
+  acc = acc + q.w;
   return acc;
 }
-template <bool SQUARE>
 __device__ __forceinline__ float chain_sum(const float* v, uint32_t n, float acc) {
-  float a[8], b[8], c[8];
-  chain_read8<SQUARE>(v, a);
-  chain_read8<SQUARE>(v + 8, b);
-  for (uint32_t i = 0;; i += 24) {
-    chain_read8<SQUARE>(v + i + 16, c);
-    acc = chain_add8<SQUARE>(a, acc);
-    if (i + 8 >= n) break;
-    chain_read8<SQUARE>(v + i + 24, a);
-    acc = chain_add8<SQUARE>(b, acc);
-    if (i + 16 >= n) break;
-    chain_read8<SQUARE>(v + i + 32, b);
-    acc = chain_add8<SQUARE>(c, acc);
-    if (i + 24 >= n) break;
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  uint32_t i = 0;
+  for (; i + 256u <= n; i += 256u) {
+#pragma unroll
+    for (uint32_t j = 0; j < 64u; ++j) acc = chain_add4(v4[i / 4u + j], acc);
+  }
+  for (; i < n; i += 8u) {
+    acc = chain_add4(v4[i / 4u], acc);
+    acc = chain_add4(v4[i / 4u + 1u], acc);
   }
   return acc;
 }
@@ -343,9 +329,14 @@ __device__ float exact_rms_scale(const RouteView& rv, uint32_t t, Selection<PER>
   float* stage = &out.prod[0][0];
   float ss = 0.0f;
   for (uint32_t c0 = 0; c0 < rv.hidden; c0 += kCols) {
-    for (uint32_t i = threadIdx.x; i < kCols; i += kSelThreads) stage[i] = load_x1(rv, t, c0 + i);
+    // The squares, each rounded as the reference rounds v * v, in parallel;
+    // then thread 0 adds them in order.
+    for (uint32_t i = threadIdx.x; i < kCols; i += kSelThreads) {
+      const float v = load_x1(rv, t, c0 + i);
+      stage[i] = v * v;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) ss = chain_sum<true>(stage, rv.hidden - c0 < kCols ? rv.hidden - c0 : kCols, ss);
+    if (threadIdx.x == 0) ss = chain_sum(stage, rv.hidden - c0 < kCols ? rv.hidden - c0 : kCols, ss);
     __syncthreads();
   }
   if (threadIdx.x == 0)
@@ -385,8 +376,10 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
       if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c + 8u, w1); else load_raw8<RD>(row, c + 8u, w1);
     }
     xv = load_x1(rv, t, c0 + tid);
-    if (rv.rms && c0 + tid < D) nwv = ldg<float>(rv.norm_weight + c0 + tid);
+    nwv = (rv.rms && c0 + tid < D) ? ldg<float>(rv.norm_weight + c0 + tid) : 1.0f;
   };
+  // Per chunk: its input and products into LDS, the next chunk's loads
+  // issued, then this chunk's additions.
   float acc = 0.0f;
   fetch(0);
   for (uint32_t c0 = 0; c0 < D; c0 += kExactCols) {
@@ -401,7 +394,7 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
     }
     __syncthreads();
     if (c0 + kExactCols < D) fetch(c0 + kExactCols);
-    if (tid < nr) acc = chain_sum<false>(out.prod[tid], D - c0 < kExactCols ? D - c0 : kExactCols, acc);
+    if (tid < nr) acc = chain_sum(out.prod[tid], D - c0 < kExactCols ? D - c0 : kExactCols, acc);
     __syncthreads();
   }
   if (tid < nr) out.ex[out.cl[first + tid]] = acc;
