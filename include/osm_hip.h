@@ -411,6 +411,62 @@ int osm_qpack_expert_repack(const osm_expert_geometry_c* g, const osm_qpack_sect
                             uint64_t slot_stride, const void* slot, void* blob, size_t blob_bytes,
                             int* identity);
 
+/* The qpack container (container/qpack.hpp:15-90, container/qpack.cpp:41-308):
+ * <dir>/manifest.json, <dir>/packed_experts/layout.json and
+ * <dir>/packed_experts/layer_LL.bin. osm_qpack_open parses both JSON files
+ * and runs QpackReader's checks (qpack.cpp:170-255): magic "QPACK",
+ * version 1, non-zero layerCount / expertCount / expertStride, a non-empty
+ * section table whose entries lie within the stride, linearLayers of
+ * layerCount entries, quantBits and quantGroupSize both or neither and in
+ * agreement with the packed gate/up/down shapes, layout.json and every layer
+ * file declared in the manifest with their sizes, each layer file
+ * expertCount x expertStride bytes. Any failure is OSM_E_RUNTIME with the
+ * reference's message ("qpack: malformed layout <path>: ...", "qpack: section
+ * exceeds expertStride: <name>", ...). */
+typedef struct osm_qpack_s* osm_qpack;
+typedef struct osm_qpack_info {
+  const char* magic;             /* valid until osm_qpack_close */
+  const char* model_name;
+  const char* source_checkpoint;
+  uint32_t version;
+  uint32_t expert_count, layer_count, section_count;
+  uint64_t expert_stride;
+  int32_t quant_bits, quant_group_size; /* -1 when the manifest has null */
+} osm_qpack_info;
+int osm_qpack_open(const char* container_dir, osm_qpack* out);
+void osm_qpack_close(osm_qpack q);
+int osm_qpack_get_info(osm_qpack q, osm_qpack_info* out);
+/* Entry i of layout.json's sections[] in file order, in the form
+ * osm_qpack_expert_repack takes (name/dtype valid until close; rank is the
+ * shape's length, rows/cols its first two entries or 0).
+ * osm_qpack_find_section is QpackLayout::find_section: OSM_E_INVALID when
+ * no section has that name. osm_qpack_section_shape copies up to max_dims
+ * entries of the full shape and returns its length in *dims. */
+int osm_qpack_get_section(osm_qpack q, uint32_t i, osm_qpack_section_c* out);
+int osm_qpack_find_section(osm_qpack q, const char* name, osm_qpack_section_c* out);
+int osm_qpack_section_shape(osm_qpack q, uint32_t i, uint64_t* shape, uint32_t max_dims, uint32_t* dims);
+/* linearLayers: out[l] = 1 for a linear-attention layer; n >= layerCount. */
+int osm_qpack_linear_layers(osm_qpack q, uint8_t* out, size_t n);
+/* manifest.files: the declared size of a file named relative to the
+ * container; OSM_E_INVALID when it is not declared. */
+int osm_qpack_file_size(osm_qpack q, const char* relative_path, uint64_t* out);
+/* QpackReader::read_expert (qpack.cpp:257-291): one expertStride slot.
+ * OSM_E_INVALID for a layer or expert out of range (std::out_of_range) or a
+ * destination under the stride (std::invalid_argument); OSM_E_RUNTIME for
+ * an open failure or short read. */
+int osm_qpack_read_expert(osm_qpack q, uint32_t layer, uint32_t expert, void* destination,
+                          size_t destination_bytes);
+/* QpackExpertStorage (storage/qpack_expert_storage.cpp:8-33) over a
+ * container opened and checked as osm_qpack_open does. g == NULL: the
+ * reference's adapter, whole expertStride slots. With a geometry, each slot
+ * is bound by section name (the osm_qpack_expert_repack checks, made once at
+ * creation) and every read lands as the blob of that geometry, so the
+ * storage feeds a host cache and the device caches directly; the stride is
+ * then osm_expert_blob_bytes(g). Reads go through pread, in parallel. The
+ * handle is destroyed with osm_expert_storage_destroy. */
+int osm_qpack_storage_create(const char* container_dir, const osm_expert_geometry_c* g,
+                             osm_expert_storage* out);
+
 typedef struct osm_host_cache_stats {
   uint64_t hits, misses, allocated_slots, capacity_slots, logical_bytes, budget_bytes;
 } osm_host_cache_stats;

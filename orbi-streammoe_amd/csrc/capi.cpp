@@ -116,7 +116,10 @@ struct osm_host_cache_s {
   std::unique_ptr<osm::HostExpertCache> cache;
 };
 struct osm_expert_storage_s {
-  std::unique_ptr<osm::PosixPreadExpertStorage> storage;
+  std::unique_ptr<osm::ExpertStorage> storage;
+};
+struct osm_qpack_s {
+  osm::QpackReader reader;
 };
 struct osm_expert_cache_s {
   osm_context owner = nullptr;
@@ -908,6 +911,113 @@ int osm_qpack_expert_repack(const osm_expert_geometry_c* g, const osm_qpack_sect
     if (!slot || !blob || blob_bytes < plan.blob_bytes) return fail(OSM_E_INVALID, "qpack repack: slot and a blob of osm_expert_blob_bytes needed");
     osm::repack_qpack_expert(plan, static_cast<const std::byte*>(slot), static_cast<std::byte*>(blob));
   }
+  return ok();
+  OSM_GUARD_END
+}
+
+// ---- qpack container ------------------------------------------------------------
+namespace {
+osm_qpack_section_c section_c(const osm::QpackSection& s) {
+  osm_qpack_section_c c{};
+  c.name = s.name.c_str();
+  c.dtype = s.dtype.c_str();
+  c.rank = static_cast<uint32_t>(s.shape.size());
+  c.rows = s.shape.size() > 0 ? s.shape[0] : 0U;
+  c.cols = s.shape.size() > 1 ? s.shape[1] : 0U;
+  c.offset = s.offset;
+  c.size = s.size;
+  return c;
+}
+}  // namespace
+
+int osm_qpack_open(const char* container_dir, osm_qpack* out) {
+  OSM_GUARD_BEGIN
+  if (!container_dir || !out) return fail(OSM_E_INVALID, "null argument");
+  *out = nullptr;
+  *out = new osm_qpack_s{osm::QpackReader(container_dir)};
+  return ok();
+  OSM_GUARD_END
+}
+void osm_qpack_close(osm_qpack q) { delete q; }
+int osm_qpack_get_info(osm_qpack q, osm_qpack_info* out) {
+  if (!q || !out) return fail(OSM_E_INVALID, "null argument");
+  const auto& m = q->reader.manifest();
+  const auto& l = q->reader.layout();
+  out->magic = m.magic.c_str();
+  out->model_name = m.model_name.c_str();
+  out->source_checkpoint = m.source_checkpoint.c_str();
+  out->version = m.version;
+  out->expert_count = l.expert_count;
+  out->layer_count = l.layer_count;
+  out->section_count = static_cast<uint32_t>(l.sections.size());
+  out->expert_stride = l.expert_stride;
+  out->quant_bits = m.quant_bits ? static_cast<int32_t>(*m.quant_bits) : -1;
+  out->quant_group_size = m.quant_group_size ? static_cast<int32_t>(*m.quant_group_size) : -1;
+  return ok();
+}
+int osm_qpack_get_section(osm_qpack q, uint32_t i, osm_qpack_section_c* out) {
+  if (!q || !out) return fail(OSM_E_INVALID, "null argument");
+  const auto& secs = q->reader.layout().sections;
+  if (i >= secs.size()) return fail(OSM_E_INVALID, "qpack: section index out of range");
+  *out = section_c(secs[i]);
+  return ok();
+}
+int osm_qpack_find_section(osm_qpack q, const char* name, osm_qpack_section_c* out) {
+  if (!q || !name || !out) return fail(OSM_E_INVALID, "null argument");
+  const osm::QpackSection* s = q->reader.layout().find_section(name);
+  if (s == nullptr) return fail(OSM_E_INVALID, std::string("qpack: no section named ") + name);
+  *out = section_c(*s);
+  return ok();
+}
+int osm_qpack_section_shape(osm_qpack q, uint32_t i, uint64_t* shape, uint32_t max_dims, uint32_t* dims) {
+  if (!q || !dims || (max_dims && !shape)) return fail(OSM_E_INVALID, "null argument");
+  const auto& secs = q->reader.layout().sections;
+  if (i >= secs.size()) return fail(OSM_E_INVALID, "qpack: section index out of range");
+  const auto& sh = secs[i].shape;
+  *dims = static_cast<uint32_t>(sh.size());
+  for (uint32_t d = 0; d < max_dims && d < sh.size(); ++d) shape[d] = sh[d];
+  return ok();
+}
+int osm_qpack_linear_layers(osm_qpack q, uint8_t* out, size_t n) {
+  if (!q || !out) return fail(OSM_E_INVALID, "null argument");
+  const auto& lin = q->reader.layout().linear_layers;
+  if (n < lin.size()) return fail(OSM_E_INVALID, "qpack: output shorter than layerCount");
+  for (std::size_t l = 0; l < lin.size(); ++l) out[l] = lin[l] ? 1 : 0;
+  return ok();
+}
+int osm_qpack_file_size(osm_qpack q, const char* relative_path, uint64_t* out) {
+  if (!q || !relative_path || !out) return fail(OSM_E_INVALID, "null argument");
+  const auto& files = q->reader.manifest().files;
+  const auto it = files.find(relative_path);
+  if (it == files.end()) return fail(OSM_E_INVALID, std::string("qpack: manifest does not declare ") + relative_path);
+  *out = it->second;
+  return ok();
+}
+int osm_qpack_read_expert(osm_qpack q, uint32_t layer, uint32_t expert, void* destination,
+                          size_t destination_bytes) {
+  OSM_GUARD_BEGIN
+  if (!q || (!destination && destination_bytes)) return fail(OSM_E_INVALID, "null argument");
+  try {
+    q->reader.read_expert(layer, expert, {static_cast<std::byte*>(destination), destination_bytes});
+  } catch (const std::out_of_range& e) {
+    return fail(OSM_E_INVALID, e.what());
+  }
+  return ok();
+  OSM_GUARD_END
+}
+int osm_qpack_storage_create(const char* container_dir, const osm_expert_geometry_c* g,
+                             osm_expert_storage* out) {
+  OSM_GUARD_BEGIN
+  if (!container_dir || !out) return fail(OSM_E_INVALID, "null argument");
+  *out = nullptr;
+  std::unique_ptr<osm::QpackExpertStorage> st;
+  if (g) {
+    const osm_expert_geometry geom = geom_of(g);
+    st = std::make_unique<osm::QpackExpertStorage>(container_dir, &geom);
+  } else {
+    st = std::make_unique<osm::QpackExpertStorage>(container_dir);
+  }
+  *out = new osm_expert_storage_s{std::move(st)};
   return ok();
   OSM_GUARD_END
 }

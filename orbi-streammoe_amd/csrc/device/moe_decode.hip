@@ -996,10 +996,8 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
 
 template <int META, int CPL, int PER, int ROWS>
 __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
-  const uint32_t lane = threadIdx.x % kWave;
   const uint32_t t = blockIdx.z;
   const uint32_t j = blockIdx.y;
-  const uint32_t D = p.g.hidden;
 
   const uint8_t* blob;
   if constexpr (PER > 0) {

@@ -857,7 +857,7 @@ __global__ void swiglu_terms_kernel(const float* __restrict__ part, uint32_t nsp
   const size_t plane = static_cast<size_t>(P) * I;
   for (size_t i0 = static_cast<size_t>(blockIdx.x) * blockDim.x; i0 < n; i0 += stride) {
     const size_t i = i0 + threadIdx.x;
-    float total = 0.0f, sq = 0.0f;
+    float total = 0.0f;
     if (i < n) {
       const size_t pair = i / words, wd = i % words;
       const float* gp = part + pair * I + wd * 8u;

@@ -395,6 +395,69 @@ struct QpackExpertPlan {
                                                 std::uint64_t slot_stride, const osm_expert_geometry& g);
 void repack_qpack_expert(const QpackExpertPlan& plan, const std::byte* slot, std::byte* blob);
 
+// The qpack container (container/qpack.hpp:15-90): manifest.json,
+// packed_experts/layout.json and packed_experts/layer_LL.bin, parsed and
+// validated as QpackReader does (container/qpack.cpp:41-247).
+struct QpackSection {
+  std::string name, dtype;
+  std::vector<std::uint64_t> shape;
+  std::uint64_t offset{}, size{};
+};
+struct QpackLayout {
+  std::uint32_t expert_count{}, layer_count{};
+  std::uint64_t expert_stride{};
+  std::vector<QpackSection> sections;
+  std::vector<bool> linear_layers;
+  [[nodiscard]] const QpackSection* find_section(std::string_view name) const noexcept;
+};
+struct QpackManifest {
+  std::string magic;
+  std::uint32_t version{};
+  std::string model_name, source_checkpoint;
+  std::optional<std::uint32_t> quant_bits, quant_group_size;
+  std::unordered_map<std::string, std::uint64_t> files;
+};
+class QpackReader {
+ public:
+  static constexpr std::string_view kMagic = "QPACK";
+  static constexpr std::uint32_t kManifestVersion = 1;
+  // Throws std::runtime_error for a container that fails a check.
+  explicit QpackReader(std::filesystem::path container_dir);
+  [[nodiscard]] const std::filesystem::path& container_dir() const noexcept { return dir_; }
+  [[nodiscard]] const QpackManifest& manifest() const noexcept { return manifest_; }
+  [[nodiscard]] const QpackLayout& layout() const noexcept { return layout_; }
+  [[nodiscard]] std::filesystem::path layer_path(std::uint32_t layer) const;
+  // One fixed-stride slot: std::out_of_range for a bad layer or expert,
+  // std::invalid_argument for a destination under the stride,
+  // std::runtime_error for an I/O failure or short read.
+  void read_expert(std::uint32_t layer, std::uint32_t expert, std::span<std::byte> destination) const;
+
+ private:
+  std::filesystem::path dir_;
+  QpackManifest manifest_;
+  QpackLayout layout_;
+};
+
+// Expert reads from a qpack container. Without a geometry it is the
+// reference's QpackExpertStorage (storage/qpack_expert_storage.cpp:8-33):
+// whole slots of expertStride bytes. With one, each slot is bound by
+// section name (plan_qpack_expert) and repacked into the blob's order on
+// admission; the stride is then the blob's size. Reads go through pread,
+// in parallel.
+class QpackExpertStorage final : public ExpertStorage {
+ public:
+  explicit QpackExpertStorage(std::filesystem::path container_dir, const osm_expert_geometry* g = nullptr);
+  [[nodiscard]] std::size_t expert_stride_bytes() const noexcept override;
+  void read_experts(std::span<ExpertReadRequest> requests) override;
+  [[nodiscard]] const QpackReader& reader() const noexcept { return reader_; }
+  [[nodiscard]] bool repacks() const noexcept { return plan_.has_value() && !plan_->identity; }
+
+ private:
+  QpackReader reader_;
+  std::optional<QpackExpertPlan> plan_;
+  std::unique_ptr<PosixPreadExpertStorage> pread_;
+};
+
 struct ExpertCacheEntry {
   ExpertId id{};
   std::size_t slot{};

@@ -154,6 +154,16 @@ _PROTOTYPES = {
     "osm_pread_storage_create": (c_int, [c_char_p, c_uint32, c_uint32, c_size_t, POINTER(_H)]),
     "osm_moe_run_cached_layers": (c_int, [_H, c_void_p, c_void_p, c_uint32, _H, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p]),
     "osm_qpack_expert_repack": (c_int, [POINTER(Geometry), c_void_p, c_size_t, c_uint64, c_void_p, c_void_p, c_size_t, POINTER(c_int)]),
+    "osm_qpack_open": (c_int, [c_char_p, POINTER(_H)]),
+    "osm_qpack_close": (None, [_H]),
+    "osm_qpack_get_info": (c_int, [_H, c_void_p]),
+    "osm_qpack_get_section": (c_int, [_H, c_uint32, c_void_p]),
+    "osm_qpack_find_section": (c_int, [_H, c_char_p, c_void_p]),
+    "osm_qpack_section_shape": (c_int, [_H, c_uint32, c_void_p, c_uint32, POINTER(c_uint32)]),
+    "osm_qpack_linear_layers": (c_int, [_H, c_void_p, c_size_t]),
+    "osm_qpack_file_size": (c_int, [_H, c_char_p, POINTER(c_uint64)]),
+    "osm_qpack_read_expert": (c_int, [_H, c_uint32, c_uint32, c_void_p, c_size_t]),
+    "osm_qpack_storage_create": (c_int, [c_char_p, c_void_p, POINTER(_H)]),
     "osm_expert_storage_destroy": (None, [_H]),
     "osm_expert_storage_stride": (c_size_t, [_H]),
     "osm_expert_storage_read": (c_int, [_H, c_void_p, c_void_p, c_void_p, c_size_t, c_size_t]),
@@ -754,6 +764,71 @@ def qpack_expert_repack(g: Geometry, sections, slot_stride, slot=None):
     return blob, bool(ident.value)
 
 
+class QpackInfo(ctypes.Structure):
+    """osm_qpack_info."""
+
+    _fields_ = [("magic", c_char_p), ("model_name", c_char_p), ("source_checkpoint", c_char_p),
+                ("version", c_uint32), ("expert_count", c_uint32), ("layer_count", c_uint32),
+                ("section_count", c_uint32), ("expert_stride", c_uint64), ("quant_bits", ctypes.c_int32),
+                ("quant_group_size", ctypes.c_int32)]
+
+
+class QpackReader(_Handle):
+    """QpackReader (container/qpack.hpp:15-90): the container's manifest and
+    layout, parsed and checked on open; fixed-stride expert reads."""
+
+    _destroy = "osm_qpack_close"
+
+    def __init__(self, container_dir):
+        h = c_void_p()
+        check(load().osm_qpack_open(os.fsencode(container_dir), ctypes.byref(h)))
+        super().__init__(h)
+        info = QpackInfo()
+        check(load().osm_qpack_get_info(self.h, ctypes.byref(info)))
+        self.magic = info.magic.decode()
+        self.model_name = info.model_name.decode()
+        self.source_checkpoint = info.source_checkpoint.decode()
+        self.version = info.version
+        self.expert_count, self.layer_count = info.expert_count, info.layer_count
+        self.expert_stride = info.expert_stride
+        self.quant_bits = None if info.quant_bits < 0 else info.quant_bits
+        self.quant_group_size = None if info.quant_group_size < 0 else info.quant_group_size
+        self.sections = [self._section(i) for i in range(info.section_count)]
+        lin = np.zeros(max(self.layer_count, 1), np.uint8)
+        check(load().osm_qpack_linear_layers(self.h, _p(lin), lin.size))
+        self.linear_layers = [bool(v) for v in lin[:self.layer_count]]
+
+    def _section(self, i) -> dict:
+        c = QpackSection()
+        check(load().osm_qpack_get_section(self.h, i, ctypes.byref(c)))
+        dims = c_uint32(0)
+        check(load().osm_qpack_section_shape(self.h, i, None, 0, ctypes.byref(dims)))
+        shape = np.zeros(max(dims.value, 1), np.uint64)
+        check(load().osm_qpack_section_shape(self.h, i, _p(shape), dims.value, ctypes.byref(dims)))
+        return {"name": c.name.decode(), "dtype": c.dtype.decode(), "shape": [int(v) for v in shape[:dims.value]],
+                "offset": int(c.offset), "size": int(c.size)}
+
+    def find_section(self, name):
+        """QpackLayout::find_section: the entry, or None."""
+        c = QpackSection()
+        if load().osm_qpack_find_section(self.h, name.encode(), ctypes.byref(c)) != OSM_OK:
+            return None
+        return next(s for s in self.sections if s["name"] == name)
+
+    def file_size(self, relative_path):
+        """manifest.files[relative_path], or None when not declared."""
+        v = c_uint64(0)
+        if load().osm_qpack_file_size(self.h, os.fsencode(relative_path), ctypes.byref(v)) != OSM_OK:
+            return None
+        return int(v.value)
+
+    def read_expert(self, layer, expert, destination_bytes=None) -> np.ndarray:
+        n = self.expert_stride if destination_bytes is None else destination_bytes
+        out = np.empty(n, np.uint8)
+        check(load().osm_qpack_read_expert(self.h, layer, expert, _p(out), n))
+        return out
+
+
 class PreadStorage(_Handle):
     """PosixPreadExpertStorage: <container_dir>/packed_experts/layer_LL.bin
     holds layer LL's `experts` blobs back to back at `stride`."""
@@ -779,6 +854,18 @@ class PreadStorage(_Handle):
         dests = (c_void_p * max(n, 1))(*[o.ctypes.data for o in outs])
         check(load().osm_expert_storage_read(self.h, _p(ls), _p(es), dests, n, size))
         return outs
+
+
+class QpackStorage(PreadStorage):
+    """QpackExpertStorage over a qpack container: whole expertStride slots,
+    or, given a geometry, each slot repacked into that geometry's blob."""
+
+    def __init__(self, container_dir, g: "Geometry | None" = None):
+        h = c_void_p()
+        check(load().osm_qpack_storage_create(os.fsencode(container_dir),
+                                              ctypes.byref(g) if g is not None else None, ctypes.byref(h)))
+        _Handle.__init__(self, h)
+        self.stride = load().osm_expert_storage_stride(self.h)
 
 
 class HostExpertCache(_Handle):

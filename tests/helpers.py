@@ -149,3 +149,80 @@ def pmap(fn, items, workers=None):
     n = workers or min(16, os.cpu_count() or 1, max(1, len(items)))
     with ThreadPoolExecutor(max_workers=n) as ex:
         return list(ex.map(fn, items))
+
+
+def write_qpack(root, layer_slots, sections, stride, *, linear_layers=None, magic="QPACK", version=1,
+                quant_bits=4, quant_group_size=None, layout_text=None, declare=True, model_name="qwen3_next"):
+    """A qpack container (container/qpack.hpp:15-90) at `root`:
+    packed_experts/layer_LL.bin from layer_slots[LL] (uint8 [experts, stride]),
+    packed_experts/layout.json from `sections` (dicts with name, dtype,
+    shape, offset, size) unless layout_text gives the file's text, and a
+    manifest.json declaring every file with its size (declare=False leaves
+    the layer files out). quant_group_size None writes null quantization."""
+    import json
+    pe = os.path.join(root, "packed_experts")
+    os.makedirs(pe, exist_ok=True)
+    layers = len(layer_slots)
+    experts = layer_slots[0].shape[0] if layers else 0
+    if layout_text is None:
+        layout_text = json.dumps({
+            "expertCount": experts, "layerCount": layers, "expertStride": stride,
+            "sections": [{"name": s["name"], "dtype": s["dtype"], "shape": list(s["shape"]),
+                          "offset": s["offset"], "size": s["size"]} for s in sections],
+            "linearLayers": list(linear_layers) if linear_layers is not None else [True] * layers,
+        }, indent=2)
+    with open(os.path.join(pe, "layout.json"), "w") as f:
+        f.write(layout_text)
+    files = {"packed_experts/layout.json": os.path.getsize(os.path.join(pe, "layout.json"))}
+    for l, slots in enumerate(layer_slots):
+        path = os.path.join(pe, f"layer_{l:02d}.bin")
+        np.ascontiguousarray(slots, dtype=np.uint8).tofile(path)
+        if declare:
+            files[f"packed_experts/layer_{l:02d}.bin"] = os.path.getsize(path)
+    manifest = {"magic": magic, "version": version, "modelName": model_name,
+                "sourceCheckpoint": "synthetic", "quantBits": quant_bits if quant_group_size else None,
+                "quantGroupSize": quant_group_size, "files": files}
+    with open(os.path.join(root, "manifest.json"), "w") as f:
+        json.dump(manifest, f, indent=2)
+    return root
+
+
+def qpack_q4_sections(D, I, G, meta_dtype, order=None, gap=0, extra=()):
+    """The nine sections of one q4 expert slot (gate/up/down x weight/scales/
+    biases) in `order` (names; default the blob's), each followed by `gap`
+    bytes; `extra` adds (name, dtype, shape, size) entries first. Returns
+    (sections, slot stride)."""
+    esz = 4 if meta_dtype == "F32" else 2
+    shapes = {}
+    for p in ("gate_proj", "up_proj", "down_proj"):
+        out, inn = (I, D) if p != "down_proj" else (D, I)
+        shapes[p + ".weight"] = ("U32", (out, inn // 8), out * inn // 8 * 4)
+        shapes[p + ".scales"] = (meta_dtype, (out, inn // G), out * inn // G * esz)
+        shapes[p + ".biases"] = (meta_dtype, (out, inn // G), out * inn // G * esz)
+    for name, dt, shape, size in extra:
+        shapes[name] = (dt, shape, size)
+    names = [e[0] for e in extra] + (order or [p + s for p in ("gate_proj", "up_proj", "down_proj")
+                                               for s in (".weight", ".scales", ".biases")])
+    secs, off = [], 0
+    for n in names:
+        dt, shape, size = shapes[n]
+        secs.append({"name": n, "dtype": dt, "shape": tuple(shape), "offset": off, "size": size})
+        off += size + gap
+    return secs, off
+
+
+def blob_to_slot(blob, sections, stride, D, I, G, meta_dtype, fill=0xA5):
+    """The q4 blob's nine sections placed at the table's offsets in a slot of
+    `stride` bytes (the rest `fill`)."""
+    esz = 4 if meta_dtype == "F32" else 2
+    parts, off = {}, 0
+    for p in ("gate_proj", "up_proj", "down_proj"):
+        out, inn = (I, D) if p != "down_proj" else (D, I)
+        for s, n in ((".weight", out * inn // 2), (".scales", out * inn // G * esz), (".biases", out * inn // G * esz)):
+            parts[p + s] = blob[off:off + n]
+            off += n
+    slot = np.full(stride, fill, np.uint8)
+    for s in sections:
+        if s["name"] in parts:
+            slot[s["offset"]:s["offset"] + s["size"]] = parts[s["name"]]
+    return slot

@@ -12,7 +12,8 @@ import pytest
 
 import oracle as O
 import osm_hip
-from helpers import cache_fixture_expert, cache_fixture_token, max_abs, rel_l2
+from helpers import (blob_to_slot, cache_fixture_expert, cache_fixture_token, max_abs, qpack_q4_sections, rel_l2,
+                     write_qpack)
 
 pytestmark = pytest.mark.gpu
 
@@ -242,6 +243,49 @@ def test_cached_decode_from_pread_storage(ctx, tmp_path):
         got = moe.run_cached(cache, 0, x[t], sublayer=t % 2 == 0)
         ref = moe.run_slab(slab, 0, x[t], sublayer=t % 2 == 0)
         assert np.array_equal(got["ids"], ref["ids"]) and np.array_equal(got["out"], ref["out"])
+    assert cache.stats()["evictions"] > 0 and host.stats()["misses"] > 0
+
+
+def test_cached_decode_from_noncanonical_qpack(ctx, tmp_path):
+    # A qpack container whose slots hold the nine sections in another order,
+    # spaced apart, after an unrelated section: layout.json parsed and
+    # checked, each slot read by pread and repacked into the blob, filled
+    # from pinned host memory into 16 HBM slots, then decoded. Layer 1 of a
+    # two-layer container is the one decoded. Outputs match the all-resident
+    # decode bit for bit, and the oracle's routing and output.
+    seed, D, I, G, E, k = 25, 256, 128, 64, 32, 4
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    order = ["up_proj.scales", "down_proj.weight", "gate_proj.biases", "up_proj.weight", "gate_proj.weight",
+             "down_proj.biases", "up_proj.biases", "down_proj.scales", "gate_proj.scales"]
+    secs, stride = qpack_q4_sections(D, I, G, "BF16", order=order, gap=40, extra=[("lm_hint", "F32", (9,), 36)])
+    blobs = [[O.synth_expert_blob(seed, l, e, D, I, G) for e in range(E)] for l in range(2)]
+    write_qpack(str(tmp_path), [np.stack([blob_to_slot(b, secs, stride, D, I, G, "BF16") for b in layer])
+                                for layer in blobs], secs, stride, linear_layers=[True, False], quant_group_size=G)
+    storage = osm_hip.QpackStorage(str(tmp_path), g)
+    assert storage.stride == osm_hip.expert_blob_bytes(g) < stride
+    host = osm_hip.HostExpertCache.from_storage(storage, 20 * storage.stride, pinned=True)
+    cache = osm_hip.ExpertCache(ctx, 16 * storage.stride, host_cache=host, g=g)
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blobs[1][e])
+    router = O.synth_router_bf16(seed, 1, E, D)
+    sg = O.synth_shared_gate_bf16(seed, 1, D)
+    norm = O.synth_norm_weight(seed, 1, D)
+    shared = O.synth_expert_blob(seed, 1, O.SHARED_EXPERT_ID, D, I, G)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, router, osm_hip.BF16, sg, norm, shared, max_tokens=1)
+    rf, sgf = O.bf16_bits_to_f32(router), O.bf16_bits_to_f32(sg)
+    x = O.synth_tokens(seed, 1, 12, D)
+    for t in range(12):
+        sub = t % 2 == 0
+        got = moe.run_cached(cache, 1, x[t], sublayer=sub)
+        ref = moe.run_slab(slab, 0, x[t], sublayer=sub)
+        assert np.array_equal(got["ids"], ref["ids"]) and np.array_equal(got["out"], ref["out"]), t
+        if sub:
+            ora = O.moe_sublayer(x[t], norm, 1e-6, rf, blobs[1], shared, sgf, D, I, G, O.META_BF16, k)
+        else:
+            ora = O.qwen_sparse_moe(x[t], rf, blobs[1], shared, sgf, D, I, G, O.META_BF16, k)
+        assert np.array_equal(np.asarray(got["ids"]).reshape(-1), ora["ids"]), t
+        assert rel_l2(np.asarray(got["out"]).reshape(-1), ora["out"]) <= 1e-3, t
     assert cache.stats()["evictions"] > 0 and host.stats()["misses"] > 0
 
 
