@@ -235,6 +235,10 @@ constexpr uint32_t kExactCols = 256;
 constexpr uint32_t kExactRows = 16;  // candidates per pass
 constexpr uint32_t kExactStride = kExactCols + 4u;  // LDS row stride: 16-byte aligned rows, adders' reads in distinct banks
 
+// Bins of the device ranking's distance histogram (rank_device).
+constexpr uint32_t kHistBins = 64;
+constexpr float kHistSpan = 256.0f;
+
 __device__ __forceinline__ float tie_margin(float mx, float l) { return 0x1p-20f + 0x1p-23f * (mx - l + 1.0f); }
 
 // Result of one token's selection, in LDS: ids, device logits and bounds and
@@ -250,16 +254,19 @@ struct Selection {
   float val[kSelThreads * PER];   // device logit of every expert
   float aux[kSelThreads * PER];   // its bound; on the exact path, its exp(fl(L - m)) (-1: no candidate)
   float ex[kSelThreads * PER];    // exact path: the reference's logit of a candidate
-  float red[2][kSelWaves];
-  uint64_t cand[kSelWaves * OSMD_MAX_TOP_K];  // (key << 32) | ~id, wavefront-major
+  float red[3][kSelWaves];
+  uint64_t cand[kWave];                       // (key << 32) | ~id of the ranked candidates
+  float clg[kWave], cbd[kWave];               // their device logits and bounds
+  uint32_t hist[kHistBins];                   // experts per bin of distance from the largest logit
   uint32_t fid[OSMD_MAX_TOP_K + 1];           // exact path: candidates by rank
   float scal[2];
-  uint32_t nunresolved, ncand, wcount[kSelWaves];
+  uint32_t nunresolved, ncand, thr, flags, wcount[kSelWaves];
   uint16_t cl[kSelThreads * PER];             // exact path: candidate list
   float xe[kExactCols];                       // exact path: the input of one chunk of columns
   __attribute__((aligned(16))) float prod[kExactRows][kExactStride];  // exact path: rounded products of one chunk
 };
 static_assert(kExactCols == kSelThreads && kExactRows * 16u == kSelThreads, "exact-path chunk mapping");
+static_assert(kSelWaves * OSMD_MAX_TOP_K <= kWave, "the fallback's candidates fit the candidate list");
 
 __device__ __forceinline__ void sort_step(uint32_t* k, uint32_t* n, int a, int b) {
   // Descending on (k, n): swap when (k[b], n[b]) > (k[a], n[a]).
@@ -512,11 +519,139 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
   return full;
 }
 
+// Maximum and minimum over the wavefront, the two reductions interleaved.
+__device__ __forceinline__ void wave_max_min(float& mx, float& mn) {
+  float a = mx, b = mn;
+  a = fmaxf(a, dpp<kDppXor1>(a, a));
+  b = fminf(b, dpp<kDppXor1>(b, b));
+  a = fmaxf(a, dpp<kDppXor2>(a, a));
+  b = fminf(b, dpp<kDppXor2>(b, b));
+  a = fmaxf(a, dpp<kDppRowHalfMirror>(a, a));
+  b = fminf(b, dpp<kDppRowHalfMirror>(b, b));
+  a = fmaxf(a, dpp<kDppRowMirror>(a, a));
+  b = fminf(b, dpp<kDppRowMirror>(b, b));
+  a = fmaxf(a, dpp<kDppRowBcast15, 0xA>(a, a));
+  b = fminf(b, dpp<kDppRowBcast15, 0xA>(b, b));
+  a = fmaxf(a, dpp<kDppRowBcast31, 0xC>(a, a));
+  b = fminf(b, dpp<kDppRowBcast31, 0xC>(b, b));
+  mx = readlane_f(a, 63);
+  mn = readlane_f(b, 63);
+}
+
+// The device ranking: the k largest (logit, lower id) keys of the workgroup's
+// experts into out.id / out.lg / out.bd. Distances from the largest logit
+// are bucketed, d = fl(fl(mx - l) * inv) with inv = kHistSpan / (mx - mn),
+// into kHistBins bins (the last, which nothing counts, takes everything
+// beyond), and the first bin at which the count reaches k bounds the
+// candidates: d is monotone in l, so every expert of a later bin has a
+// smaller logit than every candidate. At most kWave candidates are ranked
+// by one wavefront; otherwise (all logits equal, a non-finite range, a
+// distribution too skewed for the bins) each wavefront extracts its own top
+// k and wavefront 0 ranks those.
+template <int PER>
+__device__ __forceinline__ void rank_device(const RouteView& rv, const float (&l)[PER], const float (&b)[PER],
+                                            Selection<PER>& out, float mx, float mn) {
+  const uint32_t E = rv.expert_count;
+  const uint32_t k = rv.top_k;
+  const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const uint32_t base = tid * PER;
+  const float range = mx - mn;
+  const bool binned = range > 0.0f && range < INFINITY;  // workgroup-uniform
+  uint32_t bin[PER] = {};
+  if (binned) {
+    const float inv = kHistSpan / range;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float d = (mx - l[j]) * inv;  // NaN (a NaN logit) fails the test: last bin
+      bin[j] = d < static_cast<float>(kHistBins - 1u) ? static_cast<uint32_t>(d) : kHistBins - 1u;
+      if (base + j < E && bin[j] < kHistBins - 1u) atomicAdd(&out.hist[bin[j]], 1u);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float incl = wave_incl_scan(static_cast<float>(out.hist[lane]));  // counts <= 1024: exact
+    const uint64_t reached = __ballot(incl >= static_cast<float>(k));
+    const int first = reached ? __ffsll(static_cast<long long>(reached)) - 1 : kWave - 1;
+    const float count = readlane_f(incl, first);
+    if (lane == 0) {
+      out.thr = (binned && reached && count <= static_cast<float>(kWave)) ? static_cast<uint32_t>(first) : ~0u;
+      out.ncand = 0;
+    }
+  }
+  __syncthreads();
+  const uint32_t thr = out.thr;
+  if (thr != ~0u) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const uint32_t e = base + j;
+      if (e < E && bin[j] <= thr) {
+        const uint32_t pos = atomicAdd(&out.ncand, 1u);
+        out.cand[pos] = (static_cast<uint64_t>(ordered_key(l[j])) << 32) | ~e;
+        out.clg[pos] = l[j];
+        out.cbd[pos] = b[j];
+      }
+    }
+  } else {
+    // Fallback: each wavefront's top k by (logit, lower id), one pop per
+    // round, lane r keeping round r's result.
+    uint32_t key[PER], nid[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      key[j] = base + j < E ? ordered_key(l[j]) : 0u;  // above 0 for every real logit
+      nid[j] = ~(base + j);
+    }
+    sort_lane<PER>(key, nid);
+    uint32_t rk = 0u, ri = 0u;
+#pragma unroll 1
+    for (uint32_t r = 0; r < k; ++r) {
+      const uint32_t mk = wave_max_u32(key[0]);
+      const int wl = __ffsll(__ballot(key[0] == mk)) - 1;  // never empty: mk is some lane's key
+      const uint32_t sid = ~static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(nid[0]), wl));
+      rk = lane == r ? mk : rk;
+      ri = lane == r ? sid : ri;
+      const bool won = static_cast<int>(lane) == wl;  // pop the head
+#pragma unroll
+      for (int j = 0; j + 1 < PER; ++j) {
+        key[j] = won ? key[j + 1] : key[j];
+        nid[j] = won ? nid[j + 1] : nid[j];
+      }
+      key[PER - 1] = won ? 0u : key[PER - 1];
+      nid[PER - 1] = won ? 0u : nid[PER - 1];
+    }
+    if (lane < k) {
+      const uint32_t id = ri < E ? ri : E - 1u;  // key-0 entries (fewer than k experts here) stay in the table
+      out.cand[wave * k + lane] = (static_cast<uint64_t>(rk) << 32) | ~ri;
+      out.clg[wave * k + lane] = out.val[id];
+      out.cbd[wave * k + lane] = out.aux[id];
+    }
+    if (tid == 0) out.ncand = kSelWaves * k;
+  }
+  __syncthreads();
+  // Wavefront 0: each lane ranks one candidate against all of them (LDS
+  // broadcast reads); the k best write their place. Fallback candidates of
+  // key 0 (fewer than k experts in a wavefront) always have k real ones
+  // above them.
+  if (wave == 0) {
+    const uint32_t nc = out.ncand;
+    const uint64_t mine = lane < nc ? out.cand[lane] : 0u;
+    uint32_t rank = 0;
+#pragma unroll 4
+    for (uint32_t c = 0; c < nc; ++c) rank += out.cand[c] > mine ? 1u : 0u;
+    if (lane < nc && rank < k) {
+      const uint32_t id0 = ~static_cast<uint32_t>(mine);
+      out.id[rank] = id0 < E ? id0 : E - 1u;  // a table lookup always stays in the table
+      out.lg[rank] = out.clg[lane];
+      out.bd[rank] = out.cbd[lane];
+    }
+  }
+  __syncthreads();
+}
+
 // Selection from this thread's device logits l[j] and bounds b[j] of experts
 // tid*PER + j (entries past E are ignored) and their table pointers. Every
 // thread of the workgroup calls it; it ends with a barrier, after which
-// out.id and out.p are complete. `count`: add this selection to the
-// routing counters (one workgroup per token does).
+// out.id, out.p and out.flags are complete. `count`: add this selection to
+// the routing counters now (otherwise count_selection does it later).
 template <int PER>
 __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, const float (&l)[PER],
                                               const float (&b)[PER], const uint8_t* const (&tab)[PER],
@@ -525,48 +660,28 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
   const uint32_t k = rv.top_k;
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const uint32_t base = tid * PER;
-  uint32_t key[PER], nid[PER];
-  float mx = -INFINITY;
+  float mx = -INFINITY, mn = INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const bool valid = base + j < E;
-    key[j] = valid ? ordered_key(l[j]) : 0u;  // above 0 for every real logit
-    nid[j] = ~(base + j);
-    if (valid) {
+    if (base + j < E) {
       out.blob[base + j] = tab[j];
       out.val[base + j] = l[j];
       out.aux[base + j] = b[j];
       mx = fmaxf(mx, l[j]);
+      mn = fminf(mn, l[j]);
     }
   }
-  mx = wave_max(mx);
-  if (lane == 0) out.red[0][wave] = mx;
-  sort_lane<PER>(key, nid);
-
-  // This wavefront's top-k by (logit, lower id). Each round is branch-free
-  // (the pop is a select on every lane) and lane r keeps round r's result,
-  // written out after the last round. The loop stays rolled: one body,
-  // fetched once (the selection runs on one workgroup, so its code is cold).
-  uint32_t rk = 0u, ri = 0u;
-#pragma unroll 1
-  for (uint32_t r = 0; r < k; ++r) {
-    const uint32_t mk = wave_max_u32(key[0]);
-    const int wl = __ffsll(__ballot(key[0] == mk)) - 1;  // never empty: mk is some lane's key
-    const uint32_t sid = ~static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(nid[0]), wl));
-    rk = lane == r ? mk : rk;
-    ri = lane == r ? sid : ri;
-    const bool won = static_cast<int>(lane) == wl;  // pop the head
-#pragma unroll
-    for (int j = 0; j + 1 < PER; ++j) {
-      key[j] = won ? key[j + 1] : key[j];
-      nid[j] = won ? nid[j + 1] : nid[j];
-    }
-    key[PER - 1] = won ? 0u : key[PER - 1];
-    nid[PER - 1] = won ? 0u : nid[PER - 1];
+  wave_max_min(mx, mn);
+  if (lane == 0) {
+    out.red[0][wave] = mx;
+    out.red[1][wave] = mn;
   }
-  if (lane < k) out.cand[wave * k + lane] = (static_cast<uint64_t>(rk) << 32) | ~ri;
+  if (tid < kHistBins) out.hist[tid] = 0u;
   __syncthreads();
   mx = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
+  mn = fminf(fminf(out.red[1][0], out.red[1][1]), fminf(out.red[1][2], out.red[1][3]));
+
+  rank_device<PER>(rv, l, b, out, mx, mn);
 
   // The softmax denominator over every expert (reference_ops.cpp:135-151),
   // its four wavefront sums combined in a fixed order.
@@ -574,30 +689,11 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
 #pragma unroll
   for (int j = 0; j < PER; ++j) sum += (base + j < E) ? expf(l[j] - mx) : 0.0f;
   sum = wave_sum(sum);
-  if (lane == 0) out.red[1][wave] = sum;
-
-  // Wavefront 0: each lane ranks one candidate against all of them (LDS
-  // broadcast reads); the k best write their place. Candidates of key 0
-  // (fewer than k experts in a wavefront) always have k real ones above.
-  if (wave == 0) {
-    const uint32_t nc = kSelWaves * k;
-    const uint64_t mine = lane < nc ? out.cand[lane] : 0u;
-    uint32_t rank = 0;
-#pragma unroll 4
-    for (uint32_t c = 0; c < nc; ++c) rank += out.cand[c] > mine ? 1u : 0u;
-    if (lane < nc && rank < k) {
-      const uint32_t id0 = ~static_cast<uint32_t>(mine);
-      const uint32_t id = id0 < E ? id0 : E - 1u;  // a table lookup always stays in the table
-      out.id[rank] = id;
-      out.lg[rank] = out.val[id];
-      out.bd[rank] = out.aux[id];
-    }
-  }
-  __syncthreads();
-  sum = ((out.red[1][0] + out.red[1][1]) + out.red[1][2]) + out.red[1][3];
+  if (lane == 0) out.red[2][wave] = sum;
 
   // The certificate: every expert outside the picks below the k-th's lower
-  // bound, and (thread 0) the picks in order and far from underflow.
+  // bound, each adjacent pair of picks far enough apart (one thread per
+  // pair), and the k-th pick far from underflow.
   const float lk = out.lg[k - 1];
   const float low = lk - kBoundSlack * out.bd[k - 1];
   const uint64_t kth = (static_cast<uint64_t>(ordered_key(lk)) << 32) | ~out.id[k - 1];
@@ -608,18 +704,19 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
     const uint64_t c = (static_cast<uint64_t>(ordered_key(l[j])) << 32) | ~e;
     if (e < E && c < kth && !(l[j] + kBoundSlack * b[j] + tie_margin(mx, l[j]) < low)) bad = true;
   }
-  if (tid == 0) {
-    for (uint32_t i = 0; i + 1 < k; ++i) {
-      const float need = kBoundSlack * (out.bd[i] + out.bd[i + 1]) +
-                         (out.id[i] > out.id[i + 1] ? tie_margin(mx, out.lg[i + 1]) : 0.0f);
-      if (!(out.lg[i] - out.lg[i + 1] > need)) bad = true;
-    }
-    if (!(lk - mx >= -kUnderflowGap)) bad = true;
+  if (tid + 1u < k) {
+    const uint32_t i = tid;
+    const float need = kBoundSlack * (out.bd[i] + out.bd[i + 1]) +
+                       (out.id[i] > out.id[i + 1] ? tie_margin(mx, out.lg[i + 1]) : 0.0f);
+    if (!(out.lg[i] - out.lg[i + 1] > need)) bad = true;
   }
+  if (tid == 0 && !(lk - mx >= -kUnderflowGap)) bad = true;
   bad = __syncthreads_or(bad) != 0;
+  sum = ((out.red[2][0] + out.red[2][1]) + out.red[2][2]) + out.red[2][3];
   bool full = false;
   if (bad) full = select_exact<PER>(rv, t, l, b, out, mx);
   if (tid < k) out.p[tid] = expf(out.lg[tid] - mx) / sum;
+  if (tid == 0) out.flags = (bad ? 1u : 0u) | (full ? 2u : 0u);
   if (count && tid == 0 && rv.stats != nullptr) {
     atomicAdd(rv.stats + 0, 1u);
     if (bad) atomicAdd(rv.stats + 1, 1u);
@@ -627,6 +724,18 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
     if (bad && out.nunresolved != 0u) atomicAdd(rv.stats + 3, out.nunresolved);
   }
   __syncthreads();
+}
+
+// The routing counters of a selection made with count = false
+// (thread 0, after the selection).
+template <int PER>
+__device__ __forceinline__ void count_selection(const RouteView& rv, const Selection<PER>& s) {
+  if (rv.stats == nullptr) return;
+  const bool bad = (s.flags & 1u) != 0u;
+  atomicAdd(rv.stats + 0, 1u);
+  if (bad) atomicAdd(rv.stats + 1, 1u);
+  if (s.flags & 2u) atomicAdd(rv.stats + 2, 1u);
+  if (bad && s.nunresolved != 0u) atomicAdd(rv.stats + 3, s.nunresolved);
 }
 
 // Loads token t's logits and their bounds (and table pointers) and selects;
@@ -998,28 +1107,32 @@ template <int META, int CPL, int PER, int ROWS>
 __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
   const uint32_t t = blockIdx.z;
   const uint32_t j = blockIdx.y;
-
-  const uint8_t* blob;
+  // x is read with the weights, after the selection, so its slices are not
+  // held in registers through it; both loads are in flight together.
+  auto rows = [&](const uint8_t* blob) {
+    if (blob == nullptr) blob = p.rv.fallback;  // never dereference a null slot
+    float xr[CPL][32];
+    gate_up_rows<META, CPL, ROWS>(p, t, j, blockIdx.x, blob, xr, [&](size_t i, float v) { p.h[i] = v; });
+  };
   if constexpr (PER > 0) {
-    // Routed slot: the workgroup selects first; block (0, 0) also publishes
-    // the selection and counts it.
+    // Routed slot: the workgroup selects first. Workgroup (0, 0) publishes
+    // the selection and counts it after its own rows, so those stores never
+    // delay its weight loads.
     const RouteView& rv = p.rv;
     __shared__ Selection<PER> sel;
     if (j < rv.top_k) {
-      select_block<PER>(rv, t, sel, blockIdx.x == 0 && j == 0);
-      if (blockIdx.x == 0 && j == 0) publish_selection(rv, t, threadIdx.x, sel);
-      blob = pick_blob(rv, sel, j);
+      select_block<PER>(rv, t, sel, false);
+      rows(pick_blob(rv, sel, j));
+      if (blockIdx.x == 0 && j == 0) {
+        publish_selection(rv, t, threadIdx.x, sel);
+        if (threadIdx.x == 0) count_selection(rv, sel);
+      }
     } else {
-      blob = rv.shared_expert;
+      rows(rv.shared_expert);
     }
   } else {
-    blob = p.src.blob(t, j);
+    rows(p.src.blob(t, j));
   }
-  if (blob == nullptr) blob = p.rv.fallback;  // never dereference a null slot
-  // x is read with the weights, after the selection, so its slices are not
-  // held in registers through it; both loads are in flight together.
-  float xr[CPL][32];
-  gate_up_rows<META, CPL, ROWS>(p, t, j, blockIdx.x, blob, xr, [&](size_t i, float v) { p.h[i] = v; });
 }
 
 // ---------------------------------------------------------------------------
