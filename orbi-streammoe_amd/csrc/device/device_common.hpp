@@ -69,6 +69,54 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// DPP move of a double: both halves with the same control (0 where no
+// source lane, or outside the row mask).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u), CTRL, ROW_MASK, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), CTRL, ROW_MASK, 0xF, false);
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                        static_cast<uint32_t>(lo));
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v += dpp_d<kDppXor1>(v);
+  v += dpp_d<kDppXor2>(v);
+  v += dpp_d<kDppRowHalfMirror>(v);
+  v += dpp_d<kDppRowMirror>(v);
+  v += dpp_d<kDppRowBcast15, 0xA>(v);
+  v += dpp_d<kDppRowBcast31, 0xC>(v);
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 63));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), 63));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// A float and a double summed over the wavefront, the two reductions
+// interleaved; every lane gets both totals.
+__device__ __forceinline__ void wave_sum_fd(float& f, double& d) {
+  float a = f;
+  double b = d;
+  a += dpp<kDppXor1>(0.0f, a);
+  b += dpp_d<kDppXor1>(b);
+  a += dpp<kDppXor2>(0.0f, a);
+  b += dpp_d<kDppXor2>(b);
+  a += dpp<kDppRowHalfMirror>(0.0f, a);
+  b += dpp_d<kDppRowHalfMirror>(b);
+  a += dpp<kDppRowMirror>(0.0f, a);
+  b += dpp_d<kDppRowMirror>(b);
+  a += dpp<kDppRowBcast15, 0xA>(0.0f, a);
+  b += dpp_d<kDppRowBcast15, 0xA>(b);
+  a += dpp<kDppRowBcast31, 0xC>(0.0f, a);
+  b += dpp_d<kDppRowBcast31, 0xC>(b);
+  f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 63));
+  const uint64_t u = __builtin_bit_cast(uint64_t, b);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), 63));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), 63));
+  d = __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<kDppXor1>(v, v));
   v = fmaxf(v, dpp<kDppXor2>(v, v));

@@ -100,9 +100,8 @@ struct DownParams {
 
 
 // ---------------------------------------------------------------------------
-// Router elements as loaded. A wavefront of the router GEMV owns one router
-// row; lane l reads elements l*8 + 512u .. +8 (u = 0, 1, ...), kept as
-// loaded until the FMA.
+// Router elements as loaded, 8 at a time. A wavefront of the router GEMV
+// owns one router row (route_block), kept as loaded until the FMA.
 constexpr int kRouteWaves = 4;
 
 template <int RD>
@@ -834,13 +833,21 @@ __global__ __launch_bounds__(kSelThreads) void select_kernel(RouteView rv) {
 }
 
 // ---------------------------------------------------------------------------
-// Router GEMV. A wavefront owns one router row; lane l reads elements
-// l*8 + 512u .. +8 (u = 0, 1, ...), kept as loaded until the FMA.
+// Router GEMV. A wavefront owns one router row; lane l reads 32 consecutive
+// elements per pass of 2048 (route_block), kept as loaded until the FMA.
 
 // Token t's input, RMS-normalised when the flags ask for it
-// (reference_ops.cpp:96-128), into xs[D] in LDS; write_norm also stores it to
+// (reference_ops.cpp:96-128), into xs in LDS (column c at xs_index(c)); write_norm also stores it to
 // x_norm. Every workgroup that needs x normalises its own copy: the values
 // are the same bits everywhere. 256 threads, hidden <= 8192.
+// xs holds column c at xs_index(c): every 32 columns are followed by 4
+// unused floats, so lanes that read 32 consecutive columns each (16 bytes
+// at a time) spread over the LDS banks.
+__device__ __forceinline__ uint32_t xs_index(uint32_t c) { return c + (c / 32u) * 4u; }
+__host__ __device__ constexpr size_t route_lds_bytes(uint32_t hidden) {
+  return (static_cast<size_t>(hidden) + (hidden / 32u) * 4u) * sizeof(float);
+}
+
 __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, float* xs, bool write_norm) {
   __shared__ float red[kRouteWaves];
   const uint32_t D = a.geom.hidden;
@@ -879,13 +886,12 @@ __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, floa
       }
     }
   }
-  float4* xs4 = reinterpret_cast<float4*>(xs);
   float4* xn4 = reinterpret_cast<float4*>(a.x_norm + static_cast<size_t>(t) * D);
 #pragma unroll
   for (int u = 0; u < kX4PerThread; ++u) {
     const uint32_t i = tid + u * 256u;
     if (i < n4) {
-      xs4[i] = xv[u];
+      *reinterpret_cast<float4*>(xs + xs_index(4u * i)) = xv[u];
       if (write_norm) xn4[i] = xv[u];
     }
   }
@@ -894,12 +900,11 @@ __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, floa
 
 // Router rows blk*4 .. blk*4+3 of token t (row E is the shared-expert gate
 // vector): logits, or the sigmoid shared gate (reference_ops.cpp:214-216).
-// RCH loads of 8 elements per lane cover hidden <= 512 * RCH.
-// also(row, value) runs on lane 0 after each row's store (row E: the gate).
-
-// Router rows blk*4 .. blk*4+3 of token t (row E is the shared-expert gate
-// vector): logits, or the sigmoid shared gate (reference_ops.cpp:214-216).
-// RCH loads of 8 elements per lane cover hidden <= 512 * RCH.
+// A wavefront owns one row. Lane l covers columns 2048 v + 32 l .. +32 for
+// each pass v (RCH / 4 passes of four 8-element loads, hidden <= 512 RCH).
+// The dot product runs in fp64: every product of a router element (at most
+// 24 significant bits) and an fp32 input is exact there, and the sums'
+// rounding is far below fp32's.
 //
 // Each logit also gets its bound (when a.logit_bounds is set). With u =
 // 2^-24 and p_c = w_c x_c:
@@ -907,25 +912,28 @@ __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, floa
 //    product and sum, so its error is at most u (sum_c |p_c| + sum_c |S_c|),
 //    S_c its partial sums; |S_c| <= |P_c| + (a second-order term), P_c the
 //    exact prefix sums;
-//  - this kernel's sum (an FMA chain over each lane's 8-column chunk, the
-//    lane's chunks in order, then the wavefront tree) has error at most
-//    (8 + chunks per lane + 6) u sum_c |p_c|;
+//  - this kernel's logit is the fp64 sum rounded once to fp32: within
+//    u |l| of the exact sum, plus the fp64 sums' own error, below
+//    2^-40 sum_c |p_c|;
 //  - an RMS-normalised input differs from the reference's by a common factor
 //    (handled by the selection) and per element by at most 4 u.
-// sum_c |P_c| is taken over the chunks in column order: chunk (u, lane)
-// starts at the exclusive prefix of the chunk sums (a wavefront scan per u
-// plus the totals of the u before), and its 8 prefix sums are at most
-// 8 |start| + the sum of |its own partial sums|. The bound written is
-// (1 + 2^-9) u (sum |P_c| + (32 + chunks + n^2 u) sum |p_c|), n the width,
-// which the bound's own rounding leaves above the true one.
+// sum_c |P_c| over a lane's 32 columns of a pass is at most 32 |start| plus
+// the sum of |its own running sums|, start the exclusive prefix of the lane
+// totals (one wavefront scan per pass, plus the totals of the passes
+// before). The bound written is
+// (1 + 2^-9) u (sum |P_c| + (2 + 4 [RMSNorm] + n^2 u) sum |p_c| + |l|), n
+// the width; the slack covers the bound's own rounding and the fp32 running
+// sums it is computed from.
 template <int RD, int RCH>
 __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, uint32_t blk, float* xs) {
+  static_assert(RCH % 4 == 0, "four loads per pass");
   const uint32_t D = a.geom.hidden;
   const uint32_t E = a.expert_count;
   const uint32_t lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const uint32_t nrows = E + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
   const uint32_t row = blk * kRouteWaves + wave;
   constexpr size_t esz = (RD == OSM_META_F32) ? 4u : 2u;
+  auto col = [&](int u) { return static_cast<uint32_t>(u / 4) * 2048u + lane * 32u + static_cast<uint32_t>(u % 4) * 8u; };
   // The row is issued before x, so both are in flight together.
   Raw8<RD> w[RCH];
   if (row < nrows) {
@@ -933,66 +941,61 @@ __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, 
       const Q8Row qr = row < E ? q8_row(a.router, E, row, D, a.router_group)
                                : q8_row(a.shared_gate_vec, 1u, 0u, D, a.router_group);
 #pragma unroll
-      for (int u = 0; u < RCH; ++u) {
-        const uint32_t c = lane * 8u + u * 8u * kWave;
-        if (c < D) load_q8x8(qr, c, w[u]);
-      }
+      for (int u = 0; u < RCH; ++u)
+        if (col(u) < D) load_q8x8(qr, col(u), w[u]);
     } else {
       const uint8_t* wrow = row < E ? static_cast<const uint8_t*>(a.router) + static_cast<size_t>(row) * D * esz
                                     : static_cast<const uint8_t*>(a.shared_gate_vec);
 #pragma unroll
-      for (int u = 0; u < RCH; ++u) {
-        const uint32_t c = lane * 8u + u * 8u * kWave;
-        if (c < D) load_raw8<RD>(wrow, c, w[u]);
-      }
+      for (int u = 0; u < RCH; ++u)
+        if (col(u) < D) load_raw8<RD>(wrow, col(u), w[u]);
     }
   }
   stage_x(a, t, xs, blk == 0);
   if (row < nrows) {
     const bool bound = row < E && a.logit_bounds != nullptr;
-    float cs[RCH], qa[RCH];
-    float acc = 0.0f, aa = 0.0f;
+    float aa = 0.0f, rsum = 0.0f, carry = 0.0f;
+    double accd = 0.0;
 #pragma unroll
-    for (int u = 0; u < RCH; ++u) {
-      const uint32_t c = lane * 8u + u * 8u * kWave;
-      cs[u] = 0.0f;
-      qa[u] = 0.0f;
-      if (c < D) {
+    for (int v = 0; v < RCH / 4; ++v) {
+      if (static_cast<uint32_t>(v) * 2048u >= D) break;  // wavefront-uniform
+      double pd = 0.0;  // the lane's running sum over its columns of this pass
+      float qa = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = raw8_get<RD>(w[u], j), xv = xs[c + j];
-          cs[u] = fmaf(v, xv, cs[u]);
-          aa = fmaf(fabsf(v), fabsf(xv), aa);
-          qa[u] += fabsf(cs[u]);
+      for (int q = 0; q < 4; ++q) {
+        const int u = v * 4 + q;
+        const uint32_t c = col(u);
+        if (c < D) {
+          const float* xp = xs + xs_index(c);
+          const float st = static_cast<float>(pd);
+          double csd = 0.0;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float wv = raw8_get<RD>(w[u], j), xv = xp[j];
+            csd = fma(static_cast<double>(wv), static_cast<double>(xv), csd);
+            aa = fmaf(fabsf(wv), fabsf(xv), aa);
+            qa += fabsf(st + static_cast<float>(csd));
+          }
+          pd += csd;
         }
       }
-      acc += cs[u];
-    }
-    float rsum = 0.0f;
-    if (bound) {
-      float carry = 0.0f;
-#pragma unroll
-      for (int u = 0; u < RCH; ++u) {
-        if (u * 8u * kWave < D) {  // wavefront-uniform
-          const float incl = wave_incl_scan(cs[u]);
-          const uint32_t c = lane * 8u + u * 8u * kWave;
-          if (c < D) rsum += 8.0f * fabsf(carry + (incl - cs[u])) + qa[u];
-          carry += readlane_f(incl, 63);
-        }
+      if (bound) {
+        const float lf = static_cast<float>(pd);
+        const float incl = wave_incl_scan(lf);
+        rsum += 32.0f * fabsf(carry + (incl - lf)) + qa;
+        carry += readlane_f(incl, 63);
       }
-      rsum = wave_sum(rsum);
-      aa = wave_sum(aa);
+      accd += pd;
     }
-    acc = wave_sum(acc);
+    const float n = static_cast<float>(D);
+    const float c1 = ((a.flags & OSMD_MOE_RMSNORM) ? 6.0f : 2.0f) + n * n * 0x1p-24f;
+    float part = rsum + c1 * aa;
+    wave_sum_fd(part, accd);
+    const float acc = static_cast<float>(accd);
     if (lane == 0) {
       if (row < E) {
         a.logits[static_cast<size_t>(t) * E + row] = acc;
-        if (bound) {
-          const float n = static_cast<float>(D);
-          const float chunks = static_cast<float>((D + 8u * kWave - 1u) / (8u * kWave));
-          a.logit_bounds[static_cast<size_t>(t) * E + row] =
-              kBoundSlack * 0x1p-24f * (rsum + (32.0f + chunks + n * n * 0x1p-24f) * aa);
-        }
+        if (bound) a.logit_bounds[static_cast<size_t>(t) * E + row] = kBoundSlack * 0x1p-24f * (part + fabsf(acc));
       } else {
         a.shared_gate[t] = 1.0f / (1.0f + expf(-acc));
       }
@@ -1002,7 +1005,7 @@ __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, 
 
 template <int RD>
 __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
-  extern __shared__ __align__(16) float xs[];  // [D] normalised input of this token
+  extern __shared__ __align__(16) float xs[];  // normalised input of this token, at xs_index(column)
   route_block<RD, 16>(a, blockIdx.y, blockIdx.x, xs);
 }
 
@@ -1378,8 +1381,7 @@ template <int RD>
 int launch_route_rd(const osmd_moe_args& a, hipStream_t st) {
   const uint32_t nrows = a.expert_count + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
   const dim3 grid((nrows + kRouteWaves - 1) / kRouteWaves, a.tokens);
-  const size_t lds = static_cast<size_t>(a.geom.hidden) * sizeof(float);
-  route_kernel<RD><<<grid, 256, lds, st>>>(a);
+  route_kernel<RD><<<grid, 256, route_lds_bytes(a.geom.hidden), st>>>(a);
   return launch_status();
 }
 
