@@ -804,25 +804,25 @@ __device__ __forceinline__ const uint8_t* pick_blob(const RouteView& rv, const S
 // Writes the selection of token t: ids and weights in pick order, the
 // selected mass summed in pick order and the optional renormalisation
 // (qwen_router.cpp:72-91), and each slot's blob (shared expert last).
-// Threads tid <= k of the workgroup take part.
+// Lanes 0 .. k of wavefront 0 take part, one pick each; the mass is added in
+// pick order from their values.
 template <int PER>
 __device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t t, uint32_t tid,
                                                   const Selection<PER>& s) {
+  if (tid >= kWave) return;
   const uint32_t k = rv.top_k;
   const uint32_t nslot = k + rv.has_shared;
-  if (tid == 0) {
-    float mass = 0.0f;
-    for (uint32_t r = 0; r < k; ++r) mass = mass + s.p[r];
-    for (uint32_t r = 0; r < k; ++r) {
-      rv.ids[static_cast<size_t>(t) * k + r] = s.id[r];
-      rv.weights[static_cast<size_t>(t) * k + r] = rv.norm_topk_prob ? s.p[r] / mass : s.p[r];
-    }
-    rv.mass[t] = mass;
-  }
-  if (tid < k)
+  const float pr = tid < k ? s.p[tid] : 0.0f;
+  float mass = 0.0f;
+  for (uint32_t r = 0; r < k; ++r) mass = mass + readlane_f(pr, static_cast<int>(r));
+  if (tid < k) {
+    rv.ids[static_cast<size_t>(t) * k + tid] = s.id[tid];
+    rv.weights[static_cast<size_t>(t) * k + tid] = rv.norm_topk_prob ? pr / mass : pr;
     rv.slot_ptrs[static_cast<size_t>(t) * nslot + tid] = pick_blob(rv, s, tid);
-  else if (tid == k && nslot > k)
+  } else if (tid == k && nslot > k) {
     rv.slot_ptrs[static_cast<size_t>(t) * nslot + k] = rv.shared_expert;
+  }
+  if (tid == 0) rv.mass[t] = mass;
 }
 
 template <int PER>
@@ -1177,7 +1177,9 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   const uint32_t lane = tid % kWave;
   const uint32_t wave = tid / kWave;
   const uint32_t rg = wave & 1u;    // row group
-  const uint32_t half = wave >> 1;  // slots half, half + 2, ...
+  // Slots half, half + 2, ...: wavefront-uniform, so the slot pointers and
+  // weights below are scalar loads issued together.
+  const uint32_t half = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(wave >> 1)));
   const uint32_t c = lane % LPR;
   const uint32_t row_local = rg * kRowsPerGroup + lane / LPR;
   const uint32_t row = blk * kRowsPerBlock + row_local;
@@ -1201,20 +1203,27 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   };
   load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
 
-  // This wavefront's slots: pointers and weights (uniform loads), then the
-  // packed chunk and metadata of each, with no branch between them. Slots
-  // past nslot and null pointers read a valid blob with weight 0.
+  // This wavefront's slots: lane l loads slot l's pointer and weight (vector
+  // loads, in flight with h's), each slot's are then read from its lane, and
+  // the packed chunk and metadata of each are loaded with no branch between
+  // them. Slots past nslot and null pointers read a valid blob with weight 0.
+  const uint32_t ls = lane < nslot ? lane : 0u;
+  const uint8_t* lp = p.src.blob(t, ls);
+  // Per-lane addresses (a routing weight, or the shared gate): one vector load.
+  const float* wsrc = ls < p.top_k ? (p.weights ? p.weights + static_cast<size_t>(t) * p.top_k + ls : nullptr)
+                                   : (p.shared_gate ? p.shared_gate + t : nullptr);
+  const float lw = wsrc ? ldg<float>(wsrc) : 1.0f;
   const uint8_t* bp[kSlotsPerWave];
   float w[kSlotsPerWave];
 #pragma unroll
   for (int i = 0; i < kSlotsPerWave; ++i) {
     const uint32_t j = half + 2u * i;
-    const uint32_t js = j < nslot ? j : 0u;
-    bp[i] = p.src.blob(t, js);
-    if (js < p.top_k)
-      w[i] = p.weights ? p.weights[static_cast<size_t>(t) * p.top_k + js] : 1.0f;
-    else
-      w[i] = p.shared_gate ? p.shared_gate[t] : 1.0f;
+    const int src = static_cast<int>(j < nslot ? j : 0u);
+    const uint64_t pv = reinterpret_cast<uint64_t>(lp);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pv), src));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pv >> 32), src));
+    bp[i] = reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+    w[i] = readlane_f(lw, src);
     if (j >= nslot || bp[i] == nullptr) w[i] = 0.0f;
     if (bp[i] == nullptr) bp[i] = p.fallback;
   }
@@ -1230,8 +1239,10 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   }
 
   // Stage h and its per-chunk sums: 8 consecutive threads hold one 32-float
-  // chunk, summed with DPP within the lane group.
-  for (uint32_t pass = 0;; ++pass) {
+  // chunk, summed with DPP within the lane group. The first batch is staged
+  // while the weights are in flight (only its own loads are waited for);
+  // h of more than kH4PerThread * 1024 floats takes further passes.
+  auto stage = [&](uint32_t pass) {
 #pragma unroll
     for (int u = 0; u < kH4PerThread; ++u) {
       const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
@@ -1242,8 +1253,11 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
         if ((tid & 7u) == 0u) hsum[chunk] = s4;
       }
     }
-    if ((pass + 1) * kH4PerThread * kDownThreads >= n4) break;
-    load_h(pass + 1);
+  };
+  stage(0);
+  for (uint32_t pass = 1; pass * kH4PerThread * kDownThreads < n4; ++pass) {
+    load_h(pass);
+    stage(pass);
   }
   __syncthreads();
 
