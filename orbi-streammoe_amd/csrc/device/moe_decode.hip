@@ -290,10 +290,10 @@ __device__ __forceinline__ void sort_lane(uint32_t* k, uint32_t* n) {
 }
 
 // acc + v[0] + v[1] + ... + v[n-1] in order, each addition rounded to fp32,
-// v in LDS (16-byte aligned), n a multiple of 8. Runs of 256 are
-// straight-line code of 16-byte reads, which the compiler issues well ahead
-// of the additions, so the chain of additions, which cannot be shortened, is
-// what is waited on; the rest goes 8 at a time.
+// v in LDS (16-byte aligned), n a multiple of 8 and the same in every lane.
+// Values go through two register batches of 32: the next batch's reads are
+// issued before the current batch's additions, so the chain of additions,
+// which cannot be shortened, is what is waited on.
 __device__ __forceinline__ float chain_add4(float4 q, float acc) {
 #pragma clang fp contract(off)
   acc = acc + q.x;
@@ -302,14 +302,32 @@ __device__ __forceinline__ float chain_add4(float4 q, float acc) {
   acc = acc + q.w;
   return acc;
 }
+constexpr int kChainBatch = 8;  // float4 per batch
+__device__ __forceinline__ void chain_load(const float4* p, float4 (&r)[kChainBatch]) {
+#pragma unroll
+  for (int j = 0; j < kChainBatch; ++j) r[j] = p[j];
+}
+__device__ __forceinline__ float chain_batch(const float4 (&r)[kChainBatch], float acc) {
+#pragma unroll
+  for (int j = 0; j < kChainBatch; ++j) acc = chain_add4(r[j], acc);
+  return acc;
+}
 __device__ __forceinline__ float chain_sum(const float* v, uint32_t n, float acc) {
   const float4* v4 = reinterpret_cast<const float4*>(v);
-  uint32_t i = 0;
-  for (; i + 256u <= n; i += 256u) {
-#pragma unroll
-    for (uint32_t j = 0; j < 64u; ++j) acc = chain_add4(v4[i / 4u + j], acc);
+  const uint32_t nb = n / (4u * kChainBatch);
+  float4 a[kChainBatch], b[kChainBatch];
+  if (nb > 0u) chain_load(v4, a);
+  for (uint32_t k = 0; k < nb; k += 2u) {
+    const bool b_used = k + 1u < nb;
+    if (b_used) chain_load(v4 + (k + 1u) * kChainBatch, b);
+    __builtin_amdgcn_sched_barrier(0);
+    acc = chain_batch(a, acc);
+    if (!b_used) break;
+    if (k + 2u < nb) chain_load(v4 + (k + 2u) * kChainBatch, a);
+    __builtin_amdgcn_sched_barrier(0);
+    acc = chain_batch(b, acc);
   }
-  for (; i < n; i += 8u) {
+  for (uint32_t i = nb * 4u * kChainBatch; i < n; i += 8u) {
     acc = chain_add4(v4[i / 4u], acc);
     acc = chain_add4(v4[i / 4u + 1u], acc);
   }
