@@ -1,6 +1,7 @@
 // moe.cpp -- routed-MoE layer state and decode (the HIP counterparts of
 // src/model/checkpoint_sparse_moe.cpp, checkpoint_moe_sublayer.cpp and
 // routed_moe.cpp:254-430).
+#include <array>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -56,36 +57,48 @@ struct HipMoeLayer::Impl {
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
   PinnedBytes host_io;    // cache-driven path: pinned staging of inputs and outputs (grown on use)
   DeviceBytes dev_io;     // its device mirror: one copy in, one copy out per call
-  // grouped (multi-token) path: allocated on its first use
+  // grouped (multi-token) path: carved per call from the context's shared
+  // workspace (every layer on one stream uses the same memory in turn)
   HipMoePath path = HipMoePath::automatic;
-  bool grouped_ready = false;
-  DeviceBytes g_x_terms, g_x_sums, g_pair_pos, g_pair_w, g_tiles, g_tile_count, g_gu_part, g_h_terms,
-      g_h_sums, g_partial, g_logit_planes, g_x_norms, g_bound_planes;
+  enum GroupedBuf { kXTerms, kXSums, kPairPos, kPairW, kTiles, kTileCount, kGuPart, kHTerms, kHSums, kPartial,
+                    kLogitPlanes, kXNorms, kBoundPlanes, kGroupedBufs };
+  std::array<std::size_t, kGroupedBufs> g_off{};
+  std::size_t g_bytes = 0;
+  std::uint8_t* g_base = nullptr;
 
-  int ensure_grouped(osmd_stream st) {
-    if (grouped_ready) return 0;
+  void plan_grouped() {
     const osm_expert_geometry& g = cfg.geometry;
     const std::size_t T = max_tokens, D = g.hidden, I = g.inter, G = g.group;
     const std::size_t P = T * nslot();
     const std::size_t tiles = osmd_moe_grouped_max_tiles(max_tokens, nslot(), cfg.expert_count);
-    int rc = g_x_terms.allocate(T * 3U * D * 2U);
-    if (rc == 0) rc = g_x_sums.allocate(T * (D / G) * 4U);
-    if (rc == 0) rc = g_pair_pos.allocate(P * 4U);
-    if (rc == 0) rc = g_pair_w.allocate(P * 4U);
-    if (rc == 0) rc = g_tiles.allocate(tiles * 80U);
-    if (rc == 0) rc = g_tile_count.allocate(4U);
-    if (rc == 0) rc = g_gu_part.allocate(osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(D)) * 2U * P * I * 4U);
-    if (rc == 0) rc = g_h_terms.allocate(P * 2U * I * 2U);
-    if (rc == 0) rc = g_h_sums.allocate(P * (I / G) * 4U);
-    if (rc == 0) rc = g_partial.allocate(osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(I)) * P * D * 4U);
     const std::size_t parts = osmd_moe_grouped_router_parts(static_cast<std::uint32_t>(D));
-    if (rc == 0) rc = g_logit_planes.allocate(parts * T * (cfg.expert_count + 1U) * 4U);
-    if (rc == 0) rc = g_x_norms.allocate(T * (D / 32U) * 4U);
-    if (rc == 0) rc = g_bound_planes.allocate(parts * 2U * T * (cfg.expert_count + 1U) * 4U);
-    if (rc == 0) rc = osmd_zero(g_tile_count.get(), 4U, st);
-    if (rc == 0) grouped_ready = true;
-    return rc;
+    const std::array<std::size_t, kGroupedBufs> bytes = {
+        T * 3U * D * 2U,                                                            // x terms
+        T * (D / G) * 4U,                                                           // x group sums
+        P * 4U, P * 4U,                                                             // pair positions, weights
+        tiles * 80U, 4U,                                                            // tiles + rows, tile count
+        osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(D)) * 2U * P * I * 4U,  // gate/up partials
+        P * 2U * I * 2U, P * (I / G) * 4U,                                          // h terms, h sums
+        osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(I)) * P * D * 4U,   // down partials
+        parts * T * (cfg.expert_count + 1U) * 4U,                                   // logit planes
+        T * (D / 32U) * 4U,                                                         // input chunk norms
+        parts * 2U * T * (cfg.expert_count + 1U) * 4U};                             // bound planes
+    std::size_t off = 0;
+    for (std::size_t i = 0; i < bytes.size(); ++i) {
+      g_off[i] = off;
+      off += (bytes[i] + 255U) & ~static_cast<std::size_t>(255U);
+    }
+    g_bytes = off;
   }
+
+  int ensure_grouped(HipComputeContext& context) {
+    if (g_bytes == 0) plan_grouped();
+    int rc = 0;
+    g_base = static_cast<std::uint8_t*>(context.shared_workspace(g_bytes, &rc));
+    return g_base != nullptr ? 0 : (rc != 0 ? rc : 1);
+  }
+  template <typename T>
+  T* gbuf(GroupedBuf b) const { return reinterpret_cast<T*>(g_base + g_off[b]); }
 
   // Whether a decode of `tokens` rows of x goes through the grouped GEMMs.
   bool grouped_ok(const void* x) const {
@@ -103,20 +116,20 @@ struct HipMoeLayer::Impl {
     osmd_moe_grouped_args ga{};
     ga.moe = a;
     ga.x_bf16 = x_bf16 ? 1U : 0U;
-    ga.x_terms = g_x_terms.as<std::uint16_t>();
-    ga.x_sums = g_x_sums.as<float>();
-    ga.pair_pos = g_pair_pos.as<std::uint32_t>();
-    ga.pair_w = g_pair_w.as<float>();
-    ga.tiles = g_tiles.get();
-    ga.tile_count = g_tile_count.as<std::uint32_t>();
-    ga.gu_part = g_gu_part.as<float>();
-    ga.h_terms = g_h_terms.as<std::uint16_t>();
-    ga.h_sums = g_h_sums.as<float>();
-    ga.partial = g_partial.as<float>();
-    ga.logit_planes = g_logit_planes.as<float>();
+    ga.x_terms = gbuf<std::uint16_t>(kXTerms);
+    ga.x_sums = gbuf<float>(kXSums);
+    ga.pair_pos = gbuf<std::uint32_t>(kPairPos);
+    ga.pair_w = gbuf<float>(kPairW);
+    ga.tiles = gbuf<void>(kTiles);
+    ga.tile_count = gbuf<std::uint32_t>(kTileCount);
+    ga.gu_part = gbuf<float>(kGuPart);
+    ga.h_terms = gbuf<std::uint16_t>(kHTerms);
+    ga.h_sums = gbuf<float>(kHSums);
+    ga.partial = gbuf<float>(kPartial);
+    ga.logit_planes = gbuf<float>(kLogitPlanes);
     ga.router_norms = router_norms.as<const float>();
-    ga.x_norms = g_x_norms.as<float>();
-    ga.bound_planes = g_bound_planes.as<float>();
+    ga.x_norms = gbuf<float>(kXNorms);
+    ga.bound_planes = gbuf<float>(kBoundPlanes);
     return ga;
   }
 
@@ -368,7 +381,7 @@ HipDispatchResult HipMoeLayer::decode_device(HipComputeContext& context, const f
       r.diagnostic = "grouped MoE needs group 32, 64 or 128, hidden and intermediate multiples of 128, and a 16-byte aligned input";
       return r;
     }
-    rc = impl_->ensure_grouped(context.stream());
+    rc = impl_->ensure_grouped(context);
     if (rc == 0) {
       const osmd_moe_grouped_args ga = impl_->grouped_args(a, false);
       rc = osmd_moe_grouped(&ga, context.stream());
@@ -488,7 +501,7 @@ HipDispatchResult HipMoeLayer::prefill_device_bf16(HipComputeContext& context, c
     r.diagnostic = "grouped MoE needs group 32, 64 or 128, hidden and intermediate multiples of 128, and a 16-byte aligned input";
     return r;
   }
-  int rc = impl_->ensure_grouped(context.stream());
+  int rc = impl_->ensure_grouped(context);
   if (rc == 0) {
     osmd_moe_args a = impl_->args(nullptr, y, tokens, expert_table, false);
     a.x = reinterpret_cast<const float*>(x_bf16);  // read as bf16 (x_bf16 = 1)

@@ -102,6 +102,13 @@ class HipComputeContext {
   // Makes this context's device current on the calling thread.
   [[nodiscard]] bool activate(std::string* diagnostic = nullptr) const noexcept;
   [[nodiscard]] bool synchronize(std::string* diagnostic = nullptr) const noexcept;
+  // Device workspace of at least `bytes`, shared by every layer that runs on
+  // this context's stream (the grouped path's buffers): one layer's work
+  // finishes on the stream before the next layer's starts, so they never
+  // overlap. It grows and never shrinks; an outgrown buffer stays allocated
+  // until the context ends, so that graphs captured over it stay valid.
+  // Returns nullptr (and the HIP error in *rc) when the allocation fails.
+  [[nodiscard]] void* shared_workspace(std::size_t bytes, int* rc) noexcept;
 
  private:
   struct Impl;

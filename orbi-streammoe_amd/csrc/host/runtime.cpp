@@ -3,6 +3,7 @@
 // vulkan_float_buffer.cpp).
 #include <cstring>
 #include <string>
+#include <vector>
 #include <utility>
 
 #include "host_util.hpp"
@@ -73,12 +74,39 @@ struct HipComputeContext::Impl {
   std::string name;
   osmd_stream stream = nullptr;
   osmd_stream copy = nullptr;
+  DeviceBytes workspace;
+  std::vector<DeviceBytes> outgrown;  // kept for graphs captured over them
   ~Impl() {
+    outgrown.clear();
+    workspace.reset();
     if (device >= 0) osmd_set_device(device);
     if (copy) osmd_stream_destroy(copy);
     if (stream) osmd_stream_destroy(stream);
   }
 };
+
+void* HipComputeContext::shared_workspace(std::size_t bytes, int* rc) noexcept {
+  if (rc) *rc = 0;
+  if (!impl_) {
+    if (rc) *rc = 1;
+    return nullptr;
+  }
+  if (impl_->workspace.get() != nullptr && impl_->workspace.size() >= bytes) return impl_->workspace.get();
+  try {
+    DeviceBytes grown;
+    const int r = grown.allocate(bytes);
+    if (r != 0) {
+      if (rc) *rc = r;
+      return nullptr;
+    }
+    if (impl_->workspace.get() != nullptr) impl_->outgrown.push_back(std::move(impl_->workspace));
+    impl_->workspace = std::move(grown);
+    return impl_->workspace.get();
+  } catch (...) {
+    if (rc) *rc = 2;
+    return nullptr;
+  }
+}
 
 HipComputeContext::HipComputeContext() = default;
 HipComputeContext::~HipComputeContext() = default;
