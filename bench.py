@@ -22,6 +22,7 @@ import argparse
 import ctypes
 import json
 import os
+import re
 import sys
 import time
 
@@ -55,6 +56,9 @@ def parse():
                     help="HBM cap of the expert cache in the capped-cache decode (GB)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the decode-batch, prefill and capped-cache measurements")
+    ap.add_argument("--grouped-only", action="store_true",
+                    help="no benchmark line: only the 512-token prefill chunk and the 64-token grouped decode "
+                         "over --layers layer copies (for profiling the grouped kernels)")
     ap.add_argument("--counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no benchmark: summarise two rocprofv3 --pmc counter_collection.csv files "
                          "(FETCH_SIZE, WRITE_SIZE) of a run with --copy-probe-mb into HBM bytes per dispatch")
@@ -141,7 +145,16 @@ def summarize_counters(fetch_csv, write_csv, probe_mb):
     ff, fw = probe_kib / f_probe, probe_kib / w_probe
     out = {"probe_bytes": probe_mb << 20, "probe_fetch_kib": f_probe, "probe_write_kib": w_probe,
            "fetch_scale": round(ff, 4), "write_scale": round(fw, 4), "kernels": {}}
-    for short in ("route_kernel", "gate_up_kernel", "down_kernel"):
+    shorts = ["route_kernel", "gate_up_kernel", "down_kernel"]
+    # The grouped path's kernels by instantiation (gate/up is split_kernel<., 2, ...>, down <., 1, ...>).
+    for (name, _g) in fetch:
+        m = re.search(r"::(\w+_kernel)(<[^(]*>)?\(", name)
+        if m and m.group(1) not in ("route_kernel", "gate_up_kernel", "down_kernel", "copy16_kernel") \
+                and not m.group(1).startswith("synth") and m.group(1) != "zero_kernel":
+            key = m.group(1) + (m.group(2) or "")
+            if key not in shorts:
+                shorts.append(key)
+    for short in shorts:
         keys = [k for k in fetch if short in k[0]]
         if not keys:
             continue
@@ -236,6 +249,30 @@ def prefill(ctx, moes, slab, args, layers=8):
            "algorithmic_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
            "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
     log(f"[bench] prefill: {json.dumps(res)}")
+    return res
+
+
+def grouped_decode(ctx, moes, slab, args, T, layers=8):
+    """T fp32 tokens per layer step through the grouped MFMA path (config 2's
+    largest batch), one fresh batch per layer copy."""
+    steps = max(3, args.steps // 20)
+    xs = [ctx.alloc(T * D * 4) for _ in range(layers)]
+    for l in range(layers):
+        osm_hip.synth_tokens_device(ctx, args.seed, 600000 + l * T, T, D, xs[l].ptr)
+    y = ctx.alloc(T * D * 4)
+    for m in moes[:layers]:
+        m.set_path(osm_hip.PATH_GROUPED)
+
+    def step(_i):
+        for l in range(layers):
+            moes[l].decode_device(slab, l, xs[l].ptr, y.ptr, T)
+
+    step(0)
+    ms = time_steps(ctx, steps, step)
+    for m in moes[:layers]:
+        m.set_path(osm_hip.PATH_AUTO)
+    res = {"tokens": T, "layer_copies": layers, "us_per_layer_step": round(ms / steps * 1000.0 / layers, 1)}
+    log(f"[bench] grouped decode: {json.dumps(res)}")
     return res
 
 
@@ -412,6 +449,12 @@ def main():
     t0 = time.time()
     g, slab, moes = build_model(ctx, L, args.seed)
     log(f"[bench] model ready: {L} layers x {E} experts ({slab.stride * E * L / 1e9:.1f} GB) in {time.time() - t0:.1f}s on {ctx.device_name}")
+    if args.grouped_only:
+        pf = prefill(ctx, moes, slab, args, layers=min(L, 8))
+        b64 = grouped_decode(ctx, moes, slab, args, 64, layers=min(L, 8))
+        print(json.dumps({"prefill": pf, "grouped_decode_64": b64}), flush=True)
+        copy_probe(ctx, args)
+        return
 
     steps, warm = args.steps, args.warmup
     tok_bytes = D * 4
@@ -558,6 +601,10 @@ def main():
     result.update(extras)
     print(json.dumps(result), flush=True)
 
+    copy_probe(ctx, args)
+
+
+def copy_probe(ctx, args):
     if args.copy_probe_mb > 0:
         n = args.copy_probe_mb << 20
         src, dst = ctx.alloc(n), ctx.alloc(n)
