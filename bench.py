@@ -351,7 +351,7 @@ def capped_cache_decode(ctx, g, moes, args, steps=64, warm=8, repeat_p=0.6):
            "misses_per_token_layer": round((st1["misses"] - st0["misses"]) / n, 3),
            "evictions": st1["evictions"] - st0["evictions"],
            "fill_GBps": round((b1 - b0) / dt / 1e9, 2),
-           "host_path": "one native call per token for the 48-layer stack; per layer: the picks made resident (misses filled on two side streams while the router runs), expert kernels, output read back"}
+           "host_path": "one native call per token for the 48-layer stack, enqueued without host waits: activations stay on the device, each layer's misses are filled on two side streams that wait only for the kernels that last read the slots they overwrite (so fills overlap earlier layers' kernels), y read back once"}
     log(f"[bench] capped cache: {json.dumps(res)}")
     del cache, store
     return res

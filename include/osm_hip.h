@@ -325,7 +325,11 @@ int osm_moe_layer_routing_stats(osm_context ctx, osm_moe_layer l, uint32_t out[4
  * sublayer (RMSNorm, MoE, residual), on the previous layer's output; x and
  * y are host [tokens, D]. pick_ids / pick_weights (both or neither):
  * [n_layers][tokens][k] routed picks given from outside, as
- * osm_moe_layer_run_cached_picks takes them; NULL routes on the device. */
+ * osm_moe_layer_run_cached_picks takes them; NULL routes on the device.
+ * With picks given the whole stack is enqueued without a host wait: the
+ * activations stay on the device, and each layer's fills wait only for the
+ * kernels that last read the slots they overwrite, so they overlap the
+ * layers before. Outputs are the bits of the layer-by-layer calls. */
 int osm_moe_run_cached_layers(osm_context ctx, const osm_moe_layer* layers, const uint32_t* cache_layers,
                               uint32_t n_layers, osm_expert_cache cache, const float* x, uint32_t tokens,
                               const uint32_t* pick_ids, const float* pick_weights, float* y);

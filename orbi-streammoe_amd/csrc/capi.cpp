@@ -623,6 +623,21 @@ int osm_moe_run_cached_layers(osm_context ctx, const osm_moe_layer* layers, cons
       (!pick_ids) != (!pick_weights))
     return fail(OSM_E_INVALID, "invalid arguments");
   const std::size_t D = layers[0] ? layers[0]->layer.config().geometry.hidden : 0;
+  if (pick_ids) {
+    // Routing given: the whole stack is enqueued at once (activations on the
+    // device, fills overlapping earlier layers' kernels).
+    std::vector<osm::HipMoeLayer*> ls(n_layers);
+    for (uint32_t i = 0; i < n_layers; ++i) {
+      if (!layers[i]) return fail(OSM_E_INVALID, "null layer");
+      ls[i] = &layers[i]->layer;
+    }
+    std::string d;
+    if (!osm::run_cached_stack_picks(ctx->ctx, *cache->cache, ls, cache_layers,
+                                     std::span<const float>(x, static_cast<std::size_t>(tokens) * D), pick_ids,
+                                     pick_weights, y, &d))
+      return fail(OSM_E_INVALID, d);
+    return ok();
+  }
   std::vector<float> cur(x, x + static_cast<std::size_t>(tokens) * D);
   for (uint32_t i = 0; i < n_layers; ++i) {
     if (!layers[i] || layers[i]->layer.config().geometry.hidden != D)

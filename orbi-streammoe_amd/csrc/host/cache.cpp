@@ -296,6 +296,10 @@ struct HipResidentExpertCache::Impl {
   // evicted and refilled within one batch is written again on the same
   // stream, so its two copies land in order.
   std::vector<std::pair<std::size_t, osmd_stream>> batch_slots;
+  // Pipelined use: per slot, the event after its last readers (null: none
+  // pending).
+  bool pipelined = false;
+  std::vector<osmd_event> slot_reader;
 
   Impl(HipComputeContext& c, ExpertBlobSource& s, std::size_t budget)
       : ctx(c), source(s), policy(budget) {}
@@ -371,7 +375,7 @@ HipResidentExpert* HipResidentExpertCache::get(std::uint32_t layer, std::uint32_
     // stream between the gets, so the first copy's wait covers them all and
     // end_fills makes the compute stream wait once for the last copy.
     int rc = 0;
-    if (!m.batching || !m.batch_waited) {
+    if (!m.pipelined && (!m.batching || !m.batch_waited)) {
       rc = osmd_event_record(m.reuse_ev, m.ctx.stream());
       if (rc == 0) rc = osmd_stream_wait_event(m.ctx.copy_stream(), m.reuse_ev);
       if (rc == 0 && m.batching) rc = osmd_stream_wait_event(m.copy2, m.reuse_ev);
@@ -382,6 +386,11 @@ HipResidentExpert* HipResidentExpertCache::get(std::uint32_t layer, std::uint32_
       for (const auto& [bs, bst] : m.batch_slots)
         if (bs == slot) cs = bst;
       m.batch_slots.emplace_back(slot, cs);
+    }
+    if (m.pipelined && rc == 0 && slot < m.slot_reader.size() && m.slot_reader[slot] != nullptr) {
+      // Only the slot's last readers must be done before it is overwritten.
+      rc = osmd_stream_wait_event(cs, m.slot_reader[slot]);
+      m.slot_reader[slot] = nullptr;
     }
     if (rc == 0) rc = osmd_memcpy_h2d(dst, src, m.stride, cs);
     if (rc == 0 && !m.batching) {
@@ -437,6 +446,27 @@ int HipResidentExpertCache::end_fills() noexcept {
   m.batch_waited = false;
   m.batch_fills = 0;
   return rc;
+}
+
+void HipResidentExpertCache::begin_pipeline() noexcept {
+  // Work enqueued before the pipeline may read any slot: every slot starts
+  // with one event after it (a refill waits for it; once the stack's own
+  // layers read the slot, for theirs instead).
+  Impl& m = *impl_;
+  osmd_event start = nullptr;
+  if (m.ctx.activate() && osmd_event_record(m.reuse_ev, m.ctx.stream()) == 0) start = m.reuse_ev;
+  m.pipelined = true;
+  m.slot_reader.assign(m.nslots, start);
+}
+
+void HipResidentExpertCache::mark_readers(std::uint32_t layer, std::uint32_t expert, osmd_event done) noexcept {
+  const auto it = impl_->key_slot.find(LfuRecencyPolicy::make_key(layer, expert));
+  if (it != impl_->key_slot.end() && it->second < impl_->slot_reader.size()) impl_->slot_reader[it->second] = done;
+}
+
+void HipResidentExpertCache::end_pipeline() noexcept {
+  impl_->pipelined = false;
+  impl_->slot_reader.assign(impl_->slot_reader.size(), nullptr);
 }
 
 HipValuesResult HipResidentExpertCache::run(std::uint32_t layer, std::uint32_t expert,

@@ -1,6 +1,7 @@
 // moe.cpp -- routed-MoE layer state and decode (the HIP counterparts of
 // src/model/checkpoint_sparse_moe.cpp, checkpoint_moe_sublayer.cpp and
 // routed_moe.cpp:254-430).
+#include <algorithm>
 #include <array>
 #include <cmath>
 #include <cstring>
@@ -675,6 +676,161 @@ HipMoeResult HipMoeLayer::run(HipComputeContext& context, std::span<const float>
 struct MoeLayerAccess {
   static HipMoeLayer::Impl* impl(HipMoeLayer& l) { return l.impl_.get(); }
 };
+
+bool run_cached_stack_picks(HipComputeContext& context, HipResidentExpertCache& cache,
+                            std::span<HipMoeLayer* const> layers, const std::uint32_t* cache_layers,
+                            std::span<const float> x, const std::uint32_t* pick_ids, const float* pick_weights,
+                            float* y, std::string* diagnostic) noexcept {
+  auto fail = [&](std::string d) {
+    if (diagnostic) *diagnostic = std::move(d);
+    return false;
+  };
+  std::vector<osmd_event> done;
+  bool pipelined = false;
+  auto cleanup = [&]() {
+    if (pipelined) {
+      (void)osmd_stream_synchronize(context.stream());
+      cache.end_pipeline();
+      pipelined = false;
+    }
+    for (osmd_event e : done)
+      if (e != nullptr) osmd_event_destroy(e);
+    done.clear();
+  };
+  try {
+    const std::size_t n = layers.size();
+    if (n == 0 || cache_layers == nullptr || pick_ids == nullptr || pick_weights == nullptr || y == nullptr)
+      return fail("invalid arguments");
+    auto* m0 = layers[0] ? MoeLayerAccess::impl(*layers[0]) : nullptr;
+    if (m0 == nullptr || !layers[0]->valid()) return fail("layer 0: MoE layer is not valid");
+    const std::size_t D = m0->cfg.geometry.hidden, K = m0->cfg.top_k;
+    const std::uint32_t tokens = static_cast<std::uint32_t>(x.size() / (D ? D : 1));
+    if (tokens == 0 || x.size() != tokens * D) return fail("qwen router: hidden vector size mismatch");
+    if (!all_finite(x)) return fail("qwen router: hidden vector contains non-finite value");
+    std::size_t E_max = 0, nslot_max = 0;
+    for (std::size_t i = 0; i < n; ++i) {
+      auto* m = layers[i] ? MoeLayerAccess::impl(*layers[i]) : nullptr;
+      const std::string at = "layer " + std::to_string(i) + ": ";
+      if (m == nullptr || !layers[i]->valid()) return fail(at + "MoE layer is not valid");
+      if (m->cfg.geometry.hidden != D) return fail("layers must share one hidden size");
+      if (m->cfg.top_k != K) return fail("given picks need one top_k");
+      if (tokens > m->max_tokens) return fail(at + "qwen router: hidden vector size mismatch");
+      if (m->norm_weight.get() == nullptr) return fail(at + "MoE sublayer decode needs an RMSNorm weight");
+      for (std::size_t j = 0; j < tokens * K; ++j) {
+        const std::size_t o = i * tokens * K + j;
+        if (pick_ids[o] >= m->cfg.expert_count)
+          return fail(at + "routed MoE pick " + std::to_string(pick_ids[o]) + " is out of range");
+        if (!std::isfinite(pick_weights[o])) return fail(at + "routed MoE encountered a non-finite routing weight");
+      }
+      E_max = std::max<std::size_t>(E_max, m->cfg.expert_count);
+      nslot_max = std::max<std::size_t>(nslot_max, m->nslot());
+    }
+    if (!context.activate(diagnostic)) return false;
+    const osmd_stream st = context.stream();
+
+    // Device block: two activation buffers (layer outputs alternate), every
+    // layer's pick weights and slot pointers, and the routing outputs one
+    // layer at a time. Pinned host mirror: x and the weights in, the slot
+    // pointers layer by layer, y out.
+    auto al = [](std::size_t v) { return (v + 255U) & ~static_cast<std::size_t>(255U); };
+    const std::size_t xb = x.size_bytes(), wb = n * tokens * K * 4U, pb = n * tokens * nslot_max * sizeof(void*);
+    const std::size_t o_a = 0, o_b = al(xb), o_w = o_b + al(xb), o_p = o_w + al(wb), o_norm = o_p + al(pb),
+                      o_lg = o_norm + al(xb), o_mass = o_lg + al(tokens * E_max * 4U), o_gate = o_mass + al(tokens * 4U),
+                      o_rid = o_gate + al(tokens * 4U), o_rw = o_rid + al(tokens * K * 4U),
+                      total = o_rw + al(tokens * K * 4U);
+    DeviceBytes dev;
+    PinnedBytes host;
+    int rc = dev.allocate(total);
+    if (rc == 0) rc = host.allocate(total);
+    if (rc != 0) return fail(hip_error("cached stack: staging allocation failed", rc));
+    auto* h = static_cast<std::uint8_t*>(host.get());
+    auto* d = dev.as<std::uint8_t>();
+    std::memcpy(h + o_a, x.data(), xb);
+    std::memcpy(h + o_w, pick_weights, wb);
+    rc = osmd_copy_d2d(d, h, o_p, st);  // x and every layer's weights
+    if (rc != 0) return fail(hip_error("cached stack: input copy failed", rc));
+    done.assign(n, nullptr);
+    for (std::size_t i = 0; i < n && rc == 0; ++i) rc = osmd_event_create(&done[i]);
+    if (rc != 0) return fail(hip_error("cached stack: event creation failed", rc));
+
+    cache.begin_pipeline();
+    pipelined = true;
+    for (std::size_t i = 0; i < n; ++i) {
+      auto* m = MoeLayerAccess::impl(*layers[i]);
+      const std::uint32_t nslot = m->nslot();
+      const std::uint32_t* ids = pick_ids + i * tokens * K;
+      const std::uint32_t cl = cache_layers[i];
+      float* cur = reinterpret_cast<float*>(d + (i % 2 == 0 ? o_a : o_b));
+      float* nxt = reinterpret_cast<float*>(d + (i % 2 == 0 ? o_b : o_a));
+      // Every pick resident (in pick order), the misses copied on the side
+      // streams; then every pick's slot from the final residency.
+      cache.begin_fills();
+      for (std::uint32_t t = 0; t < tokens; ++t)
+        for (std::size_t j = 0; j < K; ++j) {
+          std::string gd;
+          HipResidentExpert* e = cache.get(cl, ids[t * K + j], &gd);
+          if (e == nullptr) {
+            (void)cache.end_fills();
+            cleanup();
+            return fail("layer " + std::to_string(i) + ": Qwen sparse MoE routed expert " +
+                        std::to_string(ids[t * K + j]) + " load failed: " + gd);
+          }
+          if (e->input_dim() != D || e->output_dim() != D || e->intermediate_dim() != m->cfg.geometry.inter) {
+            (void)cache.end_fills();
+            cleanup();
+            return fail("layer " + std::to_string(i) + ": Qwen sparse MoE routed expert geometry mismatch");
+          }
+        }
+      auto* hp = reinterpret_cast<const std::uint8_t**>(h + o_p) + i * tokens * nslot_max;
+      for (std::uint32_t t = 0; t < tokens; ++t) {
+        for (std::size_t j = 0; j < K; ++j) hp[t * nslot + j] = cache.resident_blob(cl, ids[t * K + j]);
+        if (nslot > K) hp[t * nslot + K] = m->shared_blob.as<const std::uint8_t>();
+      }
+      for (std::size_t j = 0; j < tokens * K; ++j)
+        if (hp[(j / K) * nslot + j % K] == nullptr) {
+          (void)cache.end_fills();
+          cleanup();
+          return fail("layer " + std::to_string(i) +
+                      ": Qwen sparse MoE: the cache budget cannot hold every expert of this batch at once");
+        }
+      const std::size_t po = o_p + i * tokens * nslot_max * sizeof(void*);
+      rc = osmd_copy_d2d(d + po, h + po, al(tokens * nslot * sizeof(void*)), st);
+      const int frc = cache.end_fills();
+      if (rc == 0) rc = frc;
+      // The sublayer: RMSNorm + router (its outputs to the shared routing
+      // block), then the experts with the given weights and slots, plus the
+      // residual.
+      osmd_moe_args ar = m->args(cur, nxt, tokens, nullptr, true);
+      ar.x_norm = reinterpret_cast<float*>(d + o_norm);
+      ar.logits = reinterpret_cast<float*>(d + o_lg);
+      ar.ids = reinterpret_cast<std::uint32_t*>(d + o_rid);
+      ar.weights = reinterpret_cast<float*>(d + o_rw);
+      ar.mass = reinterpret_cast<float*>(d + o_mass);
+      ar.shared_gate = reinterpret_cast<float*>(d + o_gate);
+      osmd_moe_args ae = ar;
+      ae.slot_ptrs = reinterpret_cast<const std::uint8_t**>(d + po);
+      ae.weights = reinterpret_cast<float*>(d + o_w) + i * tokens * K;
+      if (rc == 0) rc = osmd_moe_route(&ar, st);
+      if (rc == 0) rc = osmd_moe_experts(&ae, st);
+      if (rc == 0) rc = osmd_event_record(done[i], st);
+      if (rc != 0) {
+        cleanup();
+        return fail("layer " + std::to_string(i) + ": " + hip_error("cached stack launch failed", rc));
+      }
+      for (std::size_t j = 0; j < tokens * K; ++j) cache.mark_readers(cl, ids[j], done[i]);
+    }
+    const std::size_t o_y = n % 2 == 0 ? o_a : o_b;
+    rc = osmd_copy_d2d(h + o_y, d + o_y, al(xb), st);
+    if (rc == 0) rc = osmd_stream_synchronize(st);
+    cleanup();
+    if (rc != 0) return fail(hip_error("cached stack failed", rc));
+    std::memcpy(y, h + o_y, xb);
+    return true;
+  } catch (const std::exception& e) {
+    cleanup();
+    return fail(std::string("cached stack: ") + e.what());
+  }
+}
 
 HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpertCache& expert_cache,
                                      HipMoeLayer& layer_state, std::uint32_t layer,

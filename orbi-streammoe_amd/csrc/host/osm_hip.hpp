@@ -669,6 +669,15 @@ class HipResidentExpertCache {
   // the cache's slots.
   void begin_fills() noexcept;
   [[nodiscard]] int end_fills() noexcept;
+  // Pipelined use, for a stack of layers enqueued without host waits:
+  // between begin_pipeline and end_pipeline, the refill of a slot waits only
+  // for the work that last read it (the event given to mark_readers), not
+  // for everything enqueued on the compute stream, so one layer's fills
+  // overlap the kernels of the layers before. end_pipeline is called once
+  // the compute stream has drained (the events may then be destroyed).
+  void begin_pipeline() noexcept;
+  void mark_readers(std::uint32_t layer, std::uint32_t expert, osmd_event done) noexcept;
+  void end_pipeline() noexcept;
 
   [[nodiscard]] std::size_t slot_count() const noexcept;
   [[nodiscard]] std::size_t stride() const noexcept;
@@ -907,5 +916,17 @@ struct HipMoePicks {
     HipComputeContext& context, HipResidentExpertCache& expert_cache,
     HipMoeLayer& layer_state, std::uint32_t layer, std::span<const float> hidden,
     bool sublayer, const HipMoePicks* picks = nullptr) noexcept;
+
+// The decoder stack's layer loop (checkpoint_decoder_stack.cpp:191-204) as
+// chained MoE sublayers over the capped cache, with every layer's picks
+// given (ids and weights [n][tokens][k]): the activations stay on the
+// device, no layer waits for the host, and each layer's fills wait only for
+// the kernels that last read the slots they overwrite. Every output is the
+// bits of run_qwen_sparse_moe_hip called layer by layer. y = the last
+// layer's output [tokens][D] (host). Returns false with a diagnostic.
+[[nodiscard]] bool run_cached_stack_picks(HipComputeContext& context, HipResidentExpertCache& expert_cache,
+                                          std::span<HipMoeLayer* const> layers, const std::uint32_t* cache_layers,
+                                          std::span<const float> x, const std::uint32_t* pick_ids,
+                                          const float* pick_weights, float* y, std::string* diagnostic) noexcept;
 
 }  // namespace osm
