@@ -56,8 +56,8 @@ def parse():
                     help="HBM cap of the expert cache in the capped-cache decode (GB)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the decode-batch, prefill and capped-cache measurements")
-    ap.add_argument("--grouped-only", action="store_true",
-                    help="no benchmark line: only the 512-token prefill chunk and the 64-token grouped decode "
+    ap.add_argument("--grouped-only", choices=("prefill", "batch64", "both"),
+                    help="no benchmark line: only the 512-token prefill chunk and/or the 64-token grouped decode "
                          "over --layers layer copies (for profiling the grouped kernels)")
     ap.add_argument("--counters", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="no benchmark: summarise two rocprofv3 --pmc counter_collection.csv files "
@@ -450,9 +450,12 @@ def main():
     g, slab, moes = build_model(ctx, L, args.seed)
     log(f"[bench] model ready: {L} layers x {E} experts ({slab.stride * E * L / 1e9:.1f} GB) in {time.time() - t0:.1f}s on {ctx.device_name}")
     if args.grouped_only:
-        pf = prefill(ctx, moes, slab, args, layers=min(L, 8))
-        b64 = grouped_decode(ctx, moes, slab, args, 64, layers=min(L, 8))
-        print(json.dumps({"prefill": pf, "grouped_decode_64": b64}), flush=True)
+        res = {}
+        if args.grouped_only in ("prefill", "both"):
+            res["prefill"] = prefill(ctx, moes, slab, args, layers=min(L, 8))
+        if args.grouped_only in ("batch64", "both"):
+            res["grouped_decode_64"] = grouped_decode(ctx, moes, slab, args, 64, layers=min(L, 8))
+        print(json.dumps(res), flush=True)
         copy_probe(ctx, args)
         return
 
