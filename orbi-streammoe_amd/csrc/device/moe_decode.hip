@@ -225,13 +225,16 @@ constexpr float kBoundSlack = 1.0f + 0x1p-9f;
 constexpr float kUnderflowGap = 80.0f;
 
 // The exact path recomputes logits in the reference's order. The additions
-// of one logit form a chain that cannot be split, so the workgroup stages
-// everything else: kExactCols columns at a time, all threads load the
-// candidates' router elements and the input, round each product w * x into
-// LDS, and one thread per candidate then adds its row's products in column
-// order. The next chunk's loads are issued before the additions start.
-constexpr uint32_t kExactCols = 256;
+// of one logit form a chain that cannot be split; everything else runs
+// beside it. Wavefronts 1-3 produce: per chunk of kExactCols columns, thread
+// (candidate r, segment s) loads 16 router elements of candidate r and the
+// matching inputs and writes the rounded products w * x into one of two LDS
+// buffers. Wavefront 0 adds: lane r adds candidate r's products of the
+// previous chunk in column order while the producers fill the other buffer,
+// one barrier per chunk.
 constexpr uint32_t kExactRows = 16;  // candidates per pass
+constexpr uint32_t kExactSegs = (kSelThreads - kWave) / kExactRows;  // producer threads per candidate
+constexpr uint32_t kExactCols = kExactSegs * 16u;                     // 192 columns per chunk
 constexpr uint32_t kExactStride = kExactCols + 4u;  // LDS row stride: 16-byte aligned rows, adders' reads in distinct banks
 
 // Bins of the device ranking's distance histogram (rank_device).
@@ -261,10 +264,10 @@ struct Selection {
   float scal[2];
   uint32_t nunresolved, ncand, thr, flags, wcount[kSelWaves];
   uint16_t cl[kSelThreads * PER];             // exact path: candidate list
-  float xe[kExactCols];                       // exact path: the input of one chunk of columns
-  __attribute__((aligned(16))) float prod[kExactRows][kExactStride];  // exact path: rounded products of one chunk
+  __attribute__((aligned(16))) float xe[2][kExactCols];  // exact path: the inputs of two chunks
+  __attribute__((aligned(16))) float prod[2][kExactRows][kExactStride];  // exact path: rounded products of two chunks
 };
-static_assert(kExactCols == kSelThreads && kExactRows * 16u == kSelThreads, "exact-path chunk mapping");
+static_assert(kExactRows * kExactSegs + kWave == kSelThreads, "exact-path chunk mapping");
 static_assert(kSelWaves * OSMD_MAX_TOP_K <= kWave, "the fallback's candidates fit the candidate list");
 
 __device__ __forceinline__ void sort_step(uint32_t* k, uint32_t* n, int a, int b) {
@@ -345,12 +348,12 @@ __device__ __forceinline__ float load_x1(const RouteView& rv, uint32_t t, uint32
 // The reference's RMSNorm scale of token t: the squares summed in order,
 // then 1 / sqrt(sum / D + eps), each operation rounded to fp32
 // (reference_ops.cpp:113-121). Every thread calls it; x is staged in LDS
-// kExactRows * kExactStride columns at a time for thread 0's chain.
+// 2 * kExactRows * kExactStride columns at a time for thread 0's chain.
 template <int PER>
 __device__ float exact_rms_scale(const RouteView& rv, uint32_t t, Selection<PER>& out) {
 #pragma clang fp contract(off)
-  constexpr uint32_t kCols = kExactRows * kExactStride;
-  float* stage = &out.prod[0][0];
+  constexpr uint32_t kCols = 2u * kExactRows * kExactStride;
+  float* stage = &out.prod[0][0][0];
   float ss = 0.0f;
   for (uint32_t c0 = 0; c0 < rv.hidden; c0 += kCols) {
     // The squares, each rounded as the reference rounds v * v, in parallel;
@@ -379,9 +382,13 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
                                 float scale) {
 #pragma clang fp contract(off)
   const uint32_t D = rv.hidden, tid = threadIdx.x;
-  // This thread's products: row r, 16 columns from seg. The 16 rows of one
-  // segment sit in 16 lanes, so their LDS writes land in 16 banks.
-  const uint32_t r = tid % 16u, seg = (tid / 16u) * 16u;
+  // Producer (candidate r, columns seg .. seg + 15 of each chunk); the 16
+  // candidates of one segment sit in 16 lanes, so their LDS writes land in
+  // distinct banks. Producer ptid also stages input column ptid of a chunk.
+  const bool producer = tid >= kWave;
+  const uint32_t ptid = producer ? tid - kWave : 0u;
+  const uint32_t r = ptid % kExactRows, seg = (ptid / kExactRows) * 16u;
+  const bool active = producer && r < nr;
   const uint32_t e = r < nr ? out.cl[first + r] : out.cl[first];
   Q8Row qr{};
   const uint8_t* row = nullptr;
@@ -389,36 +396,63 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
     qr = q8_row(rv.router, rv.expert_count, e, D, rv.router_group);
   else
     row = static_cast<const uint8_t*>(rv.router) + static_cast<size_t>(e) * D * (RD == OSM_META_F32 ? 4u : 2u);
-  Raw8<RD> w0, w1;
-  float xv = 0.0f, nwv = 1.0f;
-  auto fetch = [&](uint32_t c0) {
+  Raw8<RD> w0{}, w1{};
+  auto fetch_w = [&](uint32_t c0) {
     const uint32_t c = c0 + seg;
-    if (r < nr && c < D) {
+    if (!active) return;
+    if (c < D) {
       if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c, w0); else load_raw8<RD>(row, c, w0);
     }
-    if (r < nr && c + 8u < D) {
+    if (c + 8u < D) {
       if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c + 8u, w1); else load_raw8<RD>(row, c + 8u, w1);
     }
-    xv = load_x1(rv, t, c0 + tid);
-    nwv = (rv.rms && c0 + tid < D) ? ldg<float>(rv.norm_weight + c0 + tid) : 1.0f;
   };
-  // Per chunk: its input and products into LDS, the next chunk's loads
-  // issued, then this chunk's additions.
+  float xv = 0.0f, nwv = 1.0f;
+  auto fetch_x = [&](uint32_t c0) {
+    if (!producer) return;
+    const uint32_t c = c0 + ptid;
+    xv = load_x1(rv, t, c);
+    nwv = (rv.rms && c < D) ? ldg<float>(rv.norm_weight + c) : 1.0f;
+  };
+  auto stage_x = [&](uint32_t buf) {
+    if (producer) out.xe[buf][ptid] = rv.rms ? xv * (scale * nwv) : xv;
+  };
+  // Step k: the producers write chunk k's products (router elements loaded
+  // in step k - 1, inputs staged in step k - 1), stage chunk k + 1's inputs
+  // (loaded in step k - 1) and issue the loads of chunk k + 1's router
+  // elements and chunk k + 2's inputs; lane r of wavefront 0 adds chunk
+  // k - 1. Products past D are written and never added. (Loading the router
+  // elements two steps ahead measured no faster: a step is the addition
+  // chain plus the barrier.)
+  const uint32_t nchunks = (D + kExactCols - 1u) / kExactCols;
+  fetch_x(0);
+  fetch_w(0);
+  stage_x(0);
+  fetch_x(kExactCols);
+  __syncthreads();
   float acc = 0.0f;
-  fetch(0);
-  for (uint32_t c0 = 0; c0 < D; c0 += kExactCols) {
-    out.xe[tid] = rv.rms ? xv * (scale * nwv) : xv;
-    __syncthreads();
-    if (r < nr) {
+  for (uint32_t k = 0; k <= nchunks; ++k) {
+    if (active && k < nchunks) {
+      float4* dst = reinterpret_cast<float4*>(&out.prod[k & 1u][r][seg]);
+      const float4* xs = reinterpret_cast<const float4*>(&out.xe[k & 1u][seg]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        out.prod[r][seg + j] = raw8_get<RD>(w0, j) * out.xe[seg + j];
-        out.prod[r][seg + 8 + j] = raw8_get<RD>(w1, j) * out.xe[seg + 8 + j];
+      for (int j = 0; j < 4; ++j) {
+        const float4 x4 = xs[j];
+        const Raw8<RD>& w = j < 2 ? w0 : w1;
+        const int o = 4 * (j % 2);
+        dst[j] = make_float4(raw8_get<RD>(w, o) * x4.x, raw8_get<RD>(w, o + 1) * x4.y,
+                             raw8_get<RD>(w, o + 2) * x4.z, raw8_get<RD>(w, o + 3) * x4.w);
       }
     }
-    __syncthreads();
-    if (c0 + kExactCols < D) fetch(c0 + kExactCols);
-    if (tid < nr) acc = chain_sum(out.prod[tid], D - c0 < kExactCols ? D - c0 : kExactCols, acc);
+    if (k + 1u < nchunks) {
+      stage_x((k + 1u) & 1u);
+      fetch_w((k + 1u) * kExactCols);
+      fetch_x((k + 2u) * kExactCols);
+    }
+    if (tid < nr && k > 0u) {
+      const uint32_t c0 = (k - 1u) * kExactCols;
+      acc = chain_sum(out.prod[(k - 1u) & 1u][tid], D - c0 < kExactCols ? D - c0 : kExactCols, acc);
+    }
     __syncthreads();
   }
   if (tid < nr) out.ex[out.cl[first + tid]] = acc;
