@@ -626,14 +626,19 @@ __device__ __forceinline__ void load_block(BlockWeights<META, S, NSTEP>& W, cons
   for (uint32_t nb = 0; nb < 2u; ++nb) {
     uint32_t r = block * kWgRows + mx.wave_row + nb * kBlockRows + m;
     r = r < mx.N ? r : mx.N - 1u;
-    const uint8_t* qrow = blob + mx.q_off + static_cast<size_t>(r) * (mx.K / 2u);
+    // A group is 32 S columns, 4 S words: the offsets of the runs within the
+    // range are compile-time constants (load immediates).
+    constexpr uint32_t kGroupWords = 4u * S;
+    const uint8_t* qrow = blob + mx.q_off + static_cast<size_t>(r) * (mx.K / 2u) + g0 * kGroupWords * 4u;
     if constexpr (kPairLoads<S>) {
       static_assert(GPR % 2 == 0, "group pairs");
+      const uint8_t* qlane = qrow + 16u * q;
 #pragma unroll
-      for (int gp = 0; gp < GPR / 2; ++gp) word_run<4>(qrow + ((g0 + 2 * gp) * (mx.G / 8u) + 4u * q) * 4u, &W.w[nb][4 * gp]);
+      for (int gp = 0; gp < GPR / 2; ++gp) word_run<4>(qlane + 2u * gp * kGroupWords * 4u, &W.w[nb][4 * gp]);
     } else {
+      const uint8_t* qlane = qrow + 4u * S * q;
 #pragma unroll
-      for (int gg = 0; gg < GPR; ++gg) word_run<S>(qrow + ((g0 + gg) * (mx.G / 8u) + S * q) * 4u, &W.w[nb][gg * S]);
+      for (int gg = 0; gg < GPR; ++gg) word_run<S>(qlane + gg * kGroupWords * 4u, &W.w[nb][gg * S]);
     }
     const size_t mi = static_cast<size_t>(r) * mx.ngroups + g0;
     W.sb[nb].load(blob + mx.s_off, mi);
@@ -714,7 +719,9 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
       const float sc = W.sb[nb].get(gg);
       const float cb = W.bb[nb].get(gg) - 128.0f * sc;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) total[nb][j] += sc * d[j] + cb * xs[j];
+      // Two FMAs per element (written as one sum the compiler keeps a
+      // multiply, an FMA and an add).
+      for (int j = 0; j < 4; ++j) total[nb][j] = __builtin_fmaf(sc, d[j], __builtin_fmaf(cb, xs[j], total[nb][j]));
     }
   }
 #pragma unroll
