@@ -102,14 +102,17 @@ __global__ void widen_bf16_kernel(const uint16_t* __restrict__ x, size_t n, floa
 // prepare: rows [R, K] (fp32, or bf16 when XBF16) -> terms [R][NS][K] bf16 in
 // word order and sums [R][K/G] of the values the first two terms represent
 // (the expert GEMMs read terms 0 and 1 of this layout; the router GEMM reads
-// all three when NS = 3). One thread per (row, 8-column word); the G/8
+// all three when NS = 3). A bf16 input needs one term (NS = 1): it is exact. One thread per (row, 8-column word); the G/8
 // threads of a group are adjacent lanes of one wavefront and add their sums
 // by butterfly.
 template <bool XBF16, int NS>
 __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t K, uint32_t G,
                                uint16_t* __restrict__ terms, float* __restrict__ sums,
                                float* __restrict__ norms) {
-  static_assert(NS >= kActSplit, "the expert GEMMs read the first two terms");
+  // A bf16 input is its own first term: one term is exact, and the expert
+  // GEMMs then read just that one.
+  static_assert(NS >= kActSplit || XBF16, "the expert GEMMs read the first two terms of an fp32 input");
+  constexpr int kSumTerms = NS < kActSplit ? NS : kActSplit;
   const uint32_t words = K / 8u, wpg = G / 8u;
   const size_t n = static_cast<size_t>(R) * words;  // a multiple of wpg, so groups never straddle waves
   const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
@@ -151,7 +154,7 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
         pk.z = out[4] | (static_cast<uint32_t>(out[5]) << 16);
         pk.w = out[6] | (static_cast<uint32_t>(out[7]) << 16);
         *reinterpret_cast<uint4*>(terms + (static_cast<size_t>(r) * NS + s) * K + wd * 8u) = pk;
-        if (s + 1 == kActSplit) {
+        if (s + 1 == kSumTerms) {
 #pragma unroll
           for (int k = 0; k < 8; ++k) total += rep[k];
         }
@@ -436,7 +439,7 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
 // of each group (step s: word S*q + s), so one lane load covers a group.
 struct SplitParams {
   osm_expert_geometry g;
-  const uint16_t* terms;  // A terms [rows][term_count][K]; the GEMM reads the first kActSplit
+  const uint16_t* terms;  // A terms [rows][term_count][K]; the GEMM reads the first NT
   uint32_t term_count;
   const float* sums;      // [rows][K/G]
   const uint32_t* tile_rows;  // [tiles][16] token of each pair of a tile
@@ -646,19 +649,19 @@ __device__ __forceinline__ void load_block(BlockWeights<META, S, NSTEP>& W, cons
   }
 }
 
-template <int PROJ, int NSTEP>
+template <int PROJ, int NSTEP, int NT>
 struct SplitLds {
   static constexpr uint32_t KS = 32u * NSTEP;
   static constexpr uint32_t RS = KS + 8u;  // row stride (bf16), padded against bank conflicts
-  uint16_t a[kActSplit][kTileTokens][RS];
+  uint16_t a[NT][kTileTokens][RS];
   float xs[NSTEP][kTileTokens];  // group sums (at most NSTEP groups per range)
 };
 
 // MFMAs of one block against the staged tile, then its partial sums. MFMA
 // row m reads tile row min(m, count - 1); the D rows of lane q are tile rows
 // 4q .. 4q+3 (those past count are not stored).
-template <int META, int PROJ, int S, int NSTEP, uint32_t kWgRows>
-__device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP>& lds,
+template <int META, int PROJ, int S, int NSTEP, int NT, uint32_t kWgRows>
+__device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP, NT>& lds,
                                               const BlockWeights<META, S, NSTEP>& W, const WaveMatrix& mx,
                                               uint32_t block, uint32_t split, uint32_t start, uint32_t rows,
                                               uint32_t pr, uint32_t m, uint32_t q) {
@@ -693,11 +696,11 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
           }
       }
     }
-    bf16x8 a[S][kActSplit];
+    bf16x8 a[S][NT];
 #pragma unroll
     for (int s2 = 0; s2 < S; ++s2)
 #pragma unroll
-      for (uint32_t t = 0; t < kActSplit; ++t)
+      for (int t = 0; t < NT; ++t)
         a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&lds.a[t][ar][(gg * G8 + S * slot + s2) * 8u]));
     float xs[4];
 #pragma unroll
@@ -714,7 +717,7 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
           word = W.w[nb][gg * S + s2];
         const bf16x8 b = nibble_operand(word);
 #pragma unroll
-        for (uint32_t t = 0; t < kActSplit; ++t) d = mfma(a[s2][t], b, d);
+        for (int t = 0; t < NT; ++t) d = mfma(a[s2][t], b, d);
       }
       const float sc = W.sb[nb].get(gg);
       const float cb = W.bb[nb].get(gg) - 128.0f * sc;
@@ -747,17 +750,17 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
 // one. The next item's tile record is fetched while the current one is
 // staged, and the next item's first block is in flight while the current
 // item's last block computes.
-template <int META, int PROJ, int S, int NSTEP>
+template <int META, int PROJ, int S, int NSTEP, int NT>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2))) void split_kernel(SplitParams p) {
   constexpr uint32_t KS = 32u * NSTEP;
   constexpr int GPR = NSTEP / S;  // groups per range
   constexpr uint32_t kWgRows = split_rows<PROJ>();
   constexpr uint32_t kUnitCols = KS / 8u;  // 16-byte units per staged row
-  constexpr uint32_t kUnitsPerThread = kActSplit * kTileTokens * kUnitCols / kSplitThreads;
-  static_assert(kActSplit * kTileTokens * kUnitCols % kSplitThreads == 0, "staging units");
+  constexpr uint32_t kUnitsPerThread = NT * kTileTokens * kUnitCols / kSplitThreads;
+  static_assert(NT * kTileTokens * kUnitCols % kSplitThreads == 0, "staging units");
   static_assert(GPR * kTileTokens <= kSplitThreads, "group sums: one per thread");
   constexpr uint32_t kProjWaves = PROJ == 2 ? kSplitWaves / 2u : kSplitWaves;
-  __shared__ __align__(16) SplitLds<PROJ, NSTEP> lds;
+  __shared__ __align__(16) SplitLds<PROJ, NSTEP, NT> lds;
 
   // Per-lane indices and the wave's matrix, derived from the thread index.
   // Inside the item loop the index is re-read opaquely, so that what derives
@@ -869,7 +872,7 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
     for (uint32_t bi = 0; bi < kItemBlocks; bi += 2u) {
       load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, fb + bi + 1u, split, m, q);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<META, PROJ, S, NSTEP, kWgRows>(p, lds, W0, mx, fb + bi, split, start, rows, pr, m, q);
+      compute_block<META, PROJ, S, NSTEP, NT, kWgRows>(p, lds, W0, mx, fb + bi, split, start, rows, pr, m, q);
       if (bi == 0u) next_rec = uniform_rec(tl_next);
       const bool last = bi + 2u >= kItemBlocks;
       const bool has_next = next_rec.count != 0u;
@@ -877,7 +880,7 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
                                           last ? (has_next ? wk_next.first_block : fb) : fb + bi + 2u,
                                           last && has_next ? wk_next.split : split, m, q);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<META, PROJ, S, NSTEP, kWgRows>(p, lds, W1, mx, fb + bi + 1u, split, start, rows, pr, m, q);
+      compute_block<META, PROJ, S, NSTEP, NT, kWgRows>(p, lds, W1, mx, fb + bi + 1u, split, start, rows, pr, m, q);
     }
     __syncthreads();  // the LDS tile is restaged by the next item
     item = next;
@@ -1039,11 +1042,11 @@ void set_item_blocks(SplitParams& sp, uint32_t row_blocks, uint32_t nsplit) {
 // a multiple of 8, and no more than there are items (also a multiple of 8).
 // A larger grid would leave workgroups waiting for a free slot, to start
 // their whole item list after the others end.
-template <int META, int PROJ, int S, int NSTEP>
+template <int META, int PROJ, int S, int NSTEP, int NT>
 uint32_t split_grid(uint32_t items) {
   static const uint32_t per_cu = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP>, kSplitThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP, NT>, kSplitThreads, 0) !=
             hipSuccess ||
         n < 1)
       n = 1;
@@ -1058,39 +1061,60 @@ uint32_t split_grid(uint32_t items) {
   return items < grid ? items : grid;
 }
 
-template <int META, int PROJ, int S, int NSTEP>
+template <int META, int PROJ, int S, int NSTEP, int NT>
 void launch_split_r(const SplitParams& sp, hipStream_t st) {
   // Only the ranges range_cols() can choose for this metadata and group are
   // instantiated (a wider one would not fit the registers).
   constexpr uint32_t kMetaBytes = META == OSM_META_F32 ? 4u : 2u;
   if constexpr (NSTEP / S * kMetaBytes <= 16u)
-    split_kernel<META, PROJ, S, NSTEP><<<split_grid<META, PROJ, S, NSTEP>(sp.items), kSplitThreads, 0, st>>>(sp);
+    split_kernel<META, PROJ, S, NSTEP, NT><<<split_grid<META, PROJ, S, NSTEP, NT>(sp.items), kSplitThreads, 0, st>>>(sp);
 }
 
-template <int META, int PROJ, int S>
+template <int META, int PROJ, int S, int NT>
 void launch_split_s(const SplitParams& sp, hipStream_t st) {
   switch (range_cols(sp.g, PROJ == 2 ? sp.g.hidden : sp.g.inter)) {
-    case 512: launch_split_r<META, PROJ, S, 16>(sp, st); break;
-    case 256: launch_split_r<META, PROJ, S, 8>(sp, st); break;
-    default: launch_split_r<META, PROJ, S, 4>(sp, st); break;
+    case 512: launch_split_r<META, PROJ, S, 16, NT>(sp, st); break;
+    case 256: launch_split_r<META, PROJ, S, 8, NT>(sp, st); break;
+    default: launch_split_r<META, PROJ, S, 4, NT>(sp, st); break;
   }
 }
 
-template <int META, int PROJ>
+template <int META, int PROJ, int NT>
 void launch_split_meta(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.group) {
-    case 32: launch_split_s<META, PROJ, 1>(sp, st); break;
-    case 64: launch_split_s<META, PROJ, 2>(sp, st); break;
-    default: launch_split_s<META, PROJ, 4>(sp, st); break;
+    case 32: launch_split_s<META, PROJ, 1, NT>(sp, st); break;
+    case 64: launch_split_s<META, PROJ, 2, NT>(sp, st); break;
+    default: launch_split_s<META, PROJ, 4, NT>(sp, st); break;
   }
 }
 
-template <int PROJ>
+// NT: activation terms (2 for fp32 activations, 1 for an exact bf16 input).
+template <int PROJ, int NT>
 void launch_split(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.meta_dtype) {
-    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ>(sp, st); break;
-    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ>(sp, st); break;
-    default: launch_split_meta<OSM_META_BF16, PROJ>(sp, st); break;
+    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ, NT>(sp, st); break;
+    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ, NT>(sp, st); break;
+    default: launch_split_meta<OSM_META_BF16, PROJ, NT>(sp, st); break;
+  }
+}
+
+template <int NS>
+void launch_router_gemm(uint32_t rcols, dim3 grid, hipStream_t st, const uint16_t* terms, uint32_t T, uint32_t D,
+                        const uint16_t* router, const uint16_t* sgv, uint32_t E, float* planes, const float* rnorm,
+                        const float* xnorm, float* bplanes) {
+  switch (rcols) {
+    case 512:
+      router_gemm_kernel<NS, 16><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm, xnorm,
+                                                                   bplanes);
+      break;
+    case 256:
+      router_gemm_kernel<NS, 8><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm, xnorm,
+                                                                  bplanes);
+      break;
+    default:
+      router_gemm_kernel<NS, 4><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm, xnorm,
+                                                                  bplanes);
+      break;
   }
 }
 
@@ -1149,7 +1173,10 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
     xin = m.x_norm;
     xbf16 = false;
   }
-  const uint32_t x_term_count = router_gemm ? kRouterSplit : kActSplit;
+  // A bf16 input is exact as one bf16 term: the router GEMM and the gate/up
+  // GEMM then read one term instead of three and two.
+  const bool one_term = router_gemm && xbf16;
+  const uint32_t x_term_count = router_gemm ? (one_term ? 1u : kRouterSplit) : kActSplit;
   // Error bounds of the GEMM's logits need the router's and the input's
   // 32-column norms.
   const bool gemm_bounds = router_gemm && a->router_norms != nullptr && a->x_norms != nullptr &&
@@ -1157,9 +1184,8 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   float* xnorms = gemm_bounds ? a->x_norms : nullptr;
   const size_t words = static_cast<size_t>(T) * (D / 8u);
   if (router_gemm) {
-    if (xbf16)
-      prepare_kernel<true, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums,
-                                                                                xnorms);
+    if (one_term)
+      prepare_kernel<true, 1><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums, xnorms);
     else
       prepare_kernel<false, kRouterSplit><<<blocks_for(words, 4096), 256, 0, st>>>(xin, T, D, G, a->x_terms, a->x_sums,
                                                                                 xnorms);
@@ -1181,23 +1207,13 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
                     (T + kTileTokens - 1) / kTileTokens, D / rcols);
     const uint16_t* router = static_cast<const uint16_t*>(m.router);
     const uint16_t* sgv = has_shared ? static_cast<const uint16_t*>(m.shared_gate_vec) : nullptr;
-    switch (rcols) {
-      case 512:
-        router_gemm_kernel<kRouterSplit, 16><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
-                                                                              m.expert_count, a->logit_planes, a->router_norms, xnorms,
-                                               gemm_bounds ? a->bound_planes : nullptr);
-        break;
-      case 256:
-        router_gemm_kernel<kRouterSplit, 8><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
-                                                                             m.expert_count, a->logit_planes, a->router_norms, xnorms,
-                                               gemm_bounds ? a->bound_planes : nullptr);
-        break;
-      default:
-        router_gemm_kernel<kRouterSplit, 4><<<grid, kGroupedThreads, 0, st>>>(a->x_terms, T, D, router, sgv,
-                                                                             m.expert_count, a->logit_planes, a->router_norms, xnorms,
-                                               gemm_bounds ? a->bound_planes : nullptr);
-        break;
-    }
+    float* bplanes = gemm_bounds ? a->bound_planes : nullptr;
+    if (one_term)
+      launch_router_gemm<1>(rcols, grid, st, a->x_terms, T, D, router, sgv, m.expert_count, a->logit_planes,
+                            a->router_norms, xnorms, bplanes);
+    else
+      launch_router_gemm<kRouterSplit>(rcols, grid, st, a->x_terms, T, D, router, sgv, m.expert_count,
+                                       a->logit_planes, a->router_norms, xnorms, bplanes);
     ms.logit_planes = a->logit_planes;
     ms.logit_parts = D / rcols;
     ms.bound_planes = gemm_bounds ? a->bound_planes : nullptr;
@@ -1229,7 +1245,10 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   sp.out = a->gu_part;
   const uint32_t gu_splits = osmd_moe_grouped_splits(&g, D);
   set_item_blocks(sp, (I + split_rows<2>() - 1) / split_rows<2>(), gu_splits);
-  launch_split<2>(sp, st);
+  if (one_term)
+    launch_split<2, 1>(sp, st);
+  else
+    launch_split<2, kActSplit>(sp, st);
   const size_t hwords = static_cast<size_t>(P) * (I / 8u);
   swiglu_terms_kernel<<<blocks_for(hwords, 4096), 256, 0, st>>>(a->gu_part, gu_splits, P, I, G, a->h_terms,
                                                                 a->h_sums);
@@ -1239,7 +1258,7 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   sp.out = a->partial;
   const uint32_t dn_splits = osmd_moe_grouped_splits(&g, I);
   set_item_blocks(sp, (D + split_rows<1>() - 1) / split_rows<1>(), dn_splits);
-  launch_split<1>(sp, st);
+  launch_split<1, kActSplit>(sp, st);
   const float* residual = (m.flags & OSMD_MOE_RESIDUAL) ? static_cast<const float*>(m.x) : nullptr;
   if (D % 4u == 0u && ((reinterpret_cast<uintptr_t>(m.y) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0u)
     combine4_kernel<<<blocks_for(static_cast<size_t>(T) * (D / 4u), 4096), 256, 0, st>>>(
