@@ -488,6 +488,7 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
   const float th = out.scal[0];
   bool full = false;
   float m = -INFINITY;
+  uint32_t ncand = 0;  // candidates of the last ranking
   for (;;) {
     // Candidates: a compact list in out.cl, wavefront by wavefront.
     bool member[PER];
@@ -505,9 +506,12 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
     uint32_t pos = static_cast<uint32_t>(incl) - mine;
     for (uint32_t w = 0; w < wave; ++w) pos += out.wcount[w];
     const uint32_t nc = out.wcount[0] + out.wcount[1] + out.wcount[2] + out.wcount[3];
+    uint32_t cpos[PER];  // list position of each member
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
+    for (int j = 0; j < PER; ++j) {
+      cpos[j] = pos;
       if (member[j]) out.cl[pos++] = static_cast<uint16_t>(base + j);
+    }
     __syncthreads();
     for (uint32_t first = 0; first < nc; first += kExactRows)
       exact_logits<PER>(rv, t, out, first, nc - first < kExactRows ? nc - first : kExactRows, scale);
@@ -520,21 +524,28 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
     if (lane == 0) out.red[0][wave] = lm;
     __syncthreads();
     m = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
-    // The reference's key: exp(fl(L - m)) (reference_ops.cpp:141-145).
+    // The reference's key: exp(fl(L - m)) (reference_ops.cpp:141-145), by
+    // expert in out.aux and in list order in ckey (the products' buffer is
+    // free now), so that the ranking reads keys without an indirection.
+    float* ckey = &out.prod[0][0][0];
+    float key[PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-      if (base + j < E) out.aux[base + j] = member[j] ? expf(out.ex[base + j] - m) : -1.0f;
+    for (int j = 0; j < PER; ++j) {
+      key[j] = member[j] ? expf(out.ex[base + j] - m) : -1.0f;
+      if (base + j < E) out.aux[base + j] = key[j];
+      if (member[j]) ckey[cpos[j]] = key[j];
+    }
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       if (!member[j]) continue;
       const uint32_t e = base + j;
-      const float v = out.aux[e];
+      const float v = key[j];
       uint32_t rk = 0;
+#pragma unroll 4
       for (uint32_t i = 0; i < nc; ++i) {
-        const uint32_t o = out.cl[i];
-        const float w = out.aux[o];
-        rk += (w > v || (w == v && o < e)) ? 1u : 0u;
+        const float w = ckey[i];
+        rk += (w > v || (w == v && out.cl[i] < e)) ? 1u : 0u;
       }
       if (rk <= k) out.fid[rk] = e;
     }
@@ -543,27 +554,32 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
     const bool again = !full && !(out.ex[out.fid[k - 1]] - m >= -kUnderflowGap);
     if (!again) {
       if (tid == 0) out.ncand = nc;
+      ncand = nc;
       break;
     }
     full = true;
     __syncthreads();
   }
-  if (tid == 0) {
+  if (tid < kWave) {
     // Adjacent pairs among the first k + 1 ranked candidates (there are at
-    // least k: the device's picks are candidates).
-    const uint32_t n = out.ncand < k + 1u ? out.ncand : k + 1u;
-    uint32_t unresolved = 0;
-    for (uint32_t i = 0; i + 1 < n; ++i) {
-      const uint32_t a = out.fid[i], c = out.fid[i + 1];
-      if (out.ex[a] == out.ex[c]) continue;  // equal logits, equal keys: the lower id first, certainly
-      const float ea = out.aux[a], ec = out.aux[c];
-      const bool zeros = ea == 0.0f && ec == 0.0f && out.ex[a] - m < -104.0f && out.ex[c] - m < -104.0f;
-      if (!zeros && fabsf(ea - ec) <= 5.0f * 0x1p-23f * fmaxf(ea, ec) + 5.0f * 0x1p-149f) ++unresolved;
+    // least k: the device's picks are candidates), one pair per lane.
+    const uint32_t n = ncand < k + 1u ? ncand : k + 1u;
+    bool unresolved = false;
+    if (lane + 1u < n) {
+      const uint32_t a = out.fid[lane], c = out.fid[lane + 1u];
+      // Equal logits give equal keys: the lower id first, certainly.
+      if (out.ex[a] != out.ex[c]) {
+        const float ea = out.aux[a], ec = out.aux[c];
+        const bool zeros = ea == 0.0f && ec == 0.0f && out.ex[a] - m < -104.0f && out.ex[c] - m < -104.0f;
+        unresolved = !zeros && fabsf(ea - ec) <= 5.0f * 0x1p-23f * fmaxf(ea, ec) + 5.0f * 0x1p-149f;
+      }
     }
-    out.nunresolved = unresolved;
-    for (uint32_t i = 0; i < k; ++i) {
-      out.id[i] = out.fid[i];
-      out.lg[i] = out.val[out.fid[i]];
+    const uint32_t count = static_cast<uint32_t>(__popcll(__ballot(unresolved)));
+    if (lane == 0) out.nunresolved = count;
+    if (lane < k) {
+      const uint32_t id = out.fid[lane];
+      out.id[lane] = id;
+      out.lg[lane] = out.val[id];
     }
   }
   __syncthreads();
