@@ -649,22 +649,25 @@ __device__ __forceinline__ void load_block(BlockWeights<META, S, NSTEP>& W, cons
   }
 }
 
-template <int PROJ, int NSTEP, int NT>
+// H consecutive K ranges of the tile, staged together.
+template <int PROJ, int NSTEP, int NT, int H>
 struct SplitLds {
   static constexpr uint32_t KS = 32u * NSTEP;
   static constexpr uint32_t RS = KS + 8u;  // row stride (bf16), padded against bank conflicts
-  uint16_t a[NT][kTileTokens][RS];
-  float xs[NSTEP][kTileTokens];  // group sums (at most NSTEP groups per range)
+  uint16_t a[H][NT][kTileTokens][RS];
+  float xs[H][NSTEP][kTileTokens];  // group sums (at most NSTEP groups per range)
 };
 
-// MFMAs of one block against the staged tile, then its partial sums. MFMA
-// row m reads tile row min(m, count - 1); the D rows of lane q are tile rows
-// 4q .. 4q+3 (those past count are not stored).
-template <int META, int PROJ, int S, int NSTEP, int NT, uint32_t kWgRows>
-__device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP, NT>& lds,
+// MFMAs of one block against staged range `half` of the tile, added to
+// `total` (cleared first when `first`), then, when `last`, its partial sums.
+// MFMA row m reads tile row min(m, count - 1); the D rows of lane q are tile
+// rows 4q .. 4q+3 (those past count are not stored).
+template <int META, int PROJ, int S, int NSTEP, int NT, int H, uint32_t kWgRows>
+__device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP, NT, H>& lds,
                                               const BlockWeights<META, S, NSTEP>& W, const WaveMatrix& mx,
-                                              uint32_t block, uint32_t split, uint32_t start, uint32_t rows,
-                                              uint32_t pr, uint32_t m, uint32_t q) {
+                                              uint32_t block, uint32_t split, uint32_t half, bool first, bool last,
+                                              f32x4 (&total)[2], uint32_t start, uint32_t rows, uint32_t pr,
+                                              uint32_t m, uint32_t q) {
   constexpr int GPR = NSTEP / S;
   constexpr uint32_t G8 = (32u * S) / 8u;  // 16-byte units per group
   // The tile row indices pass through an opaque copy per block: every block
@@ -678,7 +681,7 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
     xr[j] = 4u * q + j < rows ? 4u * q + j : rows - 1u;
     asm volatile("" : "+v"(xr[j]));
   }
-  f32x4 total[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  if (first) total[0] = total[1] = f32x4{0.f, 0.f, 0.f, 0.f};
   // k-slot of this lane within a group: its words are S * slot .. S * slot + S-1.
   const uint32_t slot = kPairLoads<S> ? pair_slot(q) : q;
   uint32_t pw[2][4];  // pair loads: the swapped words of the current group pair
@@ -701,10 +704,10 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
     for (int s2 = 0; s2 < S; ++s2)
 #pragma unroll
       for (int t = 0; t < NT; ++t)
-        a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&lds.a[t][ar][(gg * G8 + S * slot + s2) * 8u]));
+        a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&lds.a[half][t][ar][(gg * G8 + S * slot + s2) * 8u]));
     float xs[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xs[j] = lds.xs[gg][xr[j]];
+    for (int j = 0; j < 4; ++j) xs[j] = lds.xs[half][gg][xr[j]];
 #pragma unroll
     for (uint32_t nb = 0; nb < 2u; ++nb) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
@@ -726,6 +729,16 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
       // multiply, an FMA and an add).
       for (int j = 0; j < 4; ++j) total[nb][j] = __builtin_fmaf(sc, d[j], __builtin_fmaf(cb, xs[j], total[nb][j]));
     }
+  }
+  if (!last) {
+    // The totals carry into the block's next range: materialised here, so
+    // the compiler does not sink this range's epilogue past the next
+    // block's loads (which keeps every group's accumulators live and spills).
+#pragma unroll
+    for (uint32_t nb = 0; nb < 2u; ++nb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(total[nb][j]));
+    return;
   }
 #pragma unroll
   for (uint32_t nb = 0; nb < 2u; ++nb) {
@@ -750,7 +763,7 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
 // one. The next item's tile record is fetched while the current one is
 // staged, and the next item's first block is in flight while the current
 // item's last block computes.
-template <int META, int PROJ, int S, int NSTEP, int NT>
+template <int META, int PROJ, int S, int NSTEP, int NT, int H>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2))) void split_kernel(SplitParams p) {
   constexpr uint32_t KS = 32u * NSTEP;
   constexpr int GPR = NSTEP / S;  // groups per range
@@ -758,9 +771,9 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
   constexpr uint32_t kUnitCols = KS / 8u;  // 16-byte units per staged row
   constexpr uint32_t kUnitsPerThread = NT * kTileTokens * kUnitCols / kSplitThreads;
   static_assert(NT * kTileTokens * kUnitCols % kSplitThreads == 0, "staging units");
-  static_assert(GPR * kTileTokens <= kSplitThreads, "group sums: one per thread");
+  static_assert(H * GPR * kTileTokens <= kSplitThreads, "group sums: one per thread");
   constexpr uint32_t kProjWaves = PROJ == 2 ? kSplitWaves / 2u : kSplitWaves;
-  __shared__ __align__(16) SplitLds<PROJ, NSTEP, NT> lds;
+  __shared__ __align__(16) SplitLds<PROJ, NSTEP, NT, H> lds;
 
   // Per-lane indices and the wave's matrix, derived from the thread index.
   // Inside the item loop the index is re-read opaquely, so that what derives
@@ -796,8 +809,8 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
   if (tl.count == 0u) return;
   BlockWeights<META, S, NSTEP> W0, W1;
   // The first item's first block.
-  load_block<META, S, NSTEP, kWgRows>(W0, wave_matrix(uniform_u32(tid0 / kWave)), tl.blob, wk.first_block, wk.split,
-                                      tid0 % 16u, tid0 % kWave / 16u);
+  load_block<META, S, NSTEP, kWgRows>(W0, wave_matrix(uniform_u32(tid0 / kWave)), tl.blob, wk.first_block,
+                                      wk.split * H, tid0 % 16u, tid0 % kWave / 16u);
   while (tl.count != 0u) {
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
@@ -823,24 +836,29 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
     // real row (no branch around the loads).
     auto act_row = [&](uint32_t j) -> uint32_t { return __shfl(lane_act, static_cast<int>(j)); };
     constexpr bool kDirect = kUnitCols == kWave;
+    static_assert(kDirect || H == 1, "several ranges per item are staged directly");
     uint4 stage[kDirect ? 1u : kUnitsPerThread];
 #pragma unroll
-    for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
-      const uint32_t u = tid + i * kSplitThreads;
-      const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
-      const uint32_t arow = act_row(row < rows ? row : rows - 1u);
-      const uint16_t* src = p.terms + (static_cast<size_t>(arow) * p.term_count + term) * mx.K + split * KS + cu * 8u;
-      if constexpr (kDirect) {
-        if (uniform_u32(row) < rows) load_lds16(src, &lds.a[term][row][0]);  // term, row: wave-uniform
-      } else {
-        stage[i] = ldg16(src);
+    for (int h = 0; h < H; ++h) {
+#pragma unroll
+      for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+        const uint32_t u = tid + i * kSplitThreads;
+        const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+        const uint32_t arow = act_row(row < rows ? row : rows - 1u);
+        const uint16_t* src =
+            p.terms + (static_cast<size_t>(arow) * p.term_count + term) * mx.K + (split * H + h) * KS + cu * 8u;
+        if constexpr (kDirect) {
+          if (uniform_u32(row) < rows) load_lds16(src, &lds.a[h][term][row][0]);  // term, row: wave-uniform
+        } else {
+          stage[i] = ldg16(src);
+        }
       }
     }
-    // Group sums: thread (sg, srow) for sg < GPR; the others load a valid
-    // element and do not store it.
+    // Group sums: thread (sg, srow) for sg < H * GPR (range sg / GPR); the
+    // others load a valid element and do not store it.
     const uint32_t sg = tid / kTileTokens, srow = tid % kTileTokens;
     const uint32_t sarow = act_row(srow < rows ? srow : rows - 1u);
-    const float xsum = p.sums[static_cast<size_t>(sarow) * mx.ngroups + split * GPR + (sg < GPR ? sg : 0u)];
+    const float xsum = p.sums[static_cast<size_t>(sarow) * mx.ngroups + split * H * GPR + (sg < H * GPR ? sg : 0u)];
 
     const uint32_t next = item + gridDim.x;
     const SplitWork wk_next = split_work(p, next);
@@ -855,10 +873,10 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
       for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
         const uint32_t u = tid + i * kSplitThreads;
         const uint32_t term = u / (kTileTokens * kUnitCols), row = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
-        *reinterpret_cast<uint4*>(&lds.a[term][row][cu * 8u]) = stage[i];
+        *reinterpret_cast<uint4*>(&lds.a[0][term][row][cu * 8u]) = stage[i];
       }
     }
-    if (sg < GPR) lds.xs[sg][srow] = xsum;
+    if (sg < H * GPR) lds.xs[sg / GPR][sg % GPR][srow] = xsum;
     __syncthreads();
 
     // The item's blocks, straight-line, so that each wait is for exactly the
@@ -867,20 +885,28 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
     // scalars there. After the last block W0 loads the next item's first
     // block, or (no next item) this item's first block again, read and not
     // used.
+    // Sub-block sb is range half sb % H of block fb + sb / H; with H = 2 the
+    // two halves of a block are one pair of the loop and share its totals.
     TileRec next_rec{blob, 0u, 0u};
+    constexpr uint32_t kSub = kItemBlocks * H;
 #pragma unroll
-    for (uint32_t bi = 0; bi < kItemBlocks; bi += 2u) {
-      load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, fb + bi + 1u, split, m, q);
+    for (uint32_t sb = 0; sb < kSub; sb += 2u) {
+      f32x4 total[2];
+      const uint32_t b0 = fb + sb / H, h0 = sb % H, b1 = fb + (sb + 1u) / H, h1 = (sb + 1u) % H;
+      load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, b1, split * H + h1, m, q);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<META, PROJ, S, NSTEP, NT, kWgRows>(p, lds, W0, mx, fb + bi, split, start, rows, pr, m, q);
-      if (bi == 0u) next_rec = uniform_rec(tl_next);
-      const bool last = bi + 2u >= kItemBlocks;
+      compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows>(p, lds, W0, mx, b0, split, h0, h0 == 0u, h0 == H - 1u,
+                                                         total, start, rows, pr, m, q);
+      if (sb == 0u) next_rec = uniform_rec(tl_next);
+      const bool last = sb + 2u >= kSub;
       const bool has_next = next_rec.count != 0u;
+      const uint32_t b2 = fb + (sb + 2u) / H, h2 = (sb + 2u) % H;
       load_block<META, S, NSTEP, kWgRows>(W0, mx, last && has_next ? next_rec.blob : blob,
-                                          last ? (has_next ? wk_next.first_block : fb) : fb + bi + 2u,
-                                          last && has_next ? wk_next.split : split, m, q);
+                                          last ? (has_next ? wk_next.first_block : fb) : b2,
+                                          last ? (has_next ? wk_next.split * H : split * H) : split * H + h2, m, q);
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<META, PROJ, S, NSTEP, NT, kWgRows>(p, lds, W1, mx, fb + bi + 1u, split, start, rows, pr, m, q);
+      compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows>(p, lds, W1, mx, b1, split, h1, h1 == 0u, h1 == H - 1u,
+                                                         total, start, rows, pr, m, q);
     }
     __syncthreads();  // the LDS tile is restaged by the next item
     item = next;
@@ -1042,11 +1068,11 @@ void set_item_blocks(SplitParams& sp, uint32_t row_blocks, uint32_t nsplit) {
 // a multiple of 8, and no more than there are items (also a multiple of 8).
 // A larger grid would leave workgroups waiting for a free slot, to start
 // their whole item list after the others end.
-template <int META, int PROJ, int S, int NSTEP, int NT>
+template <int META, int PROJ, int S, int NSTEP, int NT, int H>
 uint32_t split_grid(uint32_t items) {
   static const uint32_t per_cu = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP, NT>, kSplitThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP, NT, H>, kSplitThreads, 0) !=
             hipSuccess ||
         n < 1)
       n = 1;
@@ -1061,40 +1087,43 @@ uint32_t split_grid(uint32_t items) {
   return items < grid ? items : grid;
 }
 
-template <int META, int PROJ, int S, int NSTEP, int NT>
+template <int META, int PROJ, int S, int NSTEP, int NT, int H>
 void launch_split_r(const SplitParams& sp, hipStream_t st) {
   // Only the ranges range_cols() can choose for this metadata and group are
   // instantiated (a wider one would not fit the registers).
   constexpr uint32_t kMetaBytes = META == OSM_META_F32 ? 4u : 2u;
-  if constexpr (NSTEP / S * kMetaBytes <= 16u)
-    split_kernel<META, PROJ, S, NSTEP, NT><<<split_grid<META, PROJ, S, NSTEP, NT>(sp.items), kSplitThreads, 0, st>>>(sp);
+  // Two ranges per item only with 512-column ranges (staged directly).
+  if constexpr (NSTEP / S * kMetaBytes <= 16u && (H == 1 || NSTEP == 16))
+    split_kernel<META, PROJ, S, NSTEP, NT, H>
+        <<<split_grid<META, PROJ, S, NSTEP, NT, H>(sp.items), kSplitThreads, 0, st>>>(sp);
 }
 
-template <int META, int PROJ, int S, int NT>
+template <int META, int PROJ, int S, int NT, int H>
 void launch_split_s(const SplitParams& sp, hipStream_t st) {
   switch (range_cols(sp.g, PROJ == 2 ? sp.g.hidden : sp.g.inter)) {
-    case 512: launch_split_r<META, PROJ, S, 16, NT>(sp, st); break;
-    case 256: launch_split_r<META, PROJ, S, 8, NT>(sp, st); break;
-    default: launch_split_r<META, PROJ, S, 4, NT>(sp, st); break;
+    case 512: launch_split_r<META, PROJ, S, 16, NT, H>(sp, st); break;
+    case 256: launch_split_r<META, PROJ, S, 8, NT, H>(sp, st); break;
+    default: launch_split_r<META, PROJ, S, 4, NT, H>(sp, st); break;
   }
 }
 
-template <int META, int PROJ, int NT>
+template <int META, int PROJ, int NT, int H>
 void launch_split_meta(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.group) {
-    case 32: launch_split_s<META, PROJ, 1, NT>(sp, st); break;
-    case 64: launch_split_s<META, PROJ, 2, NT>(sp, st); break;
-    default: launch_split_s<META, PROJ, 4, NT>(sp, st); break;
+    case 32: launch_split_s<META, PROJ, 1, NT, H>(sp, st); break;
+    case 64: launch_split_s<META, PROJ, 2, NT, H>(sp, st); break;
+    default: launch_split_s<META, PROJ, 4, NT, H>(sp, st); break;
   }
 }
 
-// NT: activation terms (2 for fp32 activations, 1 for an exact bf16 input).
-template <int PROJ, int NT>
+// NT: activation terms (2 for fp32 activations, 1 for an exact bf16 input);
+// H: K ranges per work item (2 only with 512-column ranges).
+template <int PROJ, int NT, int H>
 void launch_split(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.meta_dtype) {
-    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ, NT>(sp, st); break;
-    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ, NT>(sp, st); break;
-    default: launch_split_meta<OSM_META_BF16, PROJ, NT>(sp, st); break;
+    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ, NT, H>(sp, st); break;
+    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ, NT, H>(sp, st); break;
+    default: launch_split_meta<OSM_META_BF16, PROJ, NT, H>(sp, st); break;
   }
 }
 
@@ -1243,12 +1272,24 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   sp.P = P;
   sp.max_tiles = static_cast<uint32_t>(max_tiles);
   sp.out = a->gu_part;
-  const uint32_t gu_splits = osmd_moe_grouped_splits(&g, D);
+  // With 512-column ranges a gate/up work item covers two consecutive
+  // ranges and writes one partial for both: half the partials written here
+  // and read back by the SwiGLU launch.
+  const uint32_t gu_ranges = osmd_moe_grouped_splits(&g, D);
+  const bool gu_pairs = range_cols(g, D) == 512u && gu_ranges % 2u == 0u;
+  const uint32_t gu_splits = gu_pairs ? gu_ranges / 2u : gu_ranges;
   set_item_blocks(sp, (I + split_rows<2>() - 1) / split_rows<2>(), gu_splits);
-  if (one_term)
-    launch_split<2, 1>(sp, st);
-  else
-    launch_split<2, kActSplit>(sp, st);
+  if (one_term) {
+    if (gu_pairs)
+      launch_split<2, 1, 2>(sp, st);
+    else
+      launch_split<2, 1, 1>(sp, st);
+  } else {
+    if (gu_pairs)
+      launch_split<2, kActSplit, 2>(sp, st);
+    else
+      launch_split<2, kActSplit, 1>(sp, st);
+  }
   const size_t hwords = static_cast<size_t>(P) * (I / 8u);
   swiglu_terms_kernel<<<blocks_for(hwords, 4096), 256, 0, st>>>(a->gu_part, gu_splits, P, I, G, a->h_terms,
                                                                 a->h_sums);
@@ -1258,7 +1299,7 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   sp.out = a->partial;
   const uint32_t dn_splits = osmd_moe_grouped_splits(&g, I);
   set_item_blocks(sp, (D + split_rows<1>() - 1) / split_rows<1>(), dn_splits);
-  launch_split<1, kActSplit>(sp, st);
+  launch_split<1, kActSplit, 1>(sp, st);
   const float* residual = (m.flags & OSMD_MOE_RESIDUAL) ? static_cast<const float*>(m.x) : nullptr;
   if (D % 4u == 0u && ((reinterpret_cast<uintptr_t>(m.y) | reinterpret_cast<uintptr_t>(residual)) & 15u) == 0u)
     combine4_kernel<<<blocks_for(static_cast<size_t>(T) * (D / 4u), 4096), 256, 0, st>>>(
