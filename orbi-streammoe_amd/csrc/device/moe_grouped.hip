@@ -465,6 +465,10 @@ constexpr uint32_t kXcds = 8;
 // two weight buffers alternate in straight-line code; a run past the last
 // row block loads clamped rows and stores nothing.
 constexpr uint32_t kItemBlocks = 4;
+// Row blocks per item when an item covers H K ranges: four ranges (all of a
+// 2048-column K) take two blocks, so that a tile still splits into as many
+// items and the persistent grid stays balanced.
+constexpr uint32_t item_blocks(int H) { return H >= 4 ? kItemBlocks / 2u : kItemBlocks; }
 // s_waitcnt operand: vector memory counter 0, the others at their maximum.
 constexpr int kWaitVmcnt0 = 0x0F70;
 struct SplitWork {
@@ -771,7 +775,10 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
   constexpr uint32_t kUnitCols = KS / 8u;  // 16-byte units per staged row
   constexpr uint32_t kUnitsPerThread = NT * kTileTokens * kUnitCols / kSplitThreads;
   static_assert(NT * kTileTokens * kUnitCols % kSplitThreads == 0, "staging units");
-  static_assert(H * GPR * kTileTokens <= kSplitThreads, "group sums: one per thread");
+  static_assert(H * GPR * kTileTokens % kSplitThreads == 0 || H * GPR * kTileTokens < kSplitThreads,
+                "group sums: whole passes of the workgroup");
+  constexpr uint32_t kSumPasses = (H * GPR * kTileTokens + kSplitThreads - 1u) / kSplitThreads;
+  constexpr uint32_t kIB = item_blocks(H);
   constexpr uint32_t kProjWaves = PROJ == 2 ? kSplitWaves / 2u : kSplitWaves;
   __shared__ __align__(16) SplitLds<PROJ, NSTEP, NT, H> lds;
 
@@ -854,11 +861,17 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     }
-    // Group sums: thread (sg, srow) for sg < H * GPR (range sg / GPR); the
-    // others load a valid element and do not store it.
-    const uint32_t sg = tid / kTileTokens, srow = tid % kTileTokens;
+    // Group sums: thread (sg, srow) for sg < H * GPR (range sg / GPR), in
+    // kSumPasses passes of the workgroup; the others load a valid element and
+    // do not store it.
+    const uint32_t srow = tid % kTileTokens;
     const uint32_t sarow = act_row(srow < rows ? srow : rows - 1u);
-    const float xsum = p.sums[static_cast<size_t>(sarow) * mx.ngroups + split * H * GPR + (sg < H * GPR ? sg : 0u)];
+    float xsum[kSumPasses];
+#pragma unroll
+    for (uint32_t ps = 0; ps < kSumPasses; ++ps) {
+      const uint32_t sg = (tid + ps * kSplitThreads) / kTileTokens;
+      xsum[ps] = p.sums[static_cast<size_t>(sarow) * mx.ngroups + split * H * GPR + (sg < H * GPR ? sg : 0u)];
+    }
 
     const uint32_t next = item + gridDim.x;
     const SplitWork wk_next = split_work(p, next);
@@ -876,7 +889,11 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
         *reinterpret_cast<uint4*>(&lds.a[0][term][row][cu * 8u]) = stage[i];
       }
     }
-    if (sg < H * GPR) lds.xs[sg / GPR][sg % GPR][srow] = xsum;
+#pragma unroll
+    for (uint32_t ps = 0; ps < kSumPasses; ++ps) {
+      const uint32_t sg = (tid + ps * kSplitThreads) / kTileTokens;
+      if (sg < H * GPR) lds.xs[sg / GPR][sg % GPR][srow] = xsum[ps];
+    }
     __syncthreads();
 
     // The item's blocks, straight-line, so that each wait is for exactly the
@@ -885,13 +902,13 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
     // scalars there. After the last block W0 loads the next item's first
     // block, or (no next item) this item's first block again, read and not
     // used.
-    // Sub-block sb is range half sb % H of block fb + sb / H; with H = 2 the
-    // two halves of a block are one pair of the loop and share its totals.
+    // Sub-block sb is range sb % H of block fb + sb / H; a block's H ranges
+    // are consecutive sub-blocks and share its totals.
     TileRec next_rec{blob, 0u, 0u};
-    constexpr uint32_t kSub = kItemBlocks * H;
+    constexpr uint32_t kSub = kIB * H;
+    f32x4 total[2];
 #pragma unroll
     for (uint32_t sb = 0; sb < kSub; sb += 2u) {
-      f32x4 total[2];
       const uint32_t b0 = fb + sb / H, h0 = sb % H, b1 = fb + (sb + 1u) / H, h1 = (sb + 1u) % H;
       load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, b1, split * H + h1, m, q);
       __builtin_amdgcn_sched_barrier(0);
@@ -1056,10 +1073,10 @@ uint32_t range_cols(const osm_expert_geometry& g, uint32_t K) {
   return 128u;
 }
 
-void set_item_blocks(SplitParams& sp, uint32_t row_blocks, uint32_t nsplit) {
+void set_item_blocks(SplitParams& sp, uint32_t row_blocks, uint32_t nsplit, uint32_t ib = kItemBlocks) {
   sp.nsplit = nsplit;
-  sp.item_blocks = kItemBlocks;
-  sp.chunks = (row_blocks + kItemBlocks - 1u) / kItemBlocks;
+  sp.item_blocks = ib;
+  sp.chunks = (row_blocks + ib - 1u) / ib;
   sp.items = split_items(sp.max_tiles, nsplit, sp.chunks);
 }
 
@@ -1275,12 +1292,18 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   // With 512-column ranges a gate/up work item covers two consecutive
   // ranges and writes one partial for both: half the partials written here
   // and read back by the SwiGLU launch.
+  // With one activation term the staged tile is half as large, and four
+  // ranges (a 2048-column K whole) fit: one partial per block.
   const uint32_t gu_ranges = osmd_moe_grouped_splits(&g, D);
   const bool gu_pairs = range_cols(g, D) == 512u && gu_ranges % 2u == 0u;
-  const uint32_t gu_splits = gu_pairs ? gu_ranges / 2u : gu_ranges;
-  set_item_blocks(sp, (I + split_rows<2>() - 1) / split_rows<2>(), gu_splits);
+  const bool gu_quads = one_term && gu_pairs && gu_ranges % 4u == 0u;
+  const uint32_t gu_h = gu_quads ? 4u : gu_pairs ? 2u : 1u;
+  const uint32_t gu_splits = gu_ranges / gu_h;
+  set_item_blocks(sp, (I + split_rows<2>() - 1) / split_rows<2>(), gu_splits, item_blocks(static_cast<int>(gu_h)));
   if (one_term) {
-    if (gu_pairs)
+    if (gu_quads)
+      launch_split<2, 1, 4>(sp, st);
+    else if (gu_pairs)
       launch_split<2, 1, 2>(sp, st);
     else
       launch_split<2, 1, 1>(sp, st);
