@@ -294,7 +294,7 @@ __device__ __forceinline__ void sort_lane(uint32_t* k, uint32_t* n) {
 
 // acc + v[0] + v[1] + ... + v[n-1] in order, each addition rounded to fp32,
 // v in LDS (16-byte aligned), n a multiple of 8 and the same in every lane.
-// Values go through two register batches of 32: the next batch's reads are
+// Values go through two register batches of 4 CB: the next batch's reads are
 // issued before the current batch's additions, so the chain of additions,
 // which cannot be shortened, is what is waited on.
 __device__ __forceinline__ float chain_add4(float4 q, float acc) {
@@ -305,32 +305,36 @@ __device__ __forceinline__ float chain_add4(float4 q, float acc) {
   acc = acc + q.w;
   return acc;
 }
-constexpr int kChainBatch = 8;  // float4 per batch
-__device__ __forceinline__ void chain_load(const float4* p, float4 (&r)[kChainBatch]) {
+// CB: float4 per batch (8, or 16 where registers allow: the selection
+// kernel, which runs one workgroup per token).
+template <int CB>
+__device__ __forceinline__ void chain_load(const float4* p, float4 (&r)[CB]) {
 #pragma unroll
-  for (int j = 0; j < kChainBatch; ++j) r[j] = p[j];
+  for (int j = 0; j < CB; ++j) r[j] = p[j];
 }
-__device__ __forceinline__ float chain_batch(const float4 (&r)[kChainBatch], float acc) {
+template <int CB>
+__device__ __forceinline__ float chain_batch(const float4 (&r)[CB], float acc) {
 #pragma unroll
-  for (int j = 0; j < kChainBatch; ++j) acc = chain_add4(r[j], acc);
+  for (int j = 0; j < CB; ++j) acc = chain_add4(r[j], acc);
   return acc;
 }
+template <int CB = 8>
 __device__ __forceinline__ float chain_sum(const float* v, uint32_t n, float acc) {
   const float4* v4 = reinterpret_cast<const float4*>(v);
-  const uint32_t nb = n / (4u * kChainBatch);
-  float4 a[kChainBatch], b[kChainBatch];
-  if (nb > 0u) chain_load(v4, a);
+  const uint32_t nb = n / (4u * CB);
+  float4 a[CB], b[CB];
+  if (nb > 0u) chain_load<CB>(v4, a);
   for (uint32_t k = 0; k < nb; k += 2u) {
     const bool b_used = k + 1u < nb;
-    if (b_used) chain_load(v4 + (k + 1u) * kChainBatch, b);
+    if (b_used) chain_load<CB>(v4 + (k + 1u) * CB, b);
     __builtin_amdgcn_sched_barrier(0);
-    acc = chain_batch(a, acc);
+    acc = chain_batch<CB>(a, acc);
     if (!b_used) break;
-    if (k + 2u < nb) chain_load(v4 + (k + 2u) * kChainBatch, a);
+    if (k + 2u < nb) chain_load<CB>(v4 + (k + 2u) * CB, a);
     __builtin_amdgcn_sched_barrier(0);
-    acc = chain_batch(b, acc);
+    acc = chain_batch<CB>(b, acc);
   }
-  for (uint32_t i = nb * 4u * kChainBatch; i < n; i += 8u) {
+  for (uint32_t i = nb * 4u * CB; i < n; i += 8u) {
     acc = chain_add4(v4[i / 4u], acc);
     acc = chain_add4(v4[i / 4u + 1u], acc);
   }
@@ -458,21 +462,126 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
   if (tid < nr) out.ex[out.cl[first + tid]] = acc;
 }
 
-template <int PER>
+// The same logits with the loads two steps ahead: router elements in two
+// register sets used on alternate steps, inputs loaded two steps before they
+// are staged, and additions in batches of 64. For the selection kernel (one
+// workgroup per token, registers to spare): a step is then the addition chain
+// rather than the producers' wait for their loads.
+template <int RD, int PER>
+__device__ void exact_logits_deep(const RouteView& rv, uint32_t t, Selection<PER>& out, uint32_t first, uint32_t nr,
+                                  float scale) {
+#pragma clang fp contract(off)
+  const uint32_t D = rv.hidden, tid = threadIdx.x;
+  const bool producer = tid >= kWave;
+  const uint32_t ptid = producer ? tid - kWave : 0u;
+  const uint32_t r = ptid % kExactRows, seg = (ptid / kExactRows) * 16u;
+  const bool active = producer && r < nr;
+  const uint32_t e = r < nr ? out.cl[first + r] : out.cl[first];
+  Q8Row qr{};
+  const uint8_t* row = nullptr;
+  if constexpr (RD == OSM_ROUTER_AFFINE_Q8)
+    qr = q8_row(rv.router, rv.expert_count, e, D, rv.router_group);
+  else
+    row = static_cast<const uint8_t*>(rv.router) + static_cast<size_t>(e) * D * (RD == OSM_META_F32 ? 4u : 2u);
+  struct W16 {
+    Raw8<RD> lo, hi;
+  };
+  struct X1 {
+    float x, nw;
+  };
+  auto fetch_w = [&](W16& w, uint32_t chunk) {
+    const uint32_t c = chunk * kExactCols + seg;
+    if (!active) return;
+    if (c < D) {
+      if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c, w.lo); else load_raw8<RD>(row, c, w.lo);
+    }
+    if (c + 8u < D) {
+      if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c + 8u, w.hi); else load_raw8<RD>(row, c + 8u, w.hi);
+    }
+  };
+  auto fetch_x = [&](X1& v, uint32_t chunk) {
+    if (!producer) return;
+    const uint32_t c = chunk * kExactCols + ptid;
+    v.x = load_x1(rv, t, c);
+    v.nw = (rv.rms && c < D) ? ldg<float>(rv.norm_weight + c) : 1.0f;
+  };
+  auto stage_x = [&](const X1& v, uint32_t buf) {
+    if (producer) out.xe[buf][ptid] = rv.rms ? v.x * (scale * v.nw) : v.x;
+  };
+  const uint32_t nchunks = (D + kExactCols - 1u) / kExactCols;
+  float acc = 0.0f;
+  // Step k: products of chunk k from w (loaded in step k - 2), w refilled
+  // with chunk k + 2; chunk k + 1's inputs staged from xs (loaded in step
+  // k - 2), xs refilled with chunk k + 3; lane r of wavefront 0 adds chunk
+  // k - 1.
+  auto step = [&](uint32_t k, W16& w, X1& xs) {
+    if (active && k < nchunks) {
+      float4* dst = reinterpret_cast<float4*>(&out.prod[k & 1u][r][seg]);
+      const float4* xe = reinterpret_cast<const float4*>(&out.xe[k & 1u][seg]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 x4 = xe[j];
+        const Raw8<RD>& h = j < 2 ? w.lo : w.hi;
+        const int o = 4 * (j % 2);
+        dst[j] = make_float4(raw8_get<RD>(h, o) * x4.x, raw8_get<RD>(h, o + 1) * x4.y,
+                             raw8_get<RD>(h, o + 2) * x4.z, raw8_get<RD>(h, o + 3) * x4.w);
+      }
+      if (k + 2u < nchunks) fetch_w(w, k + 2u);
+    }
+    if (k + 1u < nchunks) {
+      stage_x(xs, (k + 1u) & 1u);
+      if (k + 3u < nchunks) fetch_x(xs, k + 3u);
+    }
+    if (tid < nr && k > 0u) {
+      const uint32_t c0 = (k - 1u) * kExactCols;
+      acc = chain_sum<16>(out.prod[(k - 1u) & 1u][tid], D - c0 < kExactCols ? D - c0 : kExactCols, acc);
+    }
+    __syncthreads();
+  };
+  W16 wa{}, wb{};
+  X1 xa{}, xb{};
+  fetch_x(xa, 0);
+  fetch_w(wa, 0);
+  if (nchunks > 1u) fetch_w(wb, 1);
+  stage_x(xa, 0);
+  if (nchunks > 1u) fetch_x(xb, 1);
+  if (nchunks > 2u) fetch_x(xa, 2);
+  __syncthreads();
+  // Even steps stage odd chunks from xb, odd steps even chunks from xa.
+  for (uint32_t k = 0; k <= nchunks; k += 2u) {
+    step(k, wa, xb);
+    if (k + 1u <= nchunks) step(k + 1u, wb, xa);
+  }
+  if (tid < nr) out.ex[out.cl[first + tid]] = acc;
+}
+
+template <int PER, bool DEEP>
 __device__ void exact_logits(const RouteView& rv, uint32_t t, Selection<PER>& out, uint32_t first, uint32_t nr,
                              float scale) {
   switch (rv.router_dtype) {
-    case OSM_META_F32: exact_logits_rd<OSM_META_F32>(rv, t, out, first, nr, scale); break;
-    case OSM_META_F16: exact_logits_rd<OSM_META_F16>(rv, t, out, first, nr, scale); break;
-    case OSM_ROUTER_AFFINE_Q8: exact_logits_rd<OSM_ROUTER_AFFINE_Q8>(rv, t, out, first, nr, scale); break;
-    default: exact_logits_rd<OSM_META_BF16>(rv, t, out, first, nr, scale); break;
+    case OSM_META_F32:
+      if constexpr (DEEP) exact_logits_deep<OSM_META_F32>(rv, t, out, first, nr, scale);
+      else exact_logits_rd<OSM_META_F32>(rv, t, out, first, nr, scale);
+      break;
+    case OSM_META_F16:
+      if constexpr (DEEP) exact_logits_deep<OSM_META_F16>(rv, t, out, first, nr, scale);
+      else exact_logits_rd<OSM_META_F16>(rv, t, out, first, nr, scale);
+      break;
+    case OSM_ROUTER_AFFINE_Q8:
+      if constexpr (DEEP) exact_logits_deep<OSM_ROUTER_AFFINE_Q8>(rv, t, out, first, nr, scale);
+      else exact_logits_rd<OSM_ROUTER_AFFINE_Q8>(rv, t, out, first, nr, scale);
+      break;
+    default:
+      if constexpr (DEEP) exact_logits_deep<OSM_META_BF16>(rv, t, out, first, nr, scale);
+      else exact_logits_rd<OSM_META_BF16>(rv, t, out, first, nr, scale);
+      break;
   }
 }
 
 // The exact path (every thread of the workgroup; out.id/lg/bd hold the
 // device ranking). Rewrites out.id and out.lg; returns whether every expert
 // was recomputed. out.nunresolved gets the unresolved adjacent pairs.
-template <int PER>
+template <int PER, bool DEEP>
 __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[PER], const float (&b)[PER],
                              Selection<PER>& out, float mx) {
   const uint32_t E = rv.expert_count, k = rv.top_k;
@@ -514,7 +623,7 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
     }
     __syncthreads();
     for (uint32_t first = 0; first < nc; first += kExactRows)
-      exact_logits<PER>(rv, t, out, first, nc - first < kExactRows ? nc - first : kExactRows, scale);
+      exact_logits<PER, DEEP>(rv, t, out, first, nc - first < kExactRows ? nc - first : kExactRows, scale);
     __syncthreads();
     float lm = -INFINITY;
 #pragma unroll
@@ -719,7 +828,7 @@ __device__ __forceinline__ void rank_device(const RouteView& rv, const float (&l
 // thread of the workgroup calls it; it ends with a barrier, after which
 // out.id, out.p and out.flags are complete. `count`: add this selection to
 // the routing counters now (otherwise count_selection does it later).
-template <int PER>
+template <int PER, bool DEEP = false>
 __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, const float (&l)[PER],
                                               const float (&b)[PER], const uint8_t* const (&tab)[PER],
                                               Selection<PER>& out, bool count) {
@@ -781,7 +890,7 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
   bad = __syncthreads_or(bad) != 0;
   sum = ((out.red[2][0] + out.red[2][1]) + out.red[2][2]) + out.red[2][3];
   bool full = false;
-  if (bad) full = select_exact<PER>(rv, t, l, b, out, mx);
+  if (bad) full = select_exact<PER, DEEP>(rv, t, l, b, out, mx);
   if (tid < k) out.p[tid] = expf(out.lg[tid] - mx) / sum;
   if (tid == 0) out.flags = (bad ? 1u : 0u) | (full ? 2u : 0u);
   if (count && tid == 0 && rv.stats != nullptr) {
@@ -807,7 +916,7 @@ __device__ __forceinline__ void count_selection(const RouteView& rv, const Selec
 
 // Loads token t's logits and their bounds (and table pointers) and selects;
 // every thread of the workgroup calls it.
-template <int PER>
+template <int PER, bool DEEP = false>
 __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out, bool count) {
   const uint32_t E = rv.expert_count;
   const uint32_t D = rv.hidden;
@@ -859,7 +968,7 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
     for (uint32_t part = 1; part < rv.parts; ++part) g += pl[part * ps];
     rv.gate_out[t] = 1.0f / (1.0f + expf(-g));  // reference_ops.cpp:214-216
   }
-  select_values<PER>(rv, t, p, bnd, tab, out, count);
+  select_values<PER, DEEP>(rv, t, p, bnd, tab, out, count);
 }
 
 template <int PER>
@@ -896,7 +1005,7 @@ __device__ __forceinline__ void publish_selection(const RouteView& rv, uint32_t 
 template <int PER>
 __global__ __launch_bounds__(kSelThreads) void select_kernel(RouteView rv) {
   __shared__ Selection<PER> sel;
-  select_block<PER>(rv, blockIdx.x, sel, true);
+  select_block<PER, true>(rv, blockIdx.x, sel, true);
   publish_selection(rv, blockIdx.x, threadIdx.x, sel);
 }
 
