@@ -914,6 +914,10 @@ __device__ __forceinline__ void count_selection(const RouteView& rv, const Selec
   if (bad && s.nunresolved != 0u) atomicAdd(rv.stats + 3, s.nunresolved);
 }
 
+// Router GEMM planes summed with every load in flight first (up to 8 K
+// ranges: hidden 4096 at 512-column ranges; more take a loop).
+constexpr uint32_t kMaxPlanes = 8;
+
 // Loads token t's logits and their bounds (and table pointers) and selects;
 // every thread of the workgroup calls it.
 template <int PER, bool DEEP = false>
@@ -934,19 +938,44 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
       const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
       const size_t o = static_cast<size_t>(t) * (E + 1u) + e;
       const float* pl = rv.planes + o;
-      float v = pl[0];
-      float rs = 0.0f, as = 0.0f;
+      const bool bounded = rv.bound_planes != nullptr;
       const float cols = static_cast<float>(D / rv.parts);
-      if (rv.bound_planes != nullptr) {
-        rs = rv.bound_planes[o];
-        as = rv.bound_planes[ps + o];
-      }
-      for (uint32_t part = 1; part < rv.parts; ++part) {
-        if (rv.bound_planes != nullptr) {
-          rs += rv.bound_planes[2u * part * ps + o] + cols * fabsf(v);
-          as += rv.bound_planes[(2u * part + 1u) * ps + o];
+      float v, rs = 0.0f, as = 0.0f;
+      if (rv.parts <= kMaxPlanes) {
+        // Every plane's loads issued before the first addition.
+        float pv[kMaxPlanes], rb[kMaxPlanes], ab[kMaxPlanes];
+#pragma unroll
+        for (uint32_t part = 0; part < kMaxPlanes; ++part) {
+          if (part < rv.parts) {
+            pv[part] = pl[part * ps];
+            rb[part] = bounded ? rv.bound_planes[2u * part * ps + o] : 0.0f;
+            ab[part] = bounded ? rv.bound_planes[(2u * part + 1u) * ps + o] : 0.0f;
+          }
         }
-        v += pl[part * ps];
+        v = pv[0];
+        rs = rb[0];
+        as = ab[0];
+#pragma unroll
+        for (uint32_t part = 1; part < kMaxPlanes; ++part) {
+          if (part < rv.parts) {
+            rs += rb[part] + cols * fabsf(v);
+            as += ab[part];
+            v += pv[part];
+          }
+        }
+      } else {
+        v = pl[0];
+        if (bounded) {
+          rs = rv.bound_planes[o];
+          as = rv.bound_planes[ps + o];
+        }
+        for (uint32_t part = 1; part < rv.parts; ++part) {
+          if (bounded) {
+            rs += rv.bound_planes[2u * part * ps + o] + cols * fabsf(v);
+            as += rv.bound_planes[(2u * part + 1u) * ps + o];
+          }
+          v += pl[part * ps];
+        }
       }
       p[j] = v;
       // Per plane: rs bounds the sum of |prefix sums| in the reference's
