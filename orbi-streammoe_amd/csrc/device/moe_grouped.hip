@@ -326,6 +326,11 @@ static_assert(sizeof(Tile) == 16, "tile record");
 
 constexpr uint32_t kBucketThreads = 1024;
 constexpr uint32_t kMaxBuckets = OSMD_MAX_EXPERTS + 1u;
+// The scattered outputs (tile rows, pair weights) are assembled in LDS and
+// written out in order when they fit: 12,288 tile-row entries (768 tiles) and
+// 8,192 pairs, a 512-token chunk of top-10 + shared with room to spare.
+constexpr uint32_t kBucketStageRows = 12288;
+constexpr uint32_t kBucketStagePairs = 8192;
 
 __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t* __restrict__ ids, const float* __restrict__ weights, const float* __restrict__ shared_gate,
@@ -335,6 +340,9 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     uint32_t* __restrict__ tile_count, uint32_t max_tiles) {
   __shared__ uint32_t counts[kMaxBuckets], offsets[kMaxBuckets], cursor[kMaxBuckets], tbase[kMaxBuckets];
   __shared__ uint32_t wave_total[kBucketThreads / kWave];
+  __shared__ uint32_t s_rows[kBucketStageRows];
+  __shared__ float s_w[kBucketStagePairs];
+  __shared__ uint32_t s_tiles;
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const uint32_t nb = E + (nslot > k ? 1u : 0u);
   const uint32_t P = T * nslot;
@@ -383,7 +391,10 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
       }
     }
     if (pass == 1) {
-      if (tid == 0) *tile_count = all;
+      if (tid == 0) {
+        *tile_count = all;
+        s_tiles = all;
+      }
       // Tiles past the last real one are empty (count 0): the GEMM grids
       // span the whole capacity and their workgroups read only their tile.
       for (uint32_t t = all + tid; t < max_tiles; t += kBucketThreads) tiles[t] = Tile{fallback, 0u, 0u};
@@ -402,6 +413,8 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
       tiles[tbase[b] + s] = tl;
     }
   }
+  const uint32_t ntiles = s_tiles;  // written before the last scan's barrier
+  const bool stage = ntiles * kTileTokens <= kBucketStageRows && P <= kBucketStagePairs;
 #pragma unroll 4
   for (uint32_t i = tid; i < P; i += kBucketThreads) {
     const uint32_t t = i / nslot, j = i % nslot;
@@ -412,9 +425,23 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     }
     const uint32_t in_bucket = e == E ? t : atomicAdd(&cursor[e], 1u);
     const uint32_t pos = offsets[e] + in_bucket;
-    tile_rows[(tbase[e] + in_bucket / kTileTokens) * kTileTokens + in_bucket % kTileTokens] = t;
+    const uint32_t slot = (tbase[e] + in_bucket / kTileTokens) * kTileTokens + in_bucket % kTileTokens;
+    const float w = j < k ? weights[static_cast<size_t>(t) * k + j] : (shared_gate ? shared_gate[t] : 1.0f);
     pair_pos[i] = pos;
-    pair_w[pos] = j < k ? weights[static_cast<size_t>(t) * k + j] : (shared_gate ? shared_gate[t] : 1.0f);
+    if (stage) {
+      s_rows[slot] = t;
+      s_w[pos] = w;
+    } else {
+      tile_rows[slot] = t;
+      pair_w[pos] = w;
+    }
+  }
+  if (stage) {
+    // In order: entries of a tile past its count hold whatever LDS held
+    // (no GEMM reads them).
+    __syncthreads();
+    for (uint32_t i = tid; i < ntiles * kTileTokens; i += kBucketThreads) tile_rows[i] = s_rows[i];
+    for (uint32_t i = tid; i < P; i += kBucketThreads) pair_w[i] = s_w[i];
   }
 }
 
