@@ -697,8 +697,8 @@ template <int META, int PROJ, int S, int NSTEP, int NT, int H, uint32_t kWgRows>
 __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP, NT, H>& lds,
                                               const BlockWeights<META, S, NSTEP>& W, const WaveMatrix& mx,
                                               uint32_t block, uint32_t split, uint32_t half, bool first, bool last,
-                                              f32x4 (&total)[2], uint32_t start, uint32_t rows, uint32_t pr,
-                                              uint32_t m, uint32_t q) {
+                                              f32x4 (&total)[2], const float (&pw4)[4], uint32_t start,
+                                              uint32_t rows, uint32_t pr, uint32_t m, uint32_t q) {
   constexpr int GPR = NSTEP / S;
   constexpr uint32_t G8 = (32u * S) / 8u;  // 16-byte units per group
   // The tile row indices pass through an opaque copy per block: every block
@@ -782,7 +782,7 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
         if constexpr (PROJ == 2)
           p.out[((static_cast<size_t>(split) * 2u + pr) * p.P + pair) * mx.N + r] = total[nb][j];
         else
-          p.out[(static_cast<size_t>(split) * p.P + pair) * mx.N + r] = p.pair_w[pair] * total[nb][j];
+          p.out[(static_cast<size_t>(split) * p.P + pair) * mx.N + r] = pw4[j] * total[nb][j];
       }
     }
   }
@@ -900,6 +900,14 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
       xsum[ps] = p.sums[static_cast<size_t>(sarow) * mx.ngroups + split * H * GPR + (sg < H * GPR ? sg : 0u)];
     }
 
+    // down: the pair weights of this lane's four D rows (tile rows 4q..4q+3,
+    // clamped), loaded with the staging. Loaded per block instead, each would
+    // wait for every older load -- the next block's weights included.
+    float pw4[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (PROJ == 1) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pw4[j] = p.pair_w[start + (4u * q + j < rows ? 4u * q + j : rows - 1u)];
+    }
     const uint32_t next = item + gridDim.x;
     const SplitWork wk_next = split_work(p, next);
     const TileView tl_next = next < p.items ? fetch_tile<PROJ>(p, wk_next, m) : TileView{nullptr, 0u, 0u, 0u};
@@ -940,7 +948,7 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
       load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, b1, split * H + h1, m, q);
       __builtin_amdgcn_sched_barrier(0);
       compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows>(p, lds, W0, mx, b0, split, h0, h0 == 0u, h0 == H - 1u,
-                                                         total, start, rows, pr, m, q);
+                                                         total, pw4, start, rows, pr, m, q);
       if (sb == 0u) next_rec = uniform_rec(tl_next);
       const bool last = sb + 2u >= kSub;
       const bool has_next = next_rec.count != 0u;
@@ -950,7 +958,7 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
                                           last ? (has_next ? wk_next.split * H : split * H) : split * H + h2, m, q);
       __builtin_amdgcn_sched_barrier(0);
       compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows>(p, lds, W1, mx, b1, split, h1, h1 == 0u, h1 == H - 1u,
-                                                         total, start, rows, pr, m, q);
+                                                         total, pw4, start, rows, pr, m, q);
     }
     __syncthreads();  // the LDS tile is restaged by the next item
     item = next;
