@@ -1068,6 +1068,16 @@ __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, floa
     xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   if (a.flags & OSMD_MOE_RMSNORM) {
+    // The norm weights are loaded with x, before the reduction: loaded after
+    // it, each load waited behind the previous chunk's x_norm store (vector
+    // memory operations are counted in order).
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_weight);
+    float4 nwv[kX4PerThread];
+#pragma unroll
+    for (int u = 0; u < kX4PerThread; ++u) {
+      const uint32_t i = tid + u * 256u;
+      nwv[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < kX4PerThread; ++u)
@@ -1079,12 +1089,11 @@ __device__ __forceinline__ void stage_x(const osmd_moe_args& a, uint32_t t, floa
 #pragma unroll
     for (int w2 = 0; w2 < kRouteWaves; ++w2) tot += red[w2];
     const float scale = 1.0f / sqrtf(tot / static_cast<float>(D) + a.rms_eps);
-    const float4* w4 = reinterpret_cast<const float4*>(a.norm_weight);
 #pragma unroll
     for (int u = 0; u < kX4PerThread; ++u) {
       const uint32_t i = tid + u * 256u;
       if (i < n4) {
-        const float4 nw = w4[i];
+        const float4 nw = nwv[u];
         xv[u].x = xv[u].x * (scale * nw.x);
         xv[u].y = xv[u].y * (scale * nw.y);
         xv[u].z = xv[u].z * (scale * nw.z);
