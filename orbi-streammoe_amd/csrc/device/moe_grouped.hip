@@ -203,7 +203,7 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
 // Plane 2p + 0 gets the sum over steps of 32 (|before| + a) + |after|,
 // plane 2p + 1 the sum of a; the selection adds R |start of the range| for
 // each range and scales the total.
-template <int NS, int NSTEP>
+template <int NS, int NSTEP, int TT>
 __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
     const uint16_t* __restrict__ terms, uint32_t T, uint32_t D, const uint16_t* __restrict__ router,
     const uint16_t* __restrict__ shared_gate_vec, uint32_t E, float* __restrict__ planes,
@@ -214,54 +214,50 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
   constexpr uint32_t kUnitsPerThread = NS * kTileTokens * kUnitCols / kGroupedThreads;
   static_assert(NS * kTileTokens * kUnitCols % kGroupedThreads == 0, "staging units");
   __shared__ __align__(16) uint16_t a_lds[NS][kTileTokens][RS];
+  __shared__ float xn_lds[kTileTokens][NSTEP];
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const uint32_t t0 = blockIdx.y * kTileTokens, k0 = blockIdx.z * R;
+  const uint32_t k0 = blockIdx.z * R;
   const uint32_t nrows = E + (shared_gate_vec ? 1u : 0u);
   const uint32_t m = lane % 16u, q = lane / 16u;
   const uint32_t row = (blockIdx.x * kGroupedWaves + wave) * kBlockRows + m;
   const uint32_t rr = row < nrows ? row : nrows - 1u;
   const uint16_t* wrow = (rr < E ? router + static_cast<size_t>(rr) * D : shared_gate_vec) + k0;
+  const bool bounds = bplanes != nullptr;
 
-  // 1. B: this wave's router values for the range; then the tile's terms
-  // (unit u: term u / (16 * R/8), token row (u / (R/8)) % 16, 16-byte column
-  // unit u % (R/8); rows past T load the last token).
+  // 1. B: this wave's router values for the range, kept for all TT token
+  // tiles of the workgroup; then the first tile's terms (unit u: term u /
+  // (16 * R/8), token row (u / (R/8)) % 16, 16-byte column unit u % (R/8);
+  // rows past T load the last token).
   uint4 raw[NSTEP];
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) raw[st] = ldg16(wrow + 32u * st + 8u * q);
-  const bool bounds = bplanes != nullptr;
-  __shared__ float xn_lds[kTileTokens][NSTEP];
   float wn[NSTEP];
   if (bounds) {
     const float* rn = rnorm + static_cast<size_t>(rr) * (D / 32u) + k0 / 32u;
 #pragma unroll
     for (int st = 0; st < NSTEP; ++st) wn[st] = rn[st];
-    if (tid < kTileTokens * NSTEP) {
-      const uint32_t r = tid / NSTEP, st = tid % NSTEP;
-      const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
-      xn_lds[r][st] = xnorm[static_cast<size_t>(tok) * (D / 32u) + k0 / 32u + st];
-    }
   }
   uint4 stage[kUnitsPerThread];
+  float xn = 0.0f;
+  auto fetch = [&](uint32_t t0) {
 #pragma unroll
-  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
-    const uint32_t u = tid + i * kGroupedThreads;
-    const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
-    const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
-    stage[i] = ldg16(terms + (static_cast<size_t>(tok) * NS + term) * D + k0 + cu * 8u);
-  }
-#pragma unroll
-  for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
-    const uint32_t u = tid + i * kGroupedThreads;
-    const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
-    *reinterpret_cast<uint4*>(&a_lds[term][r][cu * 8u]) = stage[i];
-  }
-  __syncthreads();
+    for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+      const uint32_t u = tid + i * kGroupedThreads;
+      const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+      const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
+      stage[i] = ldg16(terms + (static_cast<size_t>(tok) * NS + term) * D + k0 + cu * 8u);
+    }
+    if (bounds && tid < kTileTokens * NSTEP) {
+      const uint32_t r = tid / NSTEP, st = tid % NSTEP;
+      const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
+      xn = xnorm[static_cast<size_t>(tok) * (D / 32u) + k0 / 32u + st];
+    }
+  };
+  const uint32_t tile0 = blockIdx.y * TT;
+  fetch(tile0 * kTileTokens);
 
-  // 2. MFMAs: A = token m's terms at k0 + 32 st + 8q (word order), B = 8
-  // router values of row rr reordered to word order. Each step starts from
-  // zero, smallest term first; its sum joins the running sums in fp32.
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float rp[4] = {0.f, 0.f, 0.f, 0.f}, ap[4] = {0.f, 0.f, 0.f, 0.f};
+  // B operands: 8 router values of row rr in word order per step.
+  bf16x8 bop[NSTEP];
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) {
     const uint32_t h4[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
@@ -276,34 +272,60 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
     bv.y = h[word_k(2)] | (static_cast<uint32_t>(h[word_k(3)]) << 16);
     bv.z = h[word_k(4)] | (static_cast<uint32_t>(h[word_k(5)]) << 16);
     bv.w = h[word_k(6)] | (static_cast<uint32_t>(h[word_k(7)]) << 16);
-    const bf16x8 b = as_operand(bv);
-    f32x4 part = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = NS - 1; t >= 0; --t)
-      part = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * st + 8u * q])), b, part);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float before = acc[j];
-      acc[j] = before + part[j];
-      if (bounds) {
-        const float a = wn[st] * xn_lds[4u * q + j][st];
-        rp[j] += 32.0f * (fabsf(before) + a) + fabsf(acc[j]);
-        ap[j] += a;
-      }
-    }
+    bop[st] = as_operand(bv);
   }
 
-  // 3. Plane blockIdx.z, [T][E + 1] (column E: the shared gate, when there is
-  // one): D rows 4q + j are tokens, column m the router row.
+#pragma unroll 1
+  for (uint32_t tt = 0; tt < TT; ++tt) {
+    const uint32_t t0 = (tile0 + tt) * kTileTokens;
+    if (t0 >= T) break;  // workgroup-uniform
+    if (tt > 0u) __syncthreads();  // the previous tile's LDS operands are read
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint32_t t = t0 + 4u * q + j;
-    if (t < T && row < nrows) {
-      planes[(static_cast<size_t>(blockIdx.z) * T + t) * (E + 1u) + row] = acc[j];
-      if (bounds) {
-        const size_t ps = static_cast<size_t>(T) * (E + 1u);
-        bplanes[2u * blockIdx.z * ps + static_cast<size_t>(t) * (E + 1u) + row] = rp[j];
-        bplanes[(2u * blockIdx.z + 1u) * ps + static_cast<size_t>(t) * (E + 1u) + row] = ap[j];
+    for (uint32_t i = 0; i < kUnitsPerThread; ++i) {
+      const uint32_t u = tid + i * kGroupedThreads;
+      const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
+      *reinterpret_cast<uint4*>(&a_lds[term][r][cu * 8u]) = stage[i];
+    }
+    if (bounds && tid < kTileTokens * NSTEP) xn_lds[tid / NSTEP][tid % NSTEP] = xn;
+    __syncthreads();
+    // The next tile's terms are in flight while this one computes.
+    if (tt + 1u < TT && t0 + kTileTokens < T) fetch(t0 + kTileTokens);
+
+    // 2. MFMAs: A = token m's terms at k0 + 32 st + 8q (word order), B = 8
+    // router values of row rr. Each step starts from zero, smallest term
+    // first; its sum joins the running sums in fp32.
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    float rp[4] = {0.f, 0.f, 0.f, 0.f}, ap[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < NSTEP; ++st) {
+      f32x4 part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = NS - 1; t >= 0; --t)
+        part = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * st + 8u * q])), bop[st], part);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float before = acc[j];
+        acc[j] = before + part[j];
+        if (bounds) {
+          const float a = wn[st] * xn_lds[4u * q + j][st];
+          rp[j] += 32.0f * (fabsf(before) + a) + fabsf(acc[j]);
+          ap[j] += a;
+        }
+      }
+    }
+
+    // 3. Plane blockIdx.z, [T][E + 1] (column E: the shared gate, when there
+    // is one): D rows 4q + j are tokens, column m the router row.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t t = t0 + 4u * q + j;
+      if (t < T && row < nrows) {
+        planes[(static_cast<size_t>(blockIdx.z) * T + t) * (E + 1u) + row] = acc[j];
+        if (bounds) {
+          const size_t ps = static_cast<size_t>(T) * (E + 1u);
+          bplanes[2u * blockIdx.z * ps + static_cast<size_t>(t) * (E + 1u) + row] = rp[j];
+          bplanes[(2u * blockIdx.z + 1u) * ps + static_cast<size_t>(t) * (E + 1u) + row] = ap[j];
+        }
       }
     }
   }
@@ -1179,24 +1201,38 @@ void launch_split(const SplitParams& sp, hipStream_t st) {
   }
 }
 
+// A workgroup covers TT consecutive 16-token tiles with the same router rows
+// (read once): TT = 2 from 256 tokens, where the grid still holds more than
+// two workgroups per compute unit.
+constexpr uint32_t kRouterTilesPerGroupFrom = 256;
+template <int NS, int TT>
+void launch_router_gemm_tt(uint32_t rcols, dim3 grid, hipStream_t st, const uint16_t* terms, uint32_t T,
+                           uint32_t D, const uint16_t* router, const uint16_t* sgv, uint32_t E, float* planes,
+                           const float* rnorm, const float* xnorm, float* bplanes) {
+  grid.y = (grid.y + TT - 1u) / TT;
+  switch (rcols) {
+    case 512:
+      router_gemm_kernel<NS, 16, TT><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm,
+                                                                       xnorm, bplanes);
+      break;
+    case 256:
+      router_gemm_kernel<NS, 8, TT><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm,
+                                                                      xnorm, bplanes);
+      break;
+    default:
+      router_gemm_kernel<NS, 4, TT><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm,
+                                                                      xnorm, bplanes);
+      break;
+  }
+}
 template <int NS>
 void launch_router_gemm(uint32_t rcols, dim3 grid, hipStream_t st, const uint16_t* terms, uint32_t T, uint32_t D,
                         const uint16_t* router, const uint16_t* sgv, uint32_t E, float* planes, const float* rnorm,
                         const float* xnorm, float* bplanes) {
-  switch (rcols) {
-    case 512:
-      router_gemm_kernel<NS, 16><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm, xnorm,
-                                                                   bplanes);
-      break;
-    case 256:
-      router_gemm_kernel<NS, 8><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm, xnorm,
-                                                                  bplanes);
-      break;
-    default:
-      router_gemm_kernel<NS, 4><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm, xnorm,
-                                                                  bplanes);
-      break;
-  }
+  if (T >= kRouterTilesPerGroupFrom)
+    launch_router_gemm_tt<NS, 2>(rcols, grid, st, terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes);
+  else
+    launch_router_gemm_tt<NS, 1>(rcols, grid, st, terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes);
 }
 
 unsigned blocks_for(size_t n, unsigned cap) {
