@@ -102,9 +102,9 @@ __global__ void widen_bf16_kernel(const uint16_t* __restrict__ x, size_t n, floa
 // prepare: rows [R, K] (fp32, or bf16 when XBF16) -> terms [R][NS][K] bf16 in
 // word order and sums [R][K/G] of the values the first two terms represent
 // (the expert GEMMs read terms 0 and 1 of this layout; the router GEMM reads
-// all three when NS = 3). A bf16 input needs one term (NS = 1): it is exact. One thread per (row, 8-column word); the G/8
-// threads of a group are adjacent lanes of one wavefront and add their sums
-// by butterfly.
+// all three when NS = 3). A bf16 input needs one term (NS = 1): it is exact.
+// One thread per (row, 8-column word); the G/8 threads of a group are
+// adjacent lanes of one wavefront and add their sums by butterfly.
 template <bool XBF16, int NS>
 __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t K, uint32_t G,
                                uint16_t* __restrict__ terms, float* __restrict__ sums,
@@ -470,16 +470,16 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
 // ---------------------------------------------------------------------------
 // Grouped q4 GEMMs over the tile list, split along K.
 //
-// A work item is one tile (<= 16 pairs), one K range of KS = 32 * NSTEP
-// columns and a run of item_blocks consecutive row blocks; a workgroup of 4
-// waves works through items b, b + grid, ... (persistent, one grid of as
+// A work item is one tile (<= 16 pairs), H consecutive K ranges of KS = 32 *
+// NSTEP columns and a run of item_blocks consecutive row blocks; a workgroup
+// of 4 waves works through items b, b + grid, ... (persistent, one grid of as
 // many workgroups as are resident). Per item it stages the tile's activation
-// terms for the range into LDS once (rows past the tile's count are not
-// staged: MFMA rows read the last real row instead), then streams the row
-// blocks' weights with one block in flight ahead of the one being computed:
-// the packed words and metadata of block i+1 (the next item's first block,
-// after the last) are issued before block i's MFMAs. A block is 32 weight
-// rows per wave:
+// terms for its ranges into LDS once (rows past the tile's count are not
+// staged: MFMA rows read the last real row instead), then streams the
+// (block, range) sub-blocks' weights with one in flight ahead of the one
+// being computed: the packed words and metadata of sub-block i+1 (the next
+// item's first, after the last) are issued before sub-block i's MFMAs. A
+// block's totals carry over its H ranges. A block is 32 weight rows per wave:
 //   gate/up: 64 rows per workgroup; waves 0-1 gate, waves 2-3 up, 32 rows
 //            each; part[split][proj][pair][row] partial sums.
 //   down:    128 rows per workgroup (32 per wave), times the pair weight;
@@ -496,8 +496,8 @@ struct SplitParams {
   const Tile* tiles;
   uint32_t P;
   uint32_t max_tiles;   // tile capacity of the workspace
-  uint32_t nsplit;      // K ranges
-  uint32_t item_blocks; // row blocks per item (kItemBlocks)
+  uint32_t nsplit;      // partials per row: K ranges / H
+  uint32_t item_blocks; // row blocks per item (item_blocks(H))
   uint32_t chunks;      // items per tile and K range
   uint32_t items;       // tiles (rounded to whole XCD rounds) x K ranges x chunks
   float* out;
