@@ -82,6 +82,49 @@ def test_grouped_small_f32_meta_f32_router_no_shared(ctx):
         assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
 
 
+@pytest.mark.parametrize("G", [32, 128])
+def test_grouped_hidden_2048_group_sizes(ctx, G):
+    # Hidden 2048 at groups 32 and 128: group 128 keeps 512-column K ranges,
+    # which gate/up covers two per work item (fp32 decode) or two with one
+    # bf16 term (prefill); group 32 takes 256-column ranges, one per item.
+    # The grouped decode and the bf16 prefill against the per-token path
+    # (ids equal, outputs within 2e-5) and a sample against the oracle.
+    rng = np.random.default_rng(46 + G)
+    D, I, E, k, T = 2048, 512, 48, 6, 40
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    blobs = [random_blob(rng, D, I, G, O.META_BF16)[0] for _ in range(E)]
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blobs[e])
+    router_f = rng.normal(0, 0.9 / np.sqrt(D), (E, D)).astype(np.float32)
+    u = router_f.view(np.uint32)
+    router = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    router_f = O.bf16_bits_to_f32(router)
+    moe = osm_hip.MoeLayer(ctx, g, E, k, router, osm_hip.BF16, max_tokens=T)
+    x = rng.normal(0, 1, (T, D)).astype(np.float32)
+    moe.set_path(osm_hip.PATH_GROUPED)
+    gpu = moe.run_slab(slab, 0, x)
+    moe.set_path(osm_hip.PATH_PER_TOKEN)
+    per_token = moe.run_slab(slab, 0, x)
+    assert np.array_equal(gpu["ids"], per_token["ids"])
+    assert rel_l2(gpu["out"], per_token["out"]) <= 2e-5
+    for t in range(0, T, 13):
+        ora = O.qwen_sparse_moe(x[t], router_f, blobs, None, None, D, I, G, O.META_BF16, k)
+        assert np.array_equal(gpu["ids"][t], ora["ids"])
+        assert rel_l2(gpu["out"][t], ora["out"]) <= 1e-3
+    # The same tokens rounded to bf16 as a prefill chunk.
+    bits = ((x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    xw = (bits.astype(np.uint32) << 16).view(np.float32)
+    xb, y = ctx.alloc(T * D * 2), ctx.alloc(T * D * 4)
+    xb.upload(bits)
+    moe.prefill_device(slab, 0, xb.ptr, y.ptr, T)
+    got = y.download(np.float32, T * D).reshape(T, D)
+    ref = moe.run_slab(slab, 0, xw)
+    assert np.array_equal(moe.routing(T)["ids"], ref["ids"])
+    for t in range(T):
+        assert rel_l2(got[t], ref["out"][t]) <= 2e-5, t
+
+
 def test_grouped_router_gemm_planes_no_shared(ctx):
     # 96 fp32 tokens (more than 16: the router runs as the MFMA GEMM) with a
     # bf16 router at hidden 768 (three 256-column K planes that the selection
