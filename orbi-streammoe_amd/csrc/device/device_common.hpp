@@ -10,6 +10,20 @@ namespace osmk {
 
 constexpr int kWave = 64;
 
+// ---- router GEMM bounds -----------------------------------------------------
+// Per K range of the MFMA router GEMM, a logit's bound plane holds
+// sum_i (32 (|s_{i-1}| + a_i) + |s_i|) + c(D) sum_i a_i over its 32-column
+// steps i, s_i the fp32 running sum after step i (s_0 = 0) and a_i the step's
+// |w_chunk| |x_chunk|: the reference's 32 partial sums within a step are at
+// most 32 (|s_{i-1}| + a_i), adding a step sum errs by at most u |s_i|, and
+// c(D) = 112 + D^2 u (u = 2^-24) covers the MFMAs' own rounding (66 u of the
+// operands' absolute sum per step) and the reference's rounded products.
+// The selection adds R |running sum at the start| for every range after the
+// first and scales the total by (1 + 2^-9) u.
+__device__ __forceinline__ float router_gemm_bound_coef(uint32_t hidden) {
+  return 112.0f + static_cast<float>(hidden) * static_cast<float>(hidden) * 0x1p-24f;
+}
+
 // ---- metadata widening (bf16 -> f32 is a 16-bit shift, f16 -> f32 exact) --
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
   return __uint_as_float(bits << 16);

@@ -55,7 +55,7 @@ struct RouteView {
   const float* logits;                // [B, E]
   const float* bounds;                // [B, E] bound of each logit, or null (no bound: exact path)
   const float* planes;                // null, or `parts` planes [B][E + 1] of partial sums
-  const float* bound_planes;          // with planes: [parts][2][B][E + 1] bound parts, or null
+  const float* bound_planes;          // with planes: [parts][B][E + 1] bound parts, or null
   uint32_t parts, tokens;
   float* logits_out;                  // [B, E]  with planes: the summed logits
   float* gate_out;                    // [B]     with planes: the shared gate
@@ -940,49 +940,38 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
       const float* pl = rv.planes + o;
       const bool bounded = rv.bound_planes != nullptr;
       const float cols = static_cast<float>(D / rv.parts);
-      float v, rs = 0.0f, as = 0.0f;
+      float v, rs = 0.0f;
       if (rv.parts <= kMaxPlanes) {
         // Every plane's loads issued before the first addition.
-        float pv[kMaxPlanes], rb[kMaxPlanes], ab[kMaxPlanes];
+        float pv[kMaxPlanes], rb[kMaxPlanes];
 #pragma unroll
         for (uint32_t part = 0; part < kMaxPlanes; ++part) {
           if (part < rv.parts) {
             pv[part] = pl[part * ps];
-            rb[part] = bounded ? rv.bound_planes[2u * part * ps + o] : 0.0f;
-            ab[part] = bounded ? rv.bound_planes[(2u * part + 1u) * ps + o] : 0.0f;
+            rb[part] = bounded ? rv.bound_planes[part * ps + o] : 0.0f;
           }
         }
         v = pv[0];
         rs = rb[0];
-        as = ab[0];
 #pragma unroll
         for (uint32_t part = 1; part < kMaxPlanes; ++part) {
           if (part < rv.parts) {
             rs += rb[part] + cols * fabsf(v);
-            as += ab[part];
             v += pv[part];
           }
         }
       } else {
         v = pl[0];
-        if (bounded) {
-          rs = rv.bound_planes[o];
-          as = rv.bound_planes[ps + o];
-        }
+        if (bounded) rs = rv.bound_planes[o];
         for (uint32_t part = 1; part < rv.parts; ++part) {
-          if (bounded) {
-            rs += rv.bound_planes[2u * part * ps + o] + cols * fabsf(v);
-            as += rv.bound_planes[(2u * part + 1u) * ps + o];
-          }
+          if (bounded) rs += rv.bound_planes[part * ps + o] + cols * fabsf(v);
           v += pl[part * ps];
         }
       }
       p[j] = v;
-      // Per plane: rs bounds the sum of |prefix sums| in the reference's
-      // order, as bounds the sum of |w x|, which the GEMM's own rounding
-      // and the reference's products are proportional to.
-      const float cA = 112.0f + static_cast<float>(D) * static_cast<float>(D) * 0x1p-24f;
-      bnd[j] = rv.bound_planes != nullptr ? kBoundSlack * 0x1p-24f * (rs + cA * as) : INFINITY;
+      // Per plane: the GEMM's bound part (router_gemm_bound_coef), plus R
+      // |P_r| for the prefix sums of range r, which start at P_r.
+      bnd[j] = bounded ? kBoundSlack * 0x1p-24f * rs : INFINITY;
       if (base + j < E) rv.logits_out[static_cast<size_t>(t) * E + e] = v;
     } else {
       p[j] = lg[e];

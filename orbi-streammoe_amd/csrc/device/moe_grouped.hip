@@ -179,16 +179,24 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
 // Router GEMM: partial logits [T, E] and, as column E, the shared-gate dot
 // w_sg . x, one plane per K range (the selection adds the planes in order
 // and applies the sigmoid). A workgroup is 16 tokens x 64 router rows (4
-// waves x 16, bf16) x one K range of R = 32 * NSTEP columns. The tile's
-// activation terms are staged in LDS once and read by all four waves; each
-// wave's router values for the range are loaded before the staging, so both
-// streams are in flight together. Splitting K keeps a workgroup's reads small
-// (48 KB of terms, 64 KB of router rows at R = 512) and the grid large; a
-// wave that read its own copy of the terms, over all of K, moved 4x more
-// bytes through L2 than the tile holds.
+// waves x 16, bf16) x one K range of R = 32 * NSTEP columns, for TT
+// consecutive token tiles. The tile's activation terms are staged in LDS once
+// and read by all four waves; each wave's router values for the range are
+// loaded before the staging, so both streams are in flight together.
+// Splitting K keeps a workgroup's reads small (48 KB of terms, 64 KB of
+// router rows at R = 512) and the grid large; a wave that read its own copy
+// of the terms, over all of K, moved 4x more bytes through L2 than the tile
+// holds.
 //
-// Every logit plane also gets the parts of its bound on the distance from
-// the reference's sequentially summed logit (bplanes, when set;
+// The launch is one-dimensional and a multiple of 8 long. Workgroup L runs on
+// XCD L % 8 (workgroups are dispatched to the XCDs round-robin) and takes
+// item (L % 8) * (launch / 8) + L / 8 of the (router block, token group, K
+// range) items in K-range-major order, so an XCD's workgroups share a run of
+// one K range's router rows and token tiles in that XCD's L2 instead of every
+// XCD reading all of the router and all of the terms.
+//
+// Every logit plane also gets its part of the bound on the distance from
+// the reference's sequentially summed logit (bplanes, when BOUNDS;
 // reference_ops.cpp:85-93). Per 32-column step the MFMAs start from zero
 // (smallest term first) and the step sums are added in fp32, so with u =
 // 2^-24 and a the step's sum |w| |x| (at most |w_chunk| |x_chunk|, the
@@ -200,29 +208,39 @@ __global__ void prepare_kernel(const void* __restrict__ x, uint32_t R, uint32_t 
 //  - adding the step sums errs by at most u |running sum| per step;
 //  - the reference's 32 partial sums within the step are at most
 //    32 (|running sum before it| + a).
-// Plane 2p + 0 gets the sum over steps of 32 (|before| + a) + |after|,
-// plane 2p + 1 the sum of a; the selection adds R |start of the range| for
-// each range and scales the total.
-template <int NS, int NSTEP, int TT>
+// Bound plane p gets sum over steps of 32 (|before| + a) + |after| +
+// router_gemm_bound_coef(D) a, evaluated as 33 (|s_1| + ... + |s_{n-1}|) +
+// |s_n| + (32 + coef) (sum of a), s_i the running sum after step i (s_0 =
+// 0). The selection adds R |start of the range| for each range after the
+// first and scales the total.
+// The steps' MFMAs are independent (each starts from zero), so a batch of
+// them is issued before their sums join the running sums in step order.
+template <int NS, int NSTEP, int TT, bool BOUNDS>
 __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
     const uint16_t* __restrict__ terms, uint32_t T, uint32_t D, const uint16_t* __restrict__ router,
     const uint16_t* __restrict__ shared_gate_vec, uint32_t E, float* __restrict__ planes,
-    const float* __restrict__ rnorm, const float* __restrict__ xnorm, float* __restrict__ bplanes) {
+    const float* __restrict__ rnorm, const float* __restrict__ xnorm, float* __restrict__ bplanes, uint32_t gx,
+    uint32_t gy, uint32_t gz) {
   constexpr uint32_t R = 32u * NSTEP;
   constexpr uint32_t RS = R + 8u;  // LDS row stride (bf16), padded against bank conflicts
   constexpr uint32_t kUnitCols = R / 8u;
   constexpr uint32_t kUnitsPerThread = NS * kTileTokens * kUnitCols / kGroupedThreads;
+  constexpr int kBatch = 4;  // steps whose MFMAs are issued together
   static_assert(NS * kTileTokens * kUnitCols % kGroupedThreads == 0, "staging units");
+  static_assert(NSTEP % 4 == 0, "input norms read four steps at a time");
   __shared__ __align__(16) uint16_t a_lds[NS][kTileTokens][RS];
-  __shared__ float xn_lds[kTileTokens][NSTEP];
+  __shared__ __align__(16) float xn_lds[kTileTokens][NSTEP];
+  const uint32_t n8 = gridDim.x / 8u;
+  const uint32_t item = (blockIdx.x % 8u) * n8 + blockIdx.x / 8u;
+  if (item >= gx * gy * gz) return;  // the launch's padding (workgroup-uniform, before any barrier)
+  const uint32_t bx = item % gx, by = (item / gx) % gy, bz = item / (gx * gy);
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const uint32_t k0 = blockIdx.z * R;
+  const uint32_t k0 = bz * R;
   const uint32_t nrows = E + (shared_gate_vec ? 1u : 0u);
   const uint32_t m = lane % 16u, q = lane / 16u;
-  const uint32_t row = (blockIdx.x * kGroupedWaves + wave) * kBlockRows + m;
+  const uint32_t row = (bx * kGroupedWaves + wave) * kBlockRows + m;
   const uint32_t rr = row < nrows ? row : nrows - 1u;
   const uint16_t* wrow = (rr < E ? router + static_cast<size_t>(rr) * D : shared_gate_vec) + k0;
-  const bool bounds = bplanes != nullptr;
 
   // 1. B: this wave's router values for the range, kept for all TT token
   // tiles of the workgroup; then the first tile's terms (unit u: term u /
@@ -232,7 +250,7 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
 #pragma unroll
   for (int st = 0; st < NSTEP; ++st) raw[st] = ldg16(wrow + 32u * st + 8u * q);
   float wn[NSTEP];
-  if (bounds) {
+  if constexpr (BOUNDS) {
     const float* rn = rnorm + static_cast<size_t>(rr) * (D / 32u) + k0 / 32u;
 #pragma unroll
     for (int st = 0; st < NSTEP; ++st) wn[st] = rn[st];
@@ -247,13 +265,13 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
       const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
       stage[i] = ldg16(terms + (static_cast<size_t>(tok) * NS + term) * D + k0 + cu * 8u);
     }
-    if (bounds && tid < kTileTokens * NSTEP) {
+    if (BOUNDS && tid < kTileTokens * NSTEP) {
       const uint32_t r = tid / NSTEP, st = tid % NSTEP;
       const uint32_t tok = t0 + r < T ? t0 + r : T - 1u;
       xn = xnorm[static_cast<size_t>(tok) * (D / 32u) + k0 / 32u + st];
     }
   };
-  const uint32_t tile0 = blockIdx.y * TT;
+  const uint32_t tile0 = by * TT;
   fetch(tile0 * kTileTokens);
 
   // B operands: 8 router values of row rr in word order per step.
@@ -286,46 +304,59 @@ __global__ __launch_bounds__(kGroupedThreads) void router_gemm_kernel(
       const uint32_t term = u / (kTileTokens * kUnitCols), r = (u / kUnitCols) % kTileTokens, cu = u % kUnitCols;
       *reinterpret_cast<uint4*>(&a_lds[term][r][cu * 8u]) = stage[i];
     }
-    if (bounds && tid < kTileTokens * NSTEP) xn_lds[tid / NSTEP][tid % NSTEP] = xn;
+    if (BOUNDS && tid < kTileTokens * NSTEP) xn_lds[tid / NSTEP][tid % NSTEP] = xn;
     __syncthreads();
     // The next tile's terms are in flight while this one computes.
     if (tt + 1u < TT && t0 + kTileTokens < T) fetch(t0 + kTileTokens);
 
     // 2. MFMAs: A = token m's terms at k0 + 32 st + 8q (word order), B = 8
     // router values of row rr. Each step starts from zero, smallest term
-    // first; its sum joins the running sums in fp32.
+    // first; its sum joins the running sums in fp32, in step order.
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float rp[4] = {0.f, 0.f, 0.f, 0.f}, ap[4] = {0.f, 0.f, 0.f, 0.f};
+    float sabs[4] = {0.f, 0.f, 0.f, 0.f};
+    const float ca = 32.0f + router_gemm_bound_coef(D);
 #pragma unroll
-    for (int st = 0; st < NSTEP; ++st) {
-      f32x4 part = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < NSTEP; b0 += kBatch) {
+      f32x4 part[kBatch];
 #pragma unroll
-      for (int t = NS - 1; t >= 0; --t)
-        part = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * st + 8u * q])), bop[st], part);
+      for (int s = 0; s < kBatch; ++s) {
+        part[s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float before = acc[j];
-        acc[j] = before + part[j];
-        if (bounds) {
-          const float a = wn[st] * xn_lds[4u * q + j][st];
-          rp[j] += 32.0f * (fabsf(before) + a) + fabsf(acc[j]);
-          ap[j] += a;
+        for (int t = NS - 1; t >= 0; --t)
+          part[s] = mfma(as_operand(*reinterpret_cast<const uint4*>(&a_lds[t][m][32u * (b0 + s) + 8u * q])),
+                         bop[b0 + s], part[s]);
+      }
+#pragma unroll
+      for (int s = 0; s < kBatch; ++s) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[j] = acc[j] + part[s][j];
+          if (BOUNDS && b0 + s + 1 < NSTEP) sabs[j] += fabsf(acc[j]);
         }
       }
     }
 
-    // 3. Plane blockIdx.z, [T][E + 1] (column E: the shared gate, when there
-    // is one): D rows 4q + j are tokens, column m the router row.
+    // 3. Plane bz, [T][E + 1] (column E: the shared gate, when there is
+    // one): D rows 4q + j are tokens, column m the router row.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t t = t0 + 4u * q + j;
-      if (t < T && row < nrows) {
-        planes[(static_cast<size_t>(blockIdx.z) * T + t) * (E + 1u) + row] = acc[j];
-        if (bounds) {
-          const size_t ps = static_cast<size_t>(T) * (E + 1u);
-          bplanes[2u * blockIdx.z * ps + static_cast<size_t>(t) * (E + 1u) + row] = rp[j];
-          bplanes[(2u * blockIdx.z + 1u) * ps + static_cast<size_t>(t) * (E + 1u) + row] = ap[j];
+      float ap = 0.0f;
+      if constexpr (BOUNDS) {
+        const float4* xr = reinterpret_cast<const float4*>(&xn_lds[4u * q + j][0]);
+#pragma unroll
+        for (int c = 0; c < NSTEP / 4; ++c) {
+          const float4 xv = xr[c];
+          ap = fmaf(wn[4 * c + 0], xv.x, ap);
+          ap = fmaf(wn[4 * c + 1], xv.y, ap);
+          ap = fmaf(wn[4 * c + 2], xv.z, ap);
+          ap = fmaf(wn[4 * c + 3], xv.w, ap);
         }
+      }
+      if (t < T && row < nrows) {
+        const size_t o = (static_cast<size_t>(bz) * T + t) * (E + 1u) + row;
+        planes[o] = acc[j];
+        if constexpr (BOUNDS) bplanes[o] = 33.0f * sabs[j] + fabsf(acc[j]) + ca * ap;
       }
     }
   }
@@ -1205,6 +1236,20 @@ void launch_split(const SplitParams& sp, hipStream_t st) {
 // (read once): TT = 2 from 256 tokens, where the grid still holds more than
 // two workgroups per compute unit.
 constexpr uint32_t kRouterTilesPerGroupFrom = 256;
+template <int NS, int NSTEP, int TT>
+void launch_router_gemm_steps(dim3 grid, hipStream_t st, const uint16_t* terms, uint32_t T, uint32_t D,
+                              const uint16_t* router, const uint16_t* sgv, uint32_t E, float* planes,
+                              const float* rnorm, const float* xnorm, float* bplanes) {
+  // One-dimensional launch, padded to a multiple of the 8 XCDs.
+  const uint32_t items = grid.x * grid.y * grid.z;
+  const dim3 launch((items + 7u) / 8u * 8u);
+  if (bplanes != nullptr)
+    router_gemm_kernel<NS, NSTEP, TT, true><<<launch, kGroupedThreads, 0, st>>>(
+        terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes, grid.x, grid.y, grid.z);
+  else
+    router_gemm_kernel<NS, NSTEP, TT, false><<<launch, kGroupedThreads, 0, st>>>(
+        terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes, grid.x, grid.y, grid.z);
+}
 template <int NS, int TT>
 void launch_router_gemm_tt(uint32_t rcols, dim3 grid, hipStream_t st, const uint16_t* terms, uint32_t T,
                            uint32_t D, const uint16_t* router, const uint16_t* sgv, uint32_t E, float* planes,
@@ -1212,16 +1257,13 @@ void launch_router_gemm_tt(uint32_t rcols, dim3 grid, hipStream_t st, const uint
   grid.y = (grid.y + TT - 1u) / TT;
   switch (rcols) {
     case 512:
-      router_gemm_kernel<NS, 16, TT><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm,
-                                                                       xnorm, bplanes);
+      launch_router_gemm_steps<NS, 16, TT>(grid, st, terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes);
       break;
     case 256:
-      router_gemm_kernel<NS, 8, TT><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm,
-                                                                      xnorm, bplanes);
+      launch_router_gemm_steps<NS, 8, TT>(grid, st, terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes);
       break;
     default:
-      router_gemm_kernel<NS, 4, TT><<<grid, kGroupedThreads, 0, st>>>(terms, T, D, router, sgv, E, planes, rnorm,
-                                                                      xnorm, bplanes);
+      launch_router_gemm_steps<NS, 4, TT>(grid, st, terms, T, D, router, sgv, E, planes, rnorm, xnorm, bplanes);
       break;
   }
 }

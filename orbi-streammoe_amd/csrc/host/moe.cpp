@@ -83,7 +83,7 @@ struct HipMoeLayer::Impl {
         osmd_moe_grouped_splits(&g, static_cast<std::uint32_t>(I)) * P * D * 4U,   // down partials
         parts * T * (cfg.expert_count + 1U) * 4U,                                   // logit planes
         T * (D / 32U) * 4U,                                                         // input chunk norms
-        parts * 2U * T * (cfg.expert_count + 1U) * 4U};                             // bound planes
+        parts * T * (cfg.expert_count + 1U) * 4U};                                  // bound planes
     std::size_t off = 0;
     for (std::size_t i = 0; i < bytes.size(); ++i) {
       g_off[i] = off;
