@@ -385,12 +385,20 @@ constexpr uint32_t kMaxBuckets = OSMD_MAX_EXPERTS + 1u;
 constexpr uint32_t kBucketStageRows = 12288;
 constexpr uint32_t kBucketStagePairs = 8192;
 
+// ceil(2^32 / nslot) for nslot > 1: with m = (2^32 + r) / nslot, r < nslot,
+// i m / 2^32 exceeds i / nslot by i r / (nslot 2^32) < 1 / nslot for i <
+// 2^24, so the high product's floor is i / nslot exactly (a 32-bit division
+// is dozens of instructions, per pair, on the bucket pass's one compute unit).
+uint32_t slot_magic(uint32_t nslot) {
+  return nslot > 1u ? static_cast<uint32_t>((0x100000000ull + nslot - 1u) / nslot) : 0u;
+}
+
 __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t* __restrict__ ids, const float* __restrict__ weights, const float* __restrict__ shared_gate,
     uint32_t T, uint32_t k, uint32_t nslot, uint32_t E, const uint8_t* const* __restrict__ expert_table,
     const uint8_t* shared_expert, const uint8_t* fallback, uint32_t* __restrict__ pair_pos,
     float* __restrict__ pair_w, Tile* __restrict__ tiles, uint32_t* __restrict__ tile_rows,
-    uint32_t* __restrict__ tile_count, uint32_t max_tiles) {
+    uint32_t* __restrict__ tile_count, uint32_t max_tiles, uint32_t magic) {
   __shared__ uint32_t counts[kMaxBuckets], offsets[kMaxBuckets], cursor[kMaxBuckets], tbase[kMaxBuckets];
   __shared__ uint32_t wave_total[kBucketThreads / kWave];
   __shared__ uint32_t s_rows[kBucketStageRows];
@@ -399,13 +407,15 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const uint32_t nb = E + (nslot > k ? 1u : 0u);
   const uint32_t P = T * nslot;
+  // Token of pair i as a high product (slot_magic; one slot: the pair index).
+  auto token_of = [&](uint32_t i) { return nslot > 1u ? __umulhi(i, magic) : i; };
   for (uint32_t b = tid; b < nb; b += kBucketThreads) counts[b] = 0u, cursor[b] = 0u;
   __syncthreads();
   // Routed pairs only: the shared expert's bucket (E) holds one pair per
   // token, in token order, so it needs no counting or cursor.
 #pragma unroll 4
   for (uint32_t i = tid; i < P; i += kBucketThreads) {
-    const uint32_t t = i / nslot, j = i % nslot;
+    const uint32_t t = token_of(i), j = i - t * nslot;
     if (j < k) {
       uint32_t e = ids[static_cast<size_t>(t) * k + j];
       e = e < E ? e : E - 1u;
@@ -470,7 +480,7 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
   const bool stage = ntiles * kTileTokens <= kBucketStageRows && P <= kBucketStagePairs;
 #pragma unroll 4
   for (uint32_t i = tid; i < P; i += kBucketThreads) {
-    const uint32_t t = i / nslot, j = i % nslot;
+    const uint32_t t = token_of(i), j = i - t * nslot;
     uint32_t e = E;  // the shared expert's bucket
     if (j < k) {
       e = ids[static_cast<size_t>(t) * k + j];
@@ -1305,6 +1315,8 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   const uint32_t has_shared = (m.flags & OSMD_MOE_SHARED) ? 1u : 0u;
   const uint32_t nslot = m.top_k + has_shared;
   const uint32_t P = T * nslot;
+  // The bucket pass's token index (slot_magic) is exact below 2^24 pairs.
+  if (static_cast<uint64_t>(T) * nslot >= (1ull << 24)) return static_cast<int>(hipErrorInvalidValue);
   const size_t max_tiles = osmd_moe_grouped_max_tiles(T, nslot, m.expert_count);
   uint32_t* tile_rows = reinterpret_cast<uint32_t*>(static_cast<Tile*>(a->tiles) + max_tiles);
 
@@ -1389,7 +1401,8 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   bucket_kernel<<<1, kBucketThreads, 0, st>>>(m.ids, m.weights, has_shared ? m.shared_gate : nullptr, T, m.top_k,
                                               nslot, m.expert_count, m.expert_table, m.shared_expert,
                                               m.fallback_blob, a->pair_pos, a->pair_w, static_cast<Tile*>(a->tiles),
-                                              tile_rows, a->tile_count, static_cast<uint32_t>(max_tiles));
+                                              tile_rows, a->tile_count, static_cast<uint32_t>(max_tiles),
+                                              slot_magic(nslot));
 
   SplitParams sp{};
   sp.g = g;
