@@ -1293,6 +1293,7 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
 #pragma unroll
     for (int v = 0; v < 32; ++v) xsum[ci] += xr[ci][v];
   }
+  float gsum[ROWS], usum[ROWS];
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
     float ga = 0.0f, ua = 0.0f;
@@ -1303,10 +1304,20 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
       ua += meta_widen<META>(su[i][ci]) * nib_dot32(qu[i][ci], xr[ci]) +
             meta_widen<META>(bu[i][ci]) * xsum[ci];
     }
-    ga = wave_sum(ga);
-    ua = wave_sum(ua);
-    const uint32_t r = r0 + i;
-    if (lane == 0 && r < I) store((static_cast<size_t>(t) * p.src.nslot + j) * I + r, silu_mul(ga, ua));
+    gsum[i] = wave_sum(ga);
+    usum[i] = wave_sum(ua);
+  }
+  // SwiGLU of the wavefront's rows in one pass, lane i for row r0 + i (one
+  // exp and division on the wavefront's path instead of one per row).
+  if (lane < static_cast<uint32_t>(ROWS)) {
+    float g = gsum[0], u = usum[0];
+#pragma unroll
+    for (int i = 1; i < ROWS; ++i) {
+      g = lane == static_cast<uint32_t>(i) ? gsum[i] : g;
+      u = lane == static_cast<uint32_t>(i) ? usum[i] : u;
+    }
+    const uint32_t r = r0 + lane;
+    if (r < I) store((static_cast<size_t>(t) * p.src.nslot + j) * I + r, silu_mul(g, u));
   }
 }
 
