@@ -348,6 +348,18 @@ __device__ __forceinline__ float load_x1(const RouteView& rv, uint32_t t, uint32
   return rv.x_bf16 ? bf16_to_f32(ldg<uint16_t>(static_cast<const uint16_t*>(rv.x) + o))
                    : ldg<float>(static_cast<const float*>(rv.x) + o);
 }
+// The same element as loaded (fp32 bits, or a bf16 in the low half), for
+// loads issued steps ahead of their use: widening a bf16 right after its
+// load would wait for the load there.
+__device__ __forceinline__ uint32_t load_x1_bits(const RouteView& rv, uint32_t t, uint32_t c) {
+  if (c >= rv.hidden) return 0u;
+  const size_t o = static_cast<size_t>(t) * rv.hidden + c;
+  return rv.x_bf16 ? static_cast<uint32_t>(ldg<uint16_t>(static_cast<const uint16_t*>(rv.x) + o))
+                   : ldg<uint32_t>(static_cast<const float*>(rv.x) + o);
+}
+__device__ __forceinline__ float x1_value(const RouteView& rv, uint32_t bits) {
+  return rv.x_bf16 ? bf16_to_f32(bits) : __uint_as_float(bits);
+}
 
 // The reference's RMSNorm scale of token t: the squares summed in order,
 // then 1 / sqrt(sum / D + eps), each operation rounded to fp32
@@ -411,15 +423,18 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
       if constexpr (RD == OSM_ROUTER_AFFINE_Q8) load_q8x8(qr, c + 8u, w1); else load_raw8<RD>(row, c + 8u, w1);
     }
   };
-  float xv = 0.0f, nwv = 1.0f;
+  uint32_t xb = 0u;
+  float nwv = 1.0f;
   auto fetch_x = [&](uint32_t c0) {
     if (!producer) return;
     const uint32_t c = c0 + ptid;
-    xv = load_x1(rv, t, c);
+    xb = load_x1_bits(rv, t, c);
     nwv = (rv.rms && c < D) ? ldg<float>(rv.norm_weight + c) : 1.0f;
   };
   auto stage_x = [&](uint32_t buf) {
-    if (producer) out.xe[buf][ptid] = rv.rms ? xv * (scale * nwv) : xv;
+    if (!producer) return;
+    const float xv = x1_value(rv, xb);
+    out.xe[buf][ptid] = rv.rms ? xv * (scale * nwv) : xv;
   };
   // Step k: the producers write chunk k's products (router elements loaded
   // in step k - 1, inputs staged in step k - 1), stage chunk k + 1's inputs
@@ -487,7 +502,8 @@ __device__ void exact_logits_deep(const RouteView& rv, uint32_t t, Selection<PER
     Raw8<RD> lo, hi;
   };
   struct X1 {
-    float x, nw;
+    uint32_t x;  // as loaded (load_x1_bits)
+    float nw;
   };
   auto fetch_w = [&](W16& w, uint32_t chunk) {
     const uint32_t c = chunk * kExactCols + seg;
@@ -502,11 +518,13 @@ __device__ void exact_logits_deep(const RouteView& rv, uint32_t t, Selection<PER
   auto fetch_x = [&](X1& v, uint32_t chunk) {
     if (!producer) return;
     const uint32_t c = chunk * kExactCols + ptid;
-    v.x = load_x1(rv, t, c);
+    v.x = load_x1_bits(rv, t, c);
     v.nw = (rv.rms && c < D) ? ldg<float>(rv.norm_weight + c) : 1.0f;
   };
   auto stage_x = [&](const X1& v, uint32_t buf) {
-    if (producer) out.xe[buf][ptid] = rv.rms ? v.x * (scale * v.nw) : v.x;
+    if (!producer) return;
+    const float xv = x1_value(rv, v.x);
+    out.xe[buf][ptid] = rv.rms ? xv * (scale * v.nw) : xv;
   };
   const uint32_t nchunks = (D + kExactCols - 1u) / kExactCols;
   float acc = 0.0f;
