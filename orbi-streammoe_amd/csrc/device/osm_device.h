@@ -203,7 +203,7 @@ int osmd_moe_select(const osmd_moe_args* a, osmd_stream s);
  * where splits(n) = osmd_moe_grouped_splits(&moe.geom, n) K ranges of the
  * n columns (hidden for gate/up, inter for down).
  * plus the decode workspace of moe (logits, ids, weights, mass, shared_gate,
- * x_norm). */
+ * x_norm). P must be below 2^24 (hipErrorInvalidValue otherwise). */
 typedef struct osmd_moe_grouped_args {
   osmd_moe_args moe;
   uint32_t x_bf16;
@@ -221,7 +221,7 @@ typedef struct osmd_moe_grouped_args {
   /* Error bounds of the router GEMM's logits (any null: no bounds, every
    * selection takes the exact path): the router's 32-column norms
    * [E + 1][D/32] (row E the shared-gate vector), the input's [T][D/32],
-   * and the bound planes [router_parts][2][T][E + 1]. */
+   * and the bound planes [router_parts][T][E + 1]. */
   const float* router_norms;
   float* x_norms;
   float* bound_planes;
