@@ -1119,22 +1119,27 @@ __global__ void combine4_kernel(const float* __restrict__ partial, uint32_t nspl
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     uint32_t j = 0;
     if (nsplit == 1u) {
-      // One K range (the usual case): four slots' positions, then their rows,
-      // are loaded before the adds, which keep slot order.
+      // One K range (the usual case): up to twelve slots' positions, then
+      // all their rows, are loaded before the adds, which keep slot order
+      // (top-10 + shared: one round trip for the positions and one for the
+      // rows). Slots past nslot load slot 0's row and are not added.
+      constexpr uint32_t kBatch = 12;
       const float4* part4 = reinterpret_cast<const float4*>(partial);
-      for (; j + 4u <= nslot; j += 4u) {
-        size_t pos[4];
+      for (; j < nslot; j += kBatch) {
+        uint32_t pos[kBatch];
 #pragma unroll
-        for (uint32_t q = 0; q < 4u; ++q) pos[q] = pair_pos[t * nslot + j + q];
-        float4 v[4];
+        for (uint32_t q = 0; q < kBatch; ++q) pos[q] = pair_pos[t * nslot + (j + q < nslot ? j + q : 0u)];
+        float4 v[kBatch];
 #pragma unroll
-        for (uint32_t q = 0; q < 4u; ++q) v[q] = part4[pos[q] * D4 + r4];
+        for (uint32_t q = 0; q < kBatch; ++q) v[q] = part4[static_cast<size_t>(pos[q]) * D4 + r4];
 #pragma unroll
-        for (uint32_t q = 0; q < 4u; ++q) {
-          acc.x += v[q].x;
-          acc.y += v[q].y;
-          acc.z += v[q].z;
-          acc.w += v[q].w;
+        for (uint32_t q = 0; q < kBatch; ++q) {
+          if (j + q < nslot) {
+            acc.x += v[q].x;
+            acc.y += v[q].y;
+            acc.z += v[q].z;
+            acc.w += v[q].w;
+          }
         }
       }
     }
