@@ -30,8 +30,10 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "orbi-streammoe_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))  # helpers: the capped-cache routing trace
 
 import osm_hip  # noqa: E402
+from helpers import correlated_trace  # noqa: E402
 
 METRIC = "q4 routed-MoE layer decode µs/token + achieved HBM GB/s (% of ~8 TB/s peak)"
 HBM_PEAK_GBPS = 8000.0
@@ -88,7 +90,7 @@ def build_model(ctx, layers, seed):
 
 def routing_counts(moes, reset=False):
     """The layers' routing counters summed (selections, exact-path
-    selections, exact paths over every expert, unresolved adjacent picks)."""
+    selections, exact paths over every expert, near ties settled there)."""
     tot = {}
     for m in moes:
         for k, v in m.routing_stats(reset=reset).items():
@@ -276,32 +278,6 @@ def grouped_decode(ctx, moes, slab, args, T, layers=8):
     return res
 
 
-def correlated_trace(rng, layers, steps, repeat_p):
-    """Routed experts per (step, layer): each of the k picks repeats one of
-    that layer's previous-step picks with probability repeat_p, else it is a
-    fresh expert; picks within a step are distinct."""
-    prev = [None] * layers
-    trace = []
-    for _s in range(steps):
-        row = []
-        for l in range(layers):
-            ids = []
-            for _j in range(K):
-                cands = [e for e in (prev[l] or []) if e not in ids]
-                if cands and rng.random() < repeat_p:
-                    ids.append(int(rng.choice(cands)))
-                    continue
-                while True:
-                    e = int(rng.integers(E))
-                    if e not in ids:
-                        break
-                ids.append(e)
-            prev[l] = ids
-            row.append(np.array(ids, np.uint32).reshape(1, K))
-        trace.append(row)
-    return trace
-
-
 def capped_cache_decode(ctx, g, moes, args, steps=64, warm=8, repeat_p=0.6):
     """Config 3b: the layer stack as chained sublayers (RMSNorm, MoE,
     residual), one token per step, with the HBM expert cache capped at
@@ -322,7 +298,7 @@ def capped_cache_decode(ctx, g, moes, args, steps=64, warm=8, repeat_p=0.6):
     log(f"[bench] capped cache: {L * E * store.stride / 1e9:.1f} GB pinned host store, "
         f"{budget / 1e9:.0f} GB cache, ready in {time.time() - t0:.1f}s")
     rng = np.random.default_rng(args.seed + 7)
-    trace = correlated_trace(rng, L, steps, repeat_p)
+    trace = correlated_trace(rng, L, steps, K, E, repeat_p)
     w = np.arange(K, 0, -1, dtype=np.float32)
     w = (w / w.sum()).astype(np.float32).reshape(1, K)
     xs = osm_hip.synth_tokens(ctx, args.seed, 900000, steps, D)

@@ -240,13 +240,19 @@ int osm_moe_layer_run_slab(osm_context ctx, osm_moe_layer l, osm_expert_slab sla
                            uint32_t slab_layer, const float* hidden, uint32_t tokens,
                            int sublayer, const osm_moe_outputs* outputs);
 /* Same through the GPU resident cache: routing on the device, residency
- * decided on the host from the routed ids, misses filled on a side stream. */
+ * decided on the host from the routed ids (one wait), misses filled on side
+ * streams while the picks already resident run. A budget that cannot hold
+ * the call's picks at once runs them in rounds, each ending just before a
+ * get would evict one of its picks (the reference runs each pick right after
+ * its get, routed_moe.cpp:320-366); any budget of at least one expert works,
+ * and outputs have the bits of the all-resident decode. */
 int osm_moe_layer_run_cached(osm_context ctx, osm_moe_layer l, osm_expert_cache cache,
                              uint32_t layer, const float* hidden, uint32_t tokens, int sublayer,
                              const osm_moe_outputs* outputs);
 /* Same with caller-chosen routed experts: ids [tokens, k] (< expert_count)
  * and weights [tokens, k] (finite) replace the router's picks; the router
- * still gives the shared gate, logits and the normalised input. No
+ * still gives the shared gate, logits and the normalised input (no selection
+ * runs; the mass output is the given weights' sum). No
  * counterpart in the reference, whose routed MoE always routes itself
  * (routed_moe.cpp:13-92); it drives the cache with an external routing
  * trace, e.g. correlated routing across decode steps. */
@@ -306,12 +312,22 @@ int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens,
  * reference's; a selection whose order the bounds do not prove recomputes
  * its candidates' logits in the reference's order. out[0] selections (one
  * per token per call), out[1] selections that took that exact path, out[2]
- * exact paths that recomputed every expert (picks near exp underflow),
- * out[3] adjacent picks whose reference probabilities could tie only
- * through the last bit of exp (order taken from the exps; 0 in every run
- * so far). Synchronises the context's stream; reset != 0 zeroes them
- * afterwards. */
+ * exact paths that recomputed every expert and ranked them by the
+ * reference's own probabilities (picks near exp underflow, or a near tie),
+ * out[3] the near ties that sent a selection there: adjacent candidates
+ * whose exps (the host libm's bits) are close enough for their
+ * probabilities to round to one value, with the higher id ranked first.
+ * Synchronises the context's stream; reset != 0 zeroes them afterwards. */
 int osm_moe_layer_routing_stats(osm_context ctx, osm_moe_layer l, uint32_t out[4], int reset);
+
+/* Self-check of the selection's exp (no counterpart in the reference: its
+ * probabilities use the host libm's expf, src/cpu/reference_ops.cpp:141-145,
+ * whose bits the device reproduces). Evaluates the device's exp on the float
+ * bit patterns first_bits .. first_bits + count - 1 and writes
+ * ceil(count / block) host checksums: out[b] = sum over block b's inputs i
+ * (i from 0) of bits(exp(x)) * (2 i + 1) mod 2^64. A caller compares them
+ * with the same sums of its own expf. first_bits + count <= 2^32. */
+int osm_libm_expf_checksums(osm_context ctx, uint32_t first_bits, uint64_t count, uint32_t block, uint64_t* out);
 /* Enqueues n_layers decodes back to back, as the reference's decoder stack
  * runs its layers in order (src/model/checkpoint_decoder_stack.cpp:191-204).
  * chained != 0: sublayer form, layer i reads the output of layer i-1 (x_dev
@@ -326,10 +342,15 @@ int osm_moe_layer_routing_stats(osm_context ctx, osm_moe_layer l, uint32_t out[4
  * y are host [tokens, D]. pick_ids / pick_weights (both or neither):
  * [n_layers][tokens][k] routed picks given from outside, as
  * osm_moe_layer_run_cached_picks takes them; NULL routes on the device.
- * With picks given the whole stack is enqueued without a host wait: the
- * activations stay on the device, and each layer's fills wait only for the
- * kernels that last read the slots they overwrite, so they overlap the
- * layers before. Outputs are the bits of the layer-by-layer calls. */
+ * The activations stay on the device between layers, and each layer's fills
+ * wait only for the kernels that last read the slots they overwrite. With
+ * picks given the whole stack is enqueued without a host wait, so fills
+ * overlap the layers before; with device routing each layer's ids come back
+ * to the host (one wait per layer), and the picks already resident run while
+ * the misses are copied. Any budget of at least one expert works: when a
+ * layer's picks do not fit at once they run in rounds, as the reference runs
+ * each pick right after fetching it (routed_moe.cpp:320-366). Outputs are the
+ * bits of the layer-by-layer calls. */
 int osm_moe_run_cached_layers(osm_context ctx, const osm_moe_layer* layers, const uint32_t* cache_layers,
                               uint32_t n_layers, osm_expert_cache cache, const float* x, uint32_t tokens,
                               const uint32_t* pick_ids, const float* pick_weights, float* y);

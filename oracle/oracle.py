@@ -43,6 +43,8 @@ _ORACLE_PROTOS = {
     "oracle_route_qwen_top_k": (c_int, [_P, c_size_t, _P, c_size_t, c_size_t, c_size_t, c_size_t, c_int, _P, _P, _P, _P]),
     "oracle_run_shared_expert": (c_int, [_P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, _P, c_size_t, c_size_t, c_size_t, _P, _P]),
     "oracle_bf16_to_float": (c_float, [c_uint16]),
+    "oracle_libm_expf_checksums": (c_int, [c_uint32, c_uint64, c_uint32, _P]),
+    "oracle_moe_sublayer_picks": (c_int, [_P, _P, c_float, _P, c_uint32, _P, _P, _P, c_uint32, c_uint32, c_uint32, c_int, _P]),
     "oracle_f16_to_float": (c_float, [c_uint16]),
     "oracle_expert_blob_bytes": (c_size_t, [c_uint32, c_uint32, c_uint32, c_int]),
     "oracle_expert_forward": (c_int, [_P, c_uint32, c_uint32, c_uint32, c_int, _P, _P]),
@@ -239,6 +241,16 @@ def bf16_to_float(bits):
     return lib().oracle_bf16_to_float(bits)
 
 
+def libm_expf_checksums(first_bits, count, block):
+    """Block checksums of the host libm's expf (std::exp of a float, as the
+    reference's softmax calls it) over float bit patterns first_bits ..
+    first_bits + count - 1: sum over each block's inputs i of
+    bits(exp(x)) * (2 i + 1) mod 2^64."""
+    out = np.zeros((count + block - 1) // block, np.uint64)
+    _check(lib().oracle_libm_expf_checksums(first_bits, count, block, p(out)))
+    return out
+
+
 def f16_to_float(bits):
     return lib().oracle_f16_to_float(bits)
 
@@ -299,6 +311,20 @@ def moe_sublayer(residual, norm_weight, eps, router_f32, expert_blobs, shared_bl
                                      p(shared_blob) if shared_blob is not None else None, p(sg),
                                      hidden_size, inter, group, meta, p(normalized), p(out), p(ids), p(w), p(sgo)))
     return {"out": out, "normalized": normalized, "ids": ids, "weights": w, "shared_gate": float(sgo[0])}
+
+
+def moe_sublayer_picks(residual, norm_weight, eps, weights, pick_blobs, shared_blob, shared_scalar_gate, hidden_size, inter, group, meta):
+    """The sublayer with given routed experts (no router): RMSNorm, pick i's
+    expert blob accumulated with weights[i] in pick order, the sigmoid-gated
+    shared expert, the residual."""
+    x, nw, w = f32(residual), f32(norm_weight), f32(weights)
+    table = _ptr_table(pick_blobs)
+    sg = f32(shared_scalar_gate) if shared_scalar_gate is not None else None
+    out = np.zeros(hidden_size, np.float32)
+    _check(lib().oracle_moe_sublayer_picks(p(x), p(nw), eps, p(w), len(pick_blobs), ctypes.cast(table, c_void_p),
+                                           p(shared_blob) if shared_blob is not None else None, p(sg),
+                                           hidden_size, inter, group, meta, p(out)))
+    return out
 
 
 # ---- synthetic generator ----------------------------------------------------------------

@@ -27,6 +27,7 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <unordered_map>
 #include <unordered_set>
@@ -732,6 +733,26 @@ int oracle_run_shared_expert(const float* hidden, size_t hidden_len,
 }
 
 float oracle_bf16_to_float(uint16_t bits) { return bf16_widen(bits); }
+
+int oracle_libm_expf_checksums(uint32_t first, uint64_t count, uint32_t block, uint64_t* out) {
+  if (count == 0 || block == 0 || out == nullptr || static_cast<uint64_t>(first) + count > (1ULL << 32)) return 1;
+  const uint64_t nblocks = (count + block - 1) / block;
+  const unsigned nt = std::max(1U, std::thread::hardware_concurrency());
+  std::vector<std::thread> workers;
+  for (unsigned w = 0; w < nt; ++w)
+    workers.emplace_back([=] {
+      for (uint64_t b = w; b < nblocks; b += nt) {
+        uint64_t s = 0;
+        for (uint64_t i = 0; i < block && b * block + i < count; ++i) {
+          const float x = std::bit_cast<float>(static_cast<uint32_t>(first + b * block + i));
+          s += static_cast<uint64_t>(std::bit_cast<uint32_t>(std::exp(x))) * (2 * i + 1);
+        }
+        out[b] = s;
+      }
+    });
+  for (auto& t : workers) t.join();
+  return 0;
+}
 float oracle_f16_to_float(uint16_t bits) { return f16_widen(bits); }
 
 size_t oracle_expert_blob_bytes(uint32_t hidden, uint32_t inter, uint32_t group,
@@ -806,6 +827,39 @@ int oracle_moe_sublayer(const float* residual, const float* norm_weight,
     return rc;
   for (uint32_t i = 0; i < hidden_size; ++i) out[i] = residual[i] + moe[i];
   if (out_normalized) std::memcpy(out_normalized, norm.data(), hidden_size * sizeof(float));
+  return 0;
+}
+
+// The sublayer with the routed experts given instead of routed: RMSNorm
+// (checkpoint_moe_sublayer.cpp:158-183), each pick's expert on the
+// normalised input accumulated in pick order as acc + w * out
+// (routed_moe.cpp:31-62), the sigmoid-gated shared expert added as
+// sparse_moe adds it, then the residual (:21-33). pick_blobs[i] is pick i's
+// expert blob.
+int oracle_moe_sublayer_picks(const float* residual, const float* norm_weight, float eps, const float* weights,
+                              uint32_t k, const uint8_t* const* pick_blobs, const uint8_t* shared_blob,
+                              const float* shared_scalar_gate, uint32_t hidden_size, uint32_t inter, uint32_t group,
+                              int meta_dtype, float* out) {
+  std::vector<float> norm(residual, residual + hidden_size);
+  if (int rc = rms_norm(norm.data(), hidden_size, 1U, hidden_size, norm_weight, hidden_size, eps)) return rc;
+  std::vector<float> acc(hidden_size, 0.0F), e(hidden_size);
+  for (uint32_t i = 0; i < k; ++i) {
+    if (!std::isfinite(weights[i])) return fail_runtime("routed MoE encountered a non-finite routing weight");
+    if (int rc = expert_forward(pick_blobs[i], hidden_size, inter, group, meta_dtype, norm.data(), e.data()))
+      return rc;
+    for (uint32_t j = 0; j < hidden_size; ++j) {
+      const float prod = weights[i] * e[j];
+      acc[j] = acc[j] + prod;
+    }
+  }
+  if (shared_blob != nullptr) {
+    float sg = 0.0F;
+    if (int rc = shared_from_blob(shared_blob, shared_scalar_gate, hidden_size, inter, group, meta_dtype, norm.data(),
+                                  e.data(), &sg))
+      return rc;
+    for (uint32_t j = 0; j < hidden_size; ++j) acc[j] = acc[j] + e[j];
+  }
+  for (uint32_t j = 0; j < hidden_size; ++j) out[j] = residual[j] + acc[j];
   return 0;
 }
 

@@ -75,6 +75,13 @@ int oracle_run_shared_expert(const float* hidden, size_t hidden_len,
 
 /* ---- metadata widening (vulkan_qpack_expert.cpp:54-87) ---------------- */
 float oracle_bf16_to_float(uint16_t bits);
+
+/* ---- the softmax numerator's exp (reference_ops.cpp:141-145) ------------ */
+/* Block checksums of std::exp(float) -- the host libm's expf, as the
+ * reference's softmax calls it -- over float bit patterns first ..
+ * first + count - 1: out[b] = sum over block b's inputs i (i from 0) of
+ * bits(exp(x)) * (2 i + 1) mod 2^64. Runs on every hardware thread. */
+int oracle_libm_expf_checksums(uint32_t first, uint64_t count, uint32_t block, uint64_t* out);
 float oracle_f16_to_float(uint16_t bits);
 
 /* ---- expert blob (qpack section order) -------------------------------- */
@@ -115,6 +122,14 @@ int oracle_moe_sublayer(const float* residual, const float* norm_weight,
                         float* out_shared_gate);
 
 /* ---- synthetic seeded generator (counter-based, bit-reproducible) ----- */
+/* The sublayer with given routed experts: RMSNorm, pick i's expert
+ * (pick_blobs[i]) accumulated with weights[i] in pick order
+ * (routed_moe.cpp:31-62), the sigmoid-gated shared expert, the residual. */
+int oracle_moe_sublayer_picks(const float* residual, const float* norm_weight, float eps, const float* weights,
+                              uint32_t k, const uint8_t* const* pick_blobs, const uint8_t* shared_blob,
+                              const float* shared_scalar_gate, uint32_t hidden_size, uint32_t inter, uint32_t group,
+                              int meta_dtype, float* out);
+
 uint64_t oracle_synth_stream(uint64_t seed, uint32_t a, uint32_t b,
                              uint32_t tensor);
 float oracle_synth_normal(uint64_t stream, uint64_t index);

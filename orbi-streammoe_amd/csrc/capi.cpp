@@ -622,39 +622,19 @@ int osm_moe_run_cached_layers(osm_context ctx, const osm_moe_layer* layers, cons
   if (!ctx || !layers || !cache_layers || !cache || !x || !y || n_layers == 0 || tokens == 0 ||
       (!pick_ids) != (!pick_weights))
     return fail(OSM_E_INVALID, "invalid arguments");
+  // The whole stack in one native call: activations on the device, each
+  // layer's fills waiting only for the kernels that last read their slots.
   const std::size_t D = layers[0] ? layers[0]->layer.config().geometry.hidden : 0;
-  if (pick_ids) {
-    // Routing given: the whole stack is enqueued at once (activations on the
-    // device, fills overlapping earlier layers' kernels).
-    std::vector<osm::HipMoeLayer*> ls(n_layers);
-    for (uint32_t i = 0; i < n_layers; ++i) {
-      if (!layers[i]) return fail(OSM_E_INVALID, "null layer");
-      ls[i] = &layers[i]->layer;
-    }
-    std::string d;
-    if (!osm::run_cached_stack_picks(ctx->ctx, *cache->cache, ls, cache_layers,
-                                     std::span<const float>(x, static_cast<std::size_t>(tokens) * D), pick_ids,
-                                     pick_weights, y, &d))
-      return fail(OSM_E_INVALID, d);
-    return ok();
-  }
-  std::vector<float> cur(x, x + static_cast<std::size_t>(tokens) * D);
+  std::vector<osm::HipMoeLayer*> ls(n_layers);
   for (uint32_t i = 0; i < n_layers; ++i) {
-    if (!layers[i] || layers[i]->layer.config().geometry.hidden != D)
-      return fail(OSM_E_INVALID, "layers must share one hidden size");
-    const std::size_t K = layers[i]->layer.config().top_k;
-    osm::HipMoePicks picks;
-    if (pick_ids) {
-      // Every layer's picks sit at the same stride, so the layers must agree on k.
-      if (K != layers[0]->layer.config().top_k) return fail(OSM_E_INVALID, "given picks need one top_k");
-      picks = {pick_ids + static_cast<std::size_t>(i) * tokens * K, pick_weights + static_cast<std::size_t>(i) * tokens * K};
-    }
-    auto r = osm::run_qwen_sparse_moe_hip(ctx->ctx, *cache->cache, layers[i]->layer, cache_layers[i], cur, true,
-                                          pick_ids ? &picks : nullptr);
-    if (!r.executed) return fail(OSM_E_INVALID, "layer " + std::to_string(i) + ": " + r.diagnostic);
-    cur = std::move(r.values);
+    if (!layers[i]) return fail(OSM_E_INVALID, "null layer");
+    ls[i] = &layers[i]->layer;
   }
-  std::memcpy(y, cur.data(), cur.size() * sizeof(float));
+  std::string d;
+  if (!osm::run_cached_stack(ctx->ctx, *cache->cache, ls, cache_layers,
+                             std::span<const float>(x, static_cast<std::size_t>(tokens) * D), pick_ids, pick_weights,
+                             y, &d))
+    return fail(OSM_E_INVALID, d);
   return ok();
   OSM_GUARD_END
 }
@@ -825,6 +805,24 @@ int osm_moe_layer_routing_stats(osm_context ctx, osm_moe_layer l, uint32_t out[4
   if (!l->layer.routing_stats(ctx->ctx, v, reset != 0, &d)) return fail(OSM_E_DEVICE, d);
   std::memcpy(out, v, sizeof(v));
   return ok();
+}
+
+int osm_libm_expf_checksums(osm_context ctx, uint32_t first_bits, uint64_t count, uint32_t block, uint64_t* out) {
+  OSM_GUARD_BEGIN
+  if (!ctx || !out || count == 0 || block == 0) return fail(OSM_E_INVALID, "invalid arguments");
+  if (static_cast<uint64_t>(first_bits) + count > (1ULL << 32)) return fail(OSM_E_INVALID, "range past 2^32");
+  const uint64_t nblocks = (count + block - 1) / block;
+  if (nblocks > 0x7FFFFFFFULL) return fail(OSM_E_INVALID, "too many blocks");
+  std::string d;
+  if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
+  osm::DeviceBytes sums;
+  int rc = sums.allocate(nblocks * sizeof(uint64_t));
+  const osmd_stream st = ctx->ctx.stream();
+  if (rc == 0) rc = osmd_libm_expf_checksums(first_bits, count, block, sums.as<uint64_t>(), st);
+  if (rc == 0) rc = osmd_memcpy_d2h(out, sums.get(), nblocks * sizeof(uint64_t), st);
+  if (rc == 0) rc = osmd_stream_synchronize(st);
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("exp checksums", rc));
+  OSM_GUARD_END
 }
 
 int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,

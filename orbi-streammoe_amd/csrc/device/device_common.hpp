@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "libm_expf.h"
 #include "osm_device.h"
 
 namespace osmk {

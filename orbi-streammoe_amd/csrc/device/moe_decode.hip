@@ -78,13 +78,24 @@ struct RouteView {
   float rms_eps;
 };
 
+// Entry i of a slot list (osmd_slot_list_add's packing; i is uniform).
+__device__ __forceinline__ uint32_t slot_at(const osmd_slot_list& l, uint32_t i) {
+  return static_cast<uint32_t>((i < 12u ? l.lo >> (5u * i) : l.hi >> (5u * (i - 12u))) & 31u);
+}
+
 struct GateUpParams {
   osm_expert_geometry g;
   SlotSource src;
   RouteView rv;
   const float* x;  // [B, D]
   float* h;        // [B, nslot, I]
+  osmd_slot_list list;  // slots from src (count 0: all nslot, in order; the grid covers list.count)
 };
+
+// The down kernel's three forms: the fused sum over every slot (y); the
+// partials of the listed slots only (parts); y from the partials of every
+// slot, accumulated as the fused form accumulates (combine).
+enum DownMode : int { kDownFused = 0, kDownParts = 1, kDownCombine = 2 };
 
 struct DownParams {
   osm_expert_geometry g;
@@ -96,6 +107,8 @@ struct DownParams {
   const float* h;            // [B, nslot, I]
   const float* residual;     // [B, D] or null
   float* y;                  // [B, D]
+  osmd_slot_list list;       // kDownParts: the slots to run
+  float* parts;              // kDownParts (out) / kDownCombine (in): [B][nslot][D][LPR] per-lane partials
 };
 
 
@@ -209,13 +222,17 @@ __device__ __forceinline__ float raw8_get(const Raw8<RD>& r, int j) {
 // Otherwise (a near tie, equal device logits, or a missing bound) the
 // selection takes the exact path: every expert whose interval can reach the
 // picks' lowest lower bound is recomputed in the reference's order, and the
-// candidates are ranked by exp(fl(L - m)) with ties to the lower id, the
-// reference's key. When the k-th candidate is more than 80 below m (exps
-// near or at underflow, where probabilities tie at 0 and the lowest ids win
-// whatever their logits) every expert is recomputed. Two adjacent picks
-// whose logits differ but whose exps lie within 5 ulps of each other are
-// counted as unresolved: there the order rests on the exp's last bit and on
-// the rounding of the sum, which the device cannot reproduce exactly.
+// candidates are ranked by the reference's numerator e = exp(fl(L - m)),
+// with the host libm's own bits (osm_libm_expf), ties to the lower id. The
+// reference ranks by p = fl(e / S) instead, S its sum of every expert's e
+// in id order; p orders as e does, except that two different e can round to
+// one p, and then the lower id wins. That can only happen for e_a > e_c
+// within 2^-22 e_a (one ulp of the quotient, or 2^-138 where the quotient is
+// subnormal). When such a pair is adjacent among the first k + 1 candidates
+// with the higher id first, and whenever the k-th candidate is more than 80
+// below m (exps near or at underflow), every expert is recomputed: S is then
+// summed as the reference sums it and the experts are ranked by fl(e / S),
+// ties to the lower id, which is the reference's ranking itself.
 //
 // The probabilities of the picks (their weights) come from the device
 // logits in both paths: exp(l - max) / sum over every expert.
@@ -254,15 +271,15 @@ struct Selection {
   float p[OSMD_MAX_TOP_K];
   const uint8_t* blob[kSelThreads * PER];
   float val[kSelThreads * PER];   // device logit of every expert
-  float aux[kSelThreads * PER];   // its bound; on the exact path, its exp(fl(L - m)) (-1: no candidate)
+  float aux[kSelThreads * PER];   // its bound; on the exact path, its e = exp(fl(L - m)) (-1: no candidate)
   float ex[kSelThreads * PER];    // exact path: the reference's logit of a candidate
   float red[3][kSelWaves];
   uint64_t cand[kWave];                       // (key << 32) | ~id of the ranked candidates
   float clg[kWave], cbd[kWave];               // their device logits and bounds
   uint32_t hist[kHistBins];                   // experts per bin of distance from the largest logit
   uint32_t fid[OSMD_MAX_TOP_K + 1];           // exact path: candidates by rank
-  float scal[2];
-  uint32_t nunresolved, ncand, thr, flags, wcount[kSelWaves];
+  float scal[3];                              // exact path: threshold, RMS scale, softmax sum
+  uint32_t nneartie, ncand, thr, flags, wcount[kSelWaves];  // nneartie: near ties sent to the full recompute
   uint16_t cl[kSelThreads * PER];             // exact path: candidate list
   __attribute__((aligned(16))) float xe[2][kExactCols];  // exact path: the inputs of two chunks
   __attribute__((aligned(16))) float prod[2][kExactRows][kExactStride];  // exact path: rounded products of two chunks
@@ -598,7 +615,8 @@ __device__ void exact_logits(const RouteView& rv, uint32_t t, Selection<PER>& ou
 
 // The exact path (every thread of the workgroup; out.id/lg/bd hold the
 // device ranking). Rewrites out.id and out.lg; returns whether every expert
-// was recomputed. out.nunresolved gets the unresolved adjacent pairs.
+// was recomputed. out.nneartie gets the adjacent pairs that sent it to the
+// full recompute (near ties with the higher id first).
 template <int PER, bool DEEP>
 __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[PER], const float (&b)[PER],
                              Selection<PER>& out, float mx) {
@@ -615,7 +633,6 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
   const float th = out.scal[0];
   bool full = false;
   float m = -INFINITY;
-  uint32_t ncand = 0;  // candidates of the last ranking
   for (;;) {
     // Candidates: a compact list in out.cl, wavefront by wavefront.
     bool member[PER];
@@ -651,17 +668,38 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
     if (lane == 0) out.red[0][wave] = lm;
     __syncthreads();
     m = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
-    // The reference's key: exp(fl(L - m)) (reference_ops.cpp:141-145), by
-    // expert in out.aux and in list order in ckey (the products' buffer is
-    // free now), so that the ranking reads keys without an indirection.
-    float* ckey = &out.prod[0][0][0];
+    // The reference's numerator e = exp(fl(L - m)) (reference_ops.cpp:141-145)
+    // with the host libm's bits, by expert in out.aux.
     float key[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      key[j] = member[j] ? expf(out.ex[base + j] - m) : -1.0f;
+      key[j] = member[j] ? osm_libm_expf(out.ex[base + j] - m) : -1.0f;
       if (base + j < E) out.aux[base + j] = key[j];
-      if (member[j]) ckey[cpos[j]] = key[j];
     }
+    if (full) {
+      // Every expert is a member: the reference's probabilities, S summed in
+      // id order with each addition rounded (reference_ops.cpp:140-144), then
+      // p = fl(e / S) (:149-151), which rank the experts.
+      __syncthreads();
+      if (tid == 0) {
+#pragma clang fp contract(off)
+        const uint32_t n8 = E & ~7u;
+        float s = chain_sum(out.aux, n8, 0.0f);
+        for (uint32_t e = n8; e < E; ++e) s = s + out.aux[e];
+        out.scal[2] = s;
+      }
+      __syncthreads();
+      const float S = out.scal[2];
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (member[j]) key[j] = __fdiv_rn(key[j], S);
+    }
+    // Ranking keys in list order in ckey (the products' buffer is free now),
+    // so that the ranking reads them without an indirection.
+    float* ckey = &out.prod[0][0][0];
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (member[j]) ckey[cpos[j]] = key[j];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -677,37 +715,40 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
       if (rk <= k) out.fid[rk] = e;
     }
     __syncthreads();
-    // Beyond 80 below m the exps near underflow: rank every expert.
-    const bool again = !full && !(out.ex[out.fid[k - 1]] - m >= -kUnderflowGap);
+    if (full) {
+      if (tid == 0) out.ncand = nc;
+      break;
+    }
+    // Adjacent candidates among the first k + 1 (there are at least k: the
+    // device's picks are candidates), one pair per lane: a pair ranked with
+    // the higher id first whose e are close enough for their quotients by S
+    // to round to one p, where the reference would put the lower id first.
+    if (tid < kWave) {
+      const uint32_t n = nc < k + 1u ? nc : k + 1u;
+      bool near = false;
+      if (lane + 1u < n) {
+        const uint32_t a = out.fid[lane], c = out.fid[lane + 1u];
+        const float ea = out.aux[a], ec = out.aux[c];  // ea >= ec (ranked)
+        near = a > c && ea != ec && ea - ec <= 0x1p-22f * ea + 0x1p-138f;
+      }
+      const uint32_t count = static_cast<uint32_t>(__popcll(__ballot(near)));
+      if (lane == 0) out.nneartie = count;
+    }
+    __syncthreads();
+    // Such a pair, or exps near underflow beyond 80 below m: rank every
+    // expert by the reference's probabilities.
+    const bool again = out.nneartie != 0u || !(out.ex[out.fid[k - 1]] - m >= -kUnderflowGap);
     if (!again) {
       if (tid == 0) out.ncand = nc;
-      ncand = nc;
       break;
     }
     full = true;
     __syncthreads();
   }
-  if (tid < kWave) {
-    // Adjacent pairs among the first k + 1 ranked candidates (there are at
-    // least k: the device's picks are candidates), one pair per lane.
-    const uint32_t n = ncand < k + 1u ? ncand : k + 1u;
-    bool unresolved = false;
-    if (lane + 1u < n) {
-      const uint32_t a = out.fid[lane], c = out.fid[lane + 1u];
-      // Equal logits give equal keys: the lower id first, certainly.
-      if (out.ex[a] != out.ex[c]) {
-        const float ea = out.aux[a], ec = out.aux[c];
-        const bool zeros = ea == 0.0f && ec == 0.0f && out.ex[a] - m < -104.0f && out.ex[c] - m < -104.0f;
-        unresolved = !zeros && fabsf(ea - ec) <= 5.0f * 0x1p-23f * fmaxf(ea, ec) + 5.0f * 0x1p-149f;
-      }
-    }
-    const uint32_t count = static_cast<uint32_t>(__popcll(__ballot(unresolved)));
-    if (lane == 0) out.nunresolved = count;
-    if (lane < k) {
-      const uint32_t id = out.fid[lane];
-      out.id[lane] = id;
-      out.lg[lane] = out.val[id];
-    }
+  if (tid < k) {
+    const uint32_t id = out.fid[tid];
+    out.id[tid] = id;
+    out.lg[tid] = out.val[id];
   }
   __syncthreads();
   return full;
@@ -915,7 +956,7 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
     atomicAdd(rv.stats + 0, 1u);
     if (bad) atomicAdd(rv.stats + 1, 1u);
     if (full) atomicAdd(rv.stats + 2, 1u);
-    if (bad && out.nunresolved != 0u) atomicAdd(rv.stats + 3, out.nunresolved);
+    if (bad && out.nneartie != 0u) atomicAdd(rv.stats + 3, out.nneartie);
   }
   __syncthreads();
 }
@@ -929,7 +970,7 @@ __device__ __forceinline__ void count_selection(const RouteView& rv, const Selec
   atomicAdd(rv.stats + 0, 1u);
   if (bad) atomicAdd(rv.stats + 1, 1u);
   if (s.flags & 2u) atomicAdd(rv.stats + 2, 1u);
-  if (bad && s.nunresolved != 0u) atomicAdd(rv.stats + 3, s.nunresolved);
+  if (bad && s.nneartie != 0u) atomicAdd(rv.stats + 3, s.nneartie);
 }
 
 // Router GEMM planes summed with every load in flight first (up to 8 K
@@ -1367,7 +1408,12 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
       rows(rv.shared_expert);
     }
   } else {
-    rows(p.src.blob(t, j));
+    // Host-driven slots: every slot in order, or the listed ones.
+    const uint32_t js = p.list.count ? slot_at(p.list, j) : j;
+    const uint8_t* blob = p.src.blob(t, js);
+    float xr[CPL][32];
+    gate_up_rows<META, CPL, ROWS>(p, t, js, blockIdx.x, blob ? blob : p.rv.fallback, xr,
+                                  [&](size_t i, float v) { p.h[i] = v; });
   }
 }
 
@@ -1397,21 +1443,27 @@ size_t down_lds_bytes(uint32_t inter, uint32_t nslot, uint32_t rows_per_block) {
 
 
 // down + weighted accumulate for rows blk * rows_per_block ... of token t.
-template <int META, int LPR, int MAXS>
+// MODE kDownParts writes each listed slot's per-lane partial instead; MODE
+// kDownCombine reads every slot's partial back in place of computing it and
+// then accumulates exactly as kDownFused does.
+template <int META, int LPR, int MAXS, int MODE>
 __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint32_t blk, float* hs) {
   constexpr uint32_t kRowsPerGroup = kWave / LPR;
   constexpr uint32_t kRowsPerBlock = down_rows_per_block<LPR>();
   constexpr int kSlotsPerWave = (MAXS + 1) / 2;
   const uint32_t D = p.g.hidden, I = p.g.inter, G = p.g.group;
   const uint32_t nslot = p.src.nslot;
+  // The slots this launch covers, by cover index: every slot in order, or
+  // the list.
+  const uint32_t ncover = MODE == kDownParts ? p.list.count : nslot;
   const uint32_t nchd = I / 32u;
   const uint32_t gpr = I / G;
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid % kWave;
   const uint32_t wave = tid / kWave;
   const uint32_t rg = wave & 1u;    // row group
-  // Slots half, half + 2, ...: wavefront-uniform, so the slot pointers and
-  // weights below are scalar loads issued together.
+  // Cover indices half, half + 2, ...: wavefront-uniform, so the slot
+  // pointers and weights below are scalar loads issued together.
   const uint32_t half = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(wave >> 1)));
   const uint32_t c = lane % LPR;
   const uint32_t row_local = rg * kRowsPerGroup + lane / LPR;
@@ -1422,6 +1474,10 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   const osm_expert_offsets off = osm_expert_layout(p.g);
   float* hsum = hs + static_cast<size_t>(nslot) * nchd * kChunkStride;
   float* halves = hsum + static_cast<size_t>(nslot) * nchd;
+  // Per-lane partial of slot j at this lane's row and chunk.
+  auto part_at = [&](uint32_t j) {
+    return ((static_cast<size_t>(t) * nslot + j) * D + rr) * LPR + c;
+  };
 
   const float4* h4 = reinterpret_cast<const float4*>(p.h + static_cast<size_t>(t) * nslot * I);
   const uint32_t n4 = nslot * I / 4u;  // a multiple of 8 (I % 32 == 0)
@@ -1434,78 +1490,97 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
       hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
+  if constexpr (MODE != kDownCombine) load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
 
   // This wavefront's slots: lane l loads slot l's pointer and weight (vector
   // loads, in flight with h's), each slot's are then read from its lane, and
   // the packed chunk and metadata of each are loaded with no branch between
-  // them. Slots past nslot and null pointers read a valid blob with weight 0.
+  // them. Slots past nslot and null pointers read a valid blob with weight 0
+  // (the combine reads no pointer: every slot it adds was resident).
   const uint32_t ls = lane < nslot ? lane : 0u;
-  const uint8_t* lp = p.src.blob(t, ls);
+  const uint8_t* lp = MODE == kDownCombine ? nullptr : p.src.blob(t, ls);
   // Per-lane addresses (a routing weight, or the shared gate): one vector load.
   const float* wsrc = ls < p.top_k ? (p.weights ? p.weights + static_cast<size_t>(t) * p.top_k + ls : nullptr)
                                    : (p.shared_gate ? p.shared_gate + t : nullptr);
   const float lw = wsrc ? ldg<float>(wsrc) : 1.0f;
   const uint8_t* bp[kSlotsPerWave];
   float w[kSlotsPerWave];
+  uint32_t js[kSlotsPerWave];
 #pragma unroll
   for (int i = 0; i < kSlotsPerWave; ++i) {
-    const uint32_t j = half + 2u * i;
+    const uint32_t ci = half + 2u * i;
+    const uint32_t j = ci < ncover ? (MODE == kDownParts ? slot_at(p.list, ci) : ci) : nslot;
     const int src = static_cast<int>(j < nslot ? j : 0u);
     const uint64_t pv = reinterpret_cast<uint64_t>(lp);
     const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pv), src));
     const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pv >> 32), src));
     bp[i] = reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
     w[i] = readlane_f(lw, src);
-    if (j >= nslot || bp[i] == nullptr) w[i] = 0.0f;
+    js[i] = j < nslot ? j : 0u;
+    if (j >= nslot || (MODE != kDownCombine && bp[i] == nullptr)) w[i] = 0.0f;
     if (bp[i] == nullptr) bp[i] = p.fallback;
   }
   uint4 q[kSlotsPerWave];
   uint32_t sb[kSlotsPerWave], bb[kSlotsPerWave];
+  float pin[kSlotsPerWave];
   const size_t qo = (static_cast<size_t>(rr) * nchd + cc) * 16u;
   const size_t gi = static_cast<size_t>(rr) * gpr + (cc * 32u) / G;
 #pragma unroll
   for (int i = 0; i < kSlotsPerWave; ++i) {
-    q[i] = ldg16(bp[i] + off.down_q + qo);
-    sb[i] = meta_bits<META>(bp[i] + off.down_s, gi);
-    bb[i] = meta_bits<META>(bp[i] + off.down_b, gi);
+    if constexpr (MODE == kDownCombine) {
+      pin[i] = (active && half + 2u * i < nslot) ? p.parts[part_at(js[i])] : 0.0f;
+    } else {
+      q[i] = ldg16(bp[i] + off.down_q + qo);
+      sb[i] = meta_bits<META>(bp[i] + off.down_s, gi);
+      bb[i] = meta_bits<META>(bp[i] + off.down_b, gi);
+    }
   }
 
-  // Stage h and its per-chunk sums: 8 consecutive threads hold one 32-float
-  // chunk, summed with DPP within the lane group. The first batch is staged
-  // while the weights are in flight (only its own loads are waited for);
-  // h of more than kH4PerThread * 1024 floats takes further passes.
-  auto stage = [&](uint32_t pass) {
+  if constexpr (MODE != kDownCombine) {
+    // Stage h and its per-chunk sums: 8 consecutive threads hold one 32-float
+    // chunk, summed with DPP within the lane group. The first batch is staged
+    // while the weights are in flight (only its own loads are waited for);
+    // h of more than kH4PerThread * 1024 floats takes further passes.
+    auto stage = [&](uint32_t pass) {
 #pragma unroll
-    for (int u = 0; u < kH4PerThread; ++u) {
-      const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
-      const float s4 = row_sum<8>((hv[u].x + hv[u].y) + (hv[u].z + hv[u].w));
-      if (f < n4) {
-        const uint32_t chunk = f / 8u;  // slot * nchd + chunk in the slot
-        *reinterpret_cast<float4*>(hs + chunk * kChunkStride + (f % 8u) * 4u) = hv[u];
-        if ((tid & 7u) == 0u) hsum[chunk] = s4;
+      for (int u = 0; u < kH4PerThread; ++u) {
+        const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
+        const float s4 = row_sum<8>((hv[u].x + hv[u].y) + (hv[u].z + hv[u].w));
+        if (f < n4) {
+          const uint32_t chunk = f / 8u;  // slot * nchd + chunk in the slot
+          *reinterpret_cast<float4*>(hs + chunk * kChunkStride + (f % 8u) * 4u) = hv[u];
+          if ((tid & 7u) == 0u) hsum[chunk] = s4;
+        }
       }
+    };
+    stage(0);
+    for (uint32_t pass = 1; pass * kH4PerThread * kDownThreads < n4; ++pass) {
+      load_h(pass);
+      stage(pass);
     }
-  };
-  stage(0);
-  for (uint32_t pass = 1; pass * kH4PerThread * kDownThreads < n4; ++pass) {
-    load_h(pass);
-    stage(pass);
+    __syncthreads();
   }
-  __syncthreads();
 
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < kSlotsPerWave; ++i) {
-    const uint32_t j = half + 2u * i;
-    const uint32_t js = j < nslot ? j : 0u;
-    const uint32_t chunk = js * nchd + cc;
-    const float part = meta_widen<META>(sb[i]) * nib_dot32(q[i], hs + chunk * kChunkStride) +
-                       meta_widen<META>(bb[i]) * hsum[chunk];
-    acc += w[i] * part;
+    float part;
+    if constexpr (MODE == kDownCombine) {
+      part = pin[i];
+    } else {
+      const uint32_t chunk = js[i] * nchd + cc;
+      part = meta_widen<META>(sb[i]) * nib_dot32(q[i], hs + chunk * kChunkStride) +
+             meta_widen<META>(bb[i]) * hsum[chunk];
+    }
+    if constexpr (MODE == kDownParts) {
+      if (active && half + 2u * i < ncover) p.parts[part_at(js[i])] = part;
+    } else {
+      acc = fmaf(w[i], part, acc);
+    }
     // Keep each slot's LDS reads next to their use.
     __builtin_amdgcn_sched_barrier(0);
   }
+  if constexpr (MODE == kDownParts) return;
   if (!active) acc = 0.0f;
   if constexpr (LPR <= 16)
     acc = row_sum<LPR>(acc);
@@ -1523,10 +1598,10 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   }
 }
 
-template <int META, int LPR, int MAXS>
+template <int META, int LPR, int MAXS, int MODE>
 __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   extern __shared__ __align__(16) float hs[];  // chunks, then chunk sums, then [2][rows] halves
-  down_block<META, LPR, MAXS>(p, blockIdx.y, blockIdx.x, hs);
+  down_block<META, LPR, MAXS, MODE>(p, blockIdx.y, blockIdx.x, hs);
 }
 
 
@@ -1543,7 +1618,8 @@ template <int META, int CPL>
 int launch_gate_up_cpl(const GateUpParams& gp, uint32_t tokens, int per, hipStream_t st) {
   const bool one = tokens == 1u;
   const uint32_t rows_per_block = kGuWaves * (one ? kGuRowsOneToken : kGuRowsBatched);
-  const dim3 grid((gp.g.inter + rows_per_block - 1) / rows_per_block, gp.src.nslot, tokens);
+  const dim3 grid((gp.g.inter + rows_per_block - 1) / rows_per_block, gp.list.count ? gp.list.count : gp.src.nslot,
+                  tokens);
   switch (per) {
     case 0:
       if (one) gate_up_kernel<META, CPL, 0, kGuRowsOneToken><<<grid, 256, 0, st>>>(gp);
@@ -1578,45 +1654,56 @@ int launch_gate_up(const GateUpParams& gp, uint32_t tokens, int per, hipStream_t
   }
 }
 
-template <int META, int LPR>
+// The slots per wavefront follow the slot count (the list's for kDownParts):
+// the combine of nslot slots therefore runs the fused form's loop for
+// nslot, which is what makes its sums the same.
+template <int META, int LPR, int MODE>
 int launch_down_lpr(const DownParams& dp, uint32_t tokens, hipStream_t st) {
   constexpr uint32_t rows_per_block = down_rows_per_block<LPR>();
   const dim3 grid((dp.g.hidden + rows_per_block - 1) / rows_per_block, tokens);
   const size_t lds = down_lds_bytes(dp.g.inter, dp.src.nslot, rows_per_block);
-  const uint32_t n = dp.src.nslot;
+  const uint32_t n = MODE == kDownParts ? dp.list.count : dp.src.nslot;
   if (n <= 2u)
-    down_kernel<META, LPR, 2><<<grid, kDownThreads, lds, st>>>(dp);
+    down_kernel<META, LPR, 2, MODE><<<grid, kDownThreads, lds, st>>>(dp);
   else if (n <= 4u)
-    down_kernel<META, LPR, 4><<<grid, kDownThreads, lds, st>>>(dp);
+    down_kernel<META, LPR, 4, MODE><<<grid, kDownThreads, lds, st>>>(dp);
   else if (n <= 8u)
-    down_kernel<META, LPR, 8><<<grid, kDownThreads, lds, st>>>(dp);
+    down_kernel<META, LPR, 8, MODE><<<grid, kDownThreads, lds, st>>>(dp);
   else if (n <= 12u)
-    down_kernel<META, LPR, 12><<<grid, kDownThreads, lds, st>>>(dp);
+    down_kernel<META, LPR, 12, MODE><<<grid, kDownThreads, lds, st>>>(dp);
   else
-    down_kernel<META, LPR, kMaxSlots + 1><<<grid, kDownThreads, lds, st>>>(dp);
+    down_kernel<META, LPR, kMaxSlots + 1, MODE><<<grid, kDownThreads, lds, st>>>(dp);
   return launch_status();
 }
 
-template <int META>
+template <int META, int MODE>
 int launch_down_meta(const DownParams& dp, uint32_t tokens, hipStream_t st) {
   switch (pow2_at_least(dp.g.inter / 32u)) {
-    case 1: return launch_down_lpr<META, 1>(dp, tokens, st);
-    case 2: return launch_down_lpr<META, 2>(dp, tokens, st);
-    case 4: return launch_down_lpr<META, 4>(dp, tokens, st);
-    case 8: return launch_down_lpr<META, 8>(dp, tokens, st);
-    case 16: return launch_down_lpr<META, 16>(dp, tokens, st);
-    case 32: return launch_down_lpr<META, 32>(dp, tokens, st);
-    default: return launch_down_lpr<META, 64>(dp, tokens, st);
+    case 1: return launch_down_lpr<META, 1, MODE>(dp, tokens, st);
+    case 2: return launch_down_lpr<META, 2, MODE>(dp, tokens, st);
+    case 4: return launch_down_lpr<META, 4, MODE>(dp, tokens, st);
+    case 8: return launch_down_lpr<META, 8, MODE>(dp, tokens, st);
+    case 16: return launch_down_lpr<META, 16, MODE>(dp, tokens, st);
+    case 32: return launch_down_lpr<META, 32, MODE>(dp, tokens, st);
+    default: return launch_down_lpr<META, 64, MODE>(dp, tokens, st);
+  }
+}
+
+template <int MODE>
+int launch_down_mode(const DownParams& dp, uint32_t tokens, hipStream_t st) {
+  switch (dp.g.meta_dtype) {
+    case OSM_META_F32: return launch_down_meta<OSM_META_F32, MODE>(dp, tokens, st);
+    case OSM_META_F16: return launch_down_meta<OSM_META_F16, MODE>(dp, tokens, st);
+    default: return launch_down_meta<OSM_META_BF16, MODE>(dp, tokens, st);
   }
 }
 
 int launch_down(const DownParams& dp, uint32_t tokens, hipStream_t st) {
-  switch (dp.g.meta_dtype) {
-    case OSM_META_F32: return launch_down_meta<OSM_META_F32>(dp, tokens, st);
-    case OSM_META_F16: return launch_down_meta<OSM_META_F16>(dp, tokens, st);
-    default: return launch_down_meta<OSM_META_BF16>(dp, tokens, st);
-  }
+  return launch_down_mode<kDownFused>(dp, tokens, st);
 }
+
+// Lanes per output row of the down kernel (the partials' last dimension).
+uint32_t down_lanes_per_row(uint32_t inter) { return static_cast<uint32_t>(pow2_at_least(inter / 32u)); }
 
 // Experts per lane of a selection: 2 up to 512 experts, 4 beyond. One width
 // for every expert count in a range keeps the order of the wavefront sums of
@@ -1677,7 +1764,7 @@ int launch_select(const osmd_moe_args& a, hipStream_t st) {
 
 GateUpParams gate_up_params(const osmd_moe_args& a) {
   const uint32_t nslot = a.top_k + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  GateUpParams gp;
+  GateUpParams gp{};
   gp.g = a.geom;
   gp.src = SlotSource{a.slot_ptrs, nullptr, nslot};
   gp.rv = route_view(a);
@@ -1688,7 +1775,7 @@ GateUpParams gate_up_params(const osmd_moe_args& a) {
 
 DownParams down_params(const osmd_moe_args& a) {
   const uint32_t nslot = a.top_k + ((a.flags & OSMD_MOE_SHARED) ? 1u : 0u);
-  DownParams dp;
+  DownParams dp{};
   dp.g = a.geom;
   dp.src = SlotSource{a.slot_ptrs, nullptr, nslot};
   dp.top_k = a.top_k;
@@ -1742,6 +1829,37 @@ int osmd_moe_down(const osmd_moe_args* a, osmd_stream s) {
 int osmd_moe_experts(const osmd_moe_args* a, osmd_stream s) {
   const int r = osmd_moe_gate_up(a, s);
   return r != 0 ? r : osmd_moe_down(a, s);
+}
+
+size_t osmd_moe_parts_bytes(const osm_expert_geometry* g, uint32_t nslot, uint32_t tokens) {
+  return static_cast<size_t>(tokens) * nslot * g->hidden * down_lanes_per_row(g->inter) * sizeof(float);
+}
+
+int osmd_moe_experts_parts(const osmd_moe_args* a, osmd_slot_list slots, float* parts, osmd_stream s) {
+  const uint32_t nslot = a->top_k + ((a->flags & OSMD_MOE_SHARED) ? 1u : 0u);
+  if (slots.count == 0u || slots.count > nslot || parts == nullptr || a->expert_table != nullptr)
+    return static_cast<int>(hipErrorInvalidValue);
+  for (uint32_t i = 0; i < slots.count; ++i) {
+    const uint32_t j = static_cast<uint32_t>((i < 12u ? slots.lo >> (5u * i) : slots.hi >> (5u * (i - 12u))) & 31u);
+    if (j >= nslot) return static_cast<int>(hipErrorInvalidValue);
+  }
+  const hipStream_t st = static_cast<hipStream_t>(s);
+  GateUpParams gp = gate_up_params(*a);
+  gp.list = slots;
+  gp.src.nslot = nslot;
+  int r = launch_gate_up(gp, a->tokens, 0, st);
+  if (r != 0) return r;
+  DownParams dp = down_params(*a);
+  dp.list = slots;
+  dp.parts = parts;
+  return launch_down_mode<kDownParts>(dp, a->tokens, st);
+}
+
+int osmd_moe_combine(const osmd_moe_args* a, const float* parts, osmd_stream s) {
+  if (parts == nullptr) return static_cast<int>(hipErrorInvalidValue);
+  DownParams dp = down_params(*a);
+  dp.parts = const_cast<float*>(parts);
+  return launch_down_mode<kDownCombine>(dp, a->tokens, static_cast<hipStream_t>(s));
 }
 
 // From this many tokens on, the per-token decode selects in its own launch

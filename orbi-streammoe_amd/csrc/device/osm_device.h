@@ -53,6 +53,11 @@ int osmd_event_synchronize(osmd_event e);
 int osmd_stream_wait_event(osmd_stream s, osmd_event e);
 int osmd_event_elapsed_ms(osmd_event start, osmd_event stop, float* ms);
 int osmd_device_synchronize(void);
+/* Block checksums of osm_libm_expf (the selection's exp) over float bit
+ * patterns first .. first + count - 1: sums[b] = sum over block b's inputs i
+ * (i from 0) of bits(exp(x)) * (2 i + 1) mod 2^64, ceil(count / block)
+ * blocks, in device memory. */
+int osmd_libm_expf_checksums(uint32_t first, uint64_t count, uint32_t block, uint64_t* sums, osmd_stream s);
 /* The fixed workspace of the decode entry point that allocates nothing: a
  * file-scope device array of OSMD_STATIC_SCRATCH_BYTES, one copy per GPU,
  * held until the process ends. _init looks its address up on `device`,
@@ -186,6 +191,30 @@ int osmd_moe_down(const osmd_moe_args* a, osmd_stream s);
 /* The selection kernel alone: top-k of a->logits for a->tokens tokens into
  * ids / weights / mass (and slot_ptrs from expert_table when set). */
 int osmd_moe_select(const osmd_moe_args* a, osmd_stream s);
+
+/* Host-driven residency in rounds (a capped cache runs some slots before
+ * others are resident: picks that are already resident while the rest are
+ * filled, or a budget that cannot hold a token's picks at once):
+ *   osmd_moe_experts_parts: gate/up and down of the listed slots only (every
+ *     token), each slot's per-row partials written to parts;
+ *   osmd_moe_combine: y from the partials of every slot (and the residual),
+ *     accumulated exactly as osmd_moe_experts's down kernel accumulates, so
+ *     the result has its bits however the slots were split.
+ * parts holds osmd_moe_parts_bytes() bytes ([B][k+1][D][lanes per row]).
+ * Slot list: count indices (< k + 1), 5 bits each, entries 0-11 in lo and
+ * 12-16 in hi (osmd_slot_list_add). */
+typedef struct osmd_slot_list {
+  uint64_t lo, hi;
+  uint32_t count;
+} osmd_slot_list;
+static inline void osmd_slot_list_add(osmd_slot_list* l, uint32_t slot) {
+  const uint32_t i = l->count++;
+  if (i < 12u) l->lo |= (uint64_t)(slot & 31u) << (5u * i);
+  else l->hi |= (uint64_t)(slot & 31u) << (5u * (i - 12u));
+}
+size_t osmd_moe_parts_bytes(const osm_expert_geometry* g, uint32_t nslot, uint32_t tokens);
+int osmd_moe_experts_parts(const osmd_moe_args* a, osmd_slot_list slots, float* parts, osmd_stream s);
+int osmd_moe_combine(const osmd_moe_args* a, const float* parts, osmd_stream s);
 
 /* ---- grouped (multi-token) MoE ------------------------------------------
  * The routed-MoE sublayer for moe.tokens tokens with every (token, slot)

@@ -26,6 +26,28 @@ __global__ void copy16_kernel(const uint4* __restrict__ src, uint4* __restrict__
     dst[i] = src[i];
 }
 
+// Checksums of the selection's exp (osm_libm_expf) over a range of float bit
+// patterns: block b covers inputs first + b * block ..., and its sum is
+// sum_i bits(exp(x_i)) * (2 i + 1) mod 2^64 over its inputs i (an odd
+// multiplier, so any single wrong result changes the sum).
+__global__ __launch_bounds__(256) void libm_expf_sums_kernel(uint32_t first, uint64_t count, uint32_t block,
+                                                             uint64_t* __restrict__ sums) {
+  __shared__ uint64_t red[256];
+  const uint64_t b0 = static_cast<uint64_t>(blockIdx.x) * block;
+  uint64_t s = 0;
+  for (uint32_t i = threadIdx.x; i < block && b0 + i < count; i += 256u) {
+    const float x = __uint_as_float(first + static_cast<uint32_t>(b0 + i));
+    s += static_cast<uint64_t>(__float_as_uint(osm_libm_expf(x))) * (2u * static_cast<uint64_t>(i) + 1u);
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (uint32_t w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sums[blockIdx.x] = red[0];
+}
+
 }  // namespace
 
 extern "C" {
@@ -35,6 +57,14 @@ const char* osmd_error_string(int code) {
 }
 
 int osmd_device_count(int* count) { return rc(hipGetDeviceCount(count)); }
+
+int osmd_libm_expf_checksums(uint32_t first, uint64_t count, uint32_t block, uint64_t* sums, osmd_stream s) {
+  const uint64_t nblocks = (count + block - 1u) / block;
+  if (count == 0u || block == 0u || nblocks > 0x7FFFFFFFu) return static_cast<int>(hipErrorInvalidValue);
+  libm_expf_sums_kernel<<<static_cast<uint32_t>(nblocks), 256, 0, static_cast<hipStream_t>(s)>>>(first, count, block,
+                                                                                                 sums);
+  return rc(hipGetLastError());
+}
 int osmd_set_device(int device) { return rc(hipSetDevice(device)); }
 
 int osmd_device_name(int device, char* buf, size_t n) {

@@ -159,19 +159,20 @@ LfuRecencyPolicy::LfuRecencyPolicy(std::size_t budget_bytes) : budget_bytes_(bud
 }
 
 std::uint64_t LfuRecencyPolicy::victim() const {
-  bool have = false;
-  std::uint64_t v = 0;
-  std::tuple<std::size_t, std::uint64_t, std::uint64_t> best{};
-  for (const auto& [key, node] : entries_) {
-    const auto score = std::make_tuple(node.frequency, node.last_use, key);
-    if (!have || score < best) {
-      best = score;
-      v = key;
-      have = true;
-    }
+  if (order_.empty()) throw std::runtime_error("resident expert cache: no eviction victim available");
+  return std::get<2>(*order_.begin());
+}
+
+std::vector<std::uint64_t> LfuRecencyPolicy::victims_of(std::uint32_t layer, std::uint32_t expert,
+                                                        std::size_t accounted_bytes) const {
+  std::vector<std::uint64_t> out;
+  if (entries_.count(make_key(layer, expert)) != 0 || accounted_bytes > budget_bytes_) return out;
+  std::size_t resident = resident_bytes_;
+  for (auto it = order_.begin(); it != order_.end() && resident + accounted_bytes > budget_bytes_; ++it) {
+    out.push_back(std::get<2>(*it));
+    resident -= entries_.at(std::get<2>(*it)).bytes;
   }
-  if (!have) throw std::runtime_error("resident expert cache: no eviction victim available");
-  return v;
+  return out;
 }
 
 bool LfuRecencyPolicy::touch(std::uint32_t layer, std::uint32_t expert) {
@@ -181,8 +182,10 @@ bool LfuRecencyPolicy::touch(std::uint32_t layer, std::uint32_t expert) {
   history_[key] = f;
   if (auto it = entries_.find(key); it != entries_.end()) {
     ++hits;
+    order_.erase(Rank{it->second.frequency, it->second.last_use, key});
     it->second.frequency = f;
     it->second.last_use = tick_;
+    order_.insert(Rank{f, tick_, key});
     return true;
   }
   ++misses;
@@ -201,12 +204,14 @@ std::vector<std::uint64_t> LfuRecencyPolicy::admit(std::uint32_t layer, std::uin
     const std::uint64_t v = victim();
     auto it = entries_.find(v);
     resident_bytes_ -= it->second.bytes;
+    order_.erase(Rank{it->second.frequency, it->second.last_use, v});
     entries_.erase(it);
     ++evictions;
     evicted.push_back(v);
   }
   if (!entries_.emplace(key, Node{accounted_bytes, history_[key], tick_}).second)
     throw std::runtime_error("resident expert cache: duplicate insertion");
+  order_.insert(Rank{history_[key], tick_, key});
   resident_bytes_ += accounted_bytes;
   ++loads;
   return evicted;
@@ -224,6 +229,7 @@ void LfuRecencyPolicy::forget(std::uint64_t key) noexcept {
   auto it = entries_.find(key);
   if (it == entries_.end()) return;
   resident_bytes_ -= it->second.bytes;
+  order_.erase(Rank{it->second.frequency, it->second.last_use, key});
   entries_.erase(it);
   if (loads > 0) --loads;
 }
@@ -485,6 +491,10 @@ HipValuesResult HipResidentExpertCache::run(std::uint32_t layer, std::uint32_t e
 
 bool HipResidentExpertCache::contains(std::uint32_t layer, std::uint32_t expert) const noexcept {
   return impl_->policy.contains(layer, expert);
+}
+
+std::vector<std::uint64_t> HipResidentExpertCache::victims_of(std::uint32_t layer, std::uint32_t expert) const {
+  return impl_->policy.victims_of(layer, expert, impl_->stride);
 }
 
 const std::uint8_t* HipResidentExpertCache::resident_blob(std::uint32_t layer, std::uint32_t expert) const noexcept {

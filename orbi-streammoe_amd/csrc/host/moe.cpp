@@ -40,6 +40,75 @@ bool finite_q8(const osm_affine_q8& m, std::size_t rows, std::size_t cols) {
   return true;
 }
 
+// Slot-pointer tables of a call's expert launches. Each is written on the
+// host into pinned memory that a copy kernel on the compute stream reads when
+// it runs, so a table is filled once and never rewritten until the call has
+// drained; the copy lands in the table's device mirror. Chunks are kept
+// across calls (every call ends with its stream drained) and reused after
+// reset().
+class PtrTables {
+ public:
+  void reset() noexcept {
+    for (Chunk& c : chunks_) c.used = 0;
+    cur_ = 0;
+  }
+  // A fresh table of n pointers, 256-byte aligned and padded to 256 bytes.
+  int take(std::size_t n, const std::uint8_t**& host, const std::uint8_t**& dev) {
+    const std::size_t bytes = (n * sizeof(void*) + 255U) & ~static_cast<std::size_t>(255U);
+    while (cur_ < chunks_.size() && chunks_[cur_].used + bytes > chunks_[cur_].cap) ++cur_;
+    if (cur_ == chunks_.size()) {
+      Chunk c;
+      c.cap = std::max<std::size_t>(bytes, 64U << 10U);
+      int rc = c.h.allocate(c.cap);
+      if (rc == 0) rc = c.d.allocate(c.cap);
+      if (rc != 0) return rc;
+      chunks_.push_back(std::move(c));
+    }
+    Chunk& c = chunks_[cur_];
+    host = reinterpret_cast<const std::uint8_t**>(static_cast<std::uint8_t*>(c.h.get()) + c.used);
+    dev = reinterpret_cast<const std::uint8_t**>(c.d.as<std::uint8_t>() + c.used);
+    c.used += bytes;
+    return 0;
+  }
+  static std::size_t padded(std::size_t n) { return (n * sizeof(void*) + 255U) & ~static_cast<std::size_t>(255U); }
+
+ private:
+  struct Chunk {
+    PinnedBytes h;
+    DeviceBytes d;
+    std::size_t cap = 0, used = 0;
+  };
+  std::vector<Chunk> chunks_;
+  std::size_t cur_ = 0;
+};
+
+// Events that mark the slots a launch read (the capped cache's pipelined
+// refills wait for them). Reused after reset(), once the call has drained.
+class EventPool {
+ public:
+  EventPool() = default;
+  EventPool(const EventPool&) = delete;
+  EventPool& operator=(const EventPool&) = delete;
+  ~EventPool() {
+    for (osmd_event e : ev_) osmd_event_destroy(e);
+  }
+  void reset() noexcept { used_ = 0; }
+  int next(osmd_event& out) {
+    if (used_ == ev_.size()) {
+      osmd_event e = nullptr;
+      const int rc = osmd_event_create(&e);
+      if (rc != 0) return rc;
+      ev_.push_back(e);
+    }
+    out = ev_[used_++];
+    return 0;
+  }
+
+ private:
+  std::vector<osmd_event> ev_;
+  std::size_t used_ = 0;
+};
+
 }  // namespace
 
 struct HipMoeLayer::Impl {
@@ -58,6 +127,29 @@ struct HipMoeLayer::Impl {
   PinnedBytes host_ptrs;  // staging for slot pointers chosen on the host
   PinnedBytes host_io;    // cache-driven path: pinned staging of inputs and outputs (grown on use)
   DeviceBytes dev_io;     // its device mirror: one copy in, one copy out per call
+  // Cache-driven path: slot tables, events marking the slots each launch
+  // read, and the per-slot partials of runs split into rounds (grown on use;
+  // a buffer outgrown during a call is kept until the next call starts).
+  PtrTables tables;
+  EventPool events;
+  DeviceBytes parts;
+  std::vector<DeviceBytes> parts_retired;
+  void begin_cached_call() noexcept {
+    tables.reset();
+    events.reset();
+    parts_retired.clear();
+  }
+  float* ensure_parts(std::uint32_t tokens, int* rc) {
+    const std::size_t need = osmd_moe_parts_bytes(&cfg.geometry, nslot(), tokens);
+    if (parts.size() < need) {
+      DeviceBytes fresh;
+      *rc = fresh.allocate(need);
+      if (*rc != 0) return nullptr;
+      if (parts.get() != nullptr) parts_retired.push_back(std::move(parts));
+      parts = std::move(fresh);
+    }
+    return parts.as<float>();
+  }
   // grouped (multi-token) path: carved per call from the context's shared
   // workspace (every layer on one stream uses the same memory in turn)
   HipMoePath path = HipMoePath::automatic;
@@ -674,32 +766,200 @@ HipMoeResult HipMoeLayer::run(HipComputeContext& context, std::span<const float>
 
 // Internal access for the cache-driven path.
 struct MoeLayerAccess {
-  static HipMoeLayer::Impl* impl(HipMoeLayer& l) { return l.impl_.get(); }
+  using Impl = HipMoeLayer::Impl;
+  static Impl* impl(HipMoeLayer& l) { return l.impl_.get(); }
 };
 
-bool run_cached_stack_picks(HipComputeContext& context, HipResidentExpertCache& cache,
-                            std::span<HipMoeLayer* const> layers, const std::uint32_t* cache_layers,
-                            std::span<const float> x, const std::uint32_t* pick_ids, const float* pick_weights,
-                            float* y, std::string* diagnostic) noexcept {
+namespace {
+
+std::size_t align256(std::size_t v) { return (v + 255U) & ~static_cast<std::size_t>(255U); }
+
+// One layer's routed picks through the capped cache. The picks are made
+// resident in pick order, token by token, as the reference fetches them
+// (routed_moe.cpp:320-366), and their experts run:
+//  - all at once, with the fused expert kernels, when every pick of the
+//    call is resident together (the usual case);
+//  - otherwise in rounds: a round ends just before a get that would evict
+//    one of its own picks, and its experts then run while every one of them
+//    is still resident -- so any budget of at least one expert works, as in
+//    the reference, which runs each pick right after its get;
+//  - with split_hits, a round's picks that were resident before it began run
+//    before the compute stream waits for the round's fills, so they overlap
+//    the copies.
+// Rounds write per-slot partials and a combine launch adds them exactly as
+// the fused down kernel adds them, so every split gives the fused bits.
+struct CachedLayerRun {
+  CachedLayerRun(HipComputeContext& c, HipResidentExpertCache& e, MoeLayerAccess::Impl& l) : ctx(c), cache(e), m(l) {}
+  HipComputeContext& ctx;
+  HipResidentExpertCache& cache;
+  MoeLayerAccess::Impl& m;
+  std::uint32_t cache_layer = 0;
+  std::uint32_t tokens = 0;
+  const std::uint32_t* ids = nullptr;  // host [tokens][k]
+  osmd_moe_args ae{};                  // the experts' arguments (slot_ptrs is set per launch)
+  bool pipelined = false;              // cache in pipelined mode: mark the slots each launch read
+  bool split_hits = false;
+  std::string* diag = nullptr;
+
+  struct Pick {
+    std::uint32_t t, j;
+    bool ready;  // resident before this round's fills
+  };
+  std::vector<Pick> pend;
+  std::unordered_set<std::uint64_t> pend_keys, filled;
+  bool used_parts = false, shared_done = false;
+
+  // A table of every token's slots: the given picks' blobs and the shared
+  // expert's, copied to the device on the compute stream.
+  int table(std::span<const Pick> picks, bool shared, const std::uint8_t**& dev) {
+    const std::uint32_t nslot = m.nslot(), K = m.cfg.top_k;
+    const std::uint8_t** host = nullptr;
+    int rc = m.tables.take(static_cast<std::size_t>(tokens) * nslot, host, dev);
+    if (rc != 0) return rc;
+    std::fill(host, host + static_cast<std::size_t>(tokens) * nslot, nullptr);
+    for (const Pick& p : picks)
+      host[p.t * nslot + p.j] = cache.resident_blob(cache_layer, ids[p.t * K + p.j]);
+    if (shared)
+      for (std::uint32_t t = 0; t < tokens; ++t) host[t * nslot + K] = m.shared_blob.as<const std::uint8_t>();
+    return osmd_copy_d2d(dev, host, PtrTables::padded(static_cast<std::size_t>(tokens) * nslot), ctx.stream());
+  }
+
+  // Marks the slots of `picks` as read by everything enqueued so far.
+  int mark(std::span<const Pick> picks) {
+    if (!pipelined) return 0;
+    osmd_event ev = nullptr;
+    int rc = m.events.next(ev);
+    if (rc == 0) rc = osmd_event_record(ev, ctx.stream());
+    if (rc != 0) return rc;
+    for (const Pick& p : picks) cache.mark_readers(cache_layer, ids[p.t * m.cfg.top_k + p.j], ev);
+    return 0;
+  }
+
+  // Token t's listed slots, writing their partials.
+  int launch_parts(std::uint32_t t, const osmd_slot_list& l, const std::uint8_t** dev_table, float* parts) {
+    const std::size_t D = m.cfg.geometry.hidden, I = m.cfg.geometry.inter, nslot = m.nslot(), K = m.cfg.top_k;
+    osmd_moe_args a = ae;
+    a.tokens = 1;
+    a.x_norm = ae.x_norm + t * D;
+    a.h = ae.h + t * nslot * I;
+    a.slot_ptrs = dev_table + t * nslot;
+    a.weights = ae.weights + t * K;
+    a.shared_gate = ae.shared_gate + t;
+    return osmd_moe_experts_parts(&a, l, parts + osmd_moe_parts_bytes(&m.cfg.geometry, m.nslot(), t) / sizeof(float),
+                                  ctx.stream());
+  }
+
+  // Runs the pending picks (and the shared expert, the first time), then
+  // starts a new fill batch.
+  int flush() {
+    const std::uint32_t K = m.cfg.top_k;
+    int rc = 0;
+    float* parts = m.ensure_parts(tokens, &rc);
+    if (parts == nullptr) return rc != 0 ? rc : 1;
+    const bool shared = !shared_done && m.cfg.has_shared_expert;
+    const std::uint8_t** dev = nullptr;
+    rc = table(pend, shared, dev);
+    if (rc != 0) return rc;
+    std::vector<osmd_slot_list> first(tokens, osmd_slot_list{}), second(tokens, osmd_slot_list{});
+    for (const Pick& p : pend) osmd_slot_list_add(split_hits && p.ready ? &first[p.t] : &second[p.t], p.j);
+    if (shared)
+      for (std::uint32_t t = 0; t < tokens; ++t) osmd_slot_list_add(&first[t], K);
+    shared_done = true;
+    for (std::uint32_t t = 0; t < tokens && rc == 0; ++t)
+      if (first[t].count) rc = launch_parts(t, first[t], dev, parts);
+    const int frc = cache.end_fills();
+    if (rc == 0) rc = frc;
+    for (std::uint32_t t = 0; t < tokens && rc == 0; ++t)
+      if (second[t].count) rc = launch_parts(t, second[t], dev, parts);
+    if (rc == 0) rc = mark(pend);
+    cache.begin_fills();
+    pend.clear();
+    pend_keys.clear();
+    filled.clear();
+    used_parts = true;
+    return rc;
+  }
+
+  // 0, a HIP error code, or -1 with the diagnostic set.
+  int run() {
+    const std::uint32_t K = m.cfg.top_k;
+    const std::size_t D = m.cfg.geometry.hidden;
+    shared_done = !m.cfg.has_shared_expert;
+    auto fail = [&](std::string d) {
+      (void)cache.end_fills();
+      set_diag(diag, std::move(d));
+      return -1;
+    };
+    cache.begin_fills();
+    int rc = 0;
+    for (std::uint32_t t = 0; t < tokens; ++t)
+      for (std::uint32_t j = 0; j < K; ++j) {
+        const std::uint32_t id = ids[t * K + j];
+        const std::uint64_t key = LfuRecencyPolicy::make_key(cache_layer, id);
+        if (!cache.contains(cache_layer, id)) {
+          for (const std::uint64_t v : cache.victims_of(cache_layer, id))
+            if (pend_keys.count(v) != 0) {
+              rc = flush();
+              if (rc != 0) return (void)cache.end_fills(), rc;
+              break;
+            }
+        }
+        const bool ready = cache.contains(cache_layer, id) && filled.count(key) == 0;
+        std::string gd;
+        HipResidentExpert* e = cache.get(cache_layer, id, &gd);
+        if (e == nullptr) return fail("Qwen sparse MoE routed expert " + std::to_string(id) + " load failed: " + gd);
+        if (e->input_dim() != D || e->output_dim() != D || e->intermediate_dim() != m.cfg.geometry.inter)
+          return fail("Qwen sparse MoE routed expert geometry mismatch");
+        if (!ready) filled.insert(key);
+        pend.push_back({t, j, ready});
+        pend_keys.insert(key);
+      }
+    std::size_t nready = 0;
+    for (const Pick& p : pend) nready += p.ready ? 1U : 0U;
+    if (!used_parts && (!split_hits || nready == 0 || nready == pend.size())) {
+      // Every pick resident at once: the fused kernels.
+      const std::uint8_t** dev = nullptr;
+      rc = table(pend, m.cfg.has_shared_expert, dev);
+      const int frc = cache.end_fills();
+      if (rc == 0) rc = frc;
+      osmd_moe_args a = ae;
+      a.slot_ptrs = dev;
+      if (rc == 0) rc = osmd_moe_experts(&a, ctx.stream());
+      if (rc == 0) rc = mark(pend);
+      return rc;
+    }
+    rc = flush();
+    (void)cache.end_fills();
+    if (rc == 0) rc = osmd_moe_combine(&ae, m.parts.as<const float>(), ctx.stream());
+    return rc;
+  }
+};
+
+}  // namespace
+
+bool run_cached_stack(HipComputeContext& context, HipResidentExpertCache& cache,
+                      std::span<HipMoeLayer* const> layers, const std::uint32_t* cache_layers,
+                      std::span<const float> x, const std::uint32_t* pick_ids, const float* pick_weights,
+                      float* y, std::string* diagnostic) noexcept {
   auto fail = [&](std::string d) {
     if (diagnostic) *diagnostic = std::move(d);
     return false;
   };
-  std::vector<osmd_event> done;
   bool pipelined = false;
+  osmd_event ids_ready = nullptr;
   auto cleanup = [&]() {
     if (pipelined) {
       (void)osmd_stream_synchronize(context.stream());
       cache.end_pipeline();
       pipelined = false;
     }
-    for (osmd_event e : done)
-      if (e != nullptr) osmd_event_destroy(e);
-    done.clear();
+    if (ids_ready != nullptr) osmd_event_destroy(ids_ready);
+    ids_ready = nullptr;
   };
   try {
     const std::size_t n = layers.size();
-    if (n == 0 || cache_layers == nullptr || pick_ids == nullptr || pick_weights == nullptr || y == nullptr)
+    const bool given = pick_ids != nullptr;
+    if (n == 0 || cache_layers == nullptr || y == nullptr || given != (pick_weights != nullptr))
       return fail("invalid arguments");
     auto* m0 = layers[0] ? MoeLayerAccess::impl(*layers[0]) : nullptr;
     if (m0 == nullptr || !layers[0]->valid()) return fail("layer 0: MoE layer is not valid");
@@ -707,99 +967,57 @@ bool run_cached_stack_picks(HipComputeContext& context, HipResidentExpertCache& 
     const std::uint32_t tokens = static_cast<std::uint32_t>(x.size() / (D ? D : 1));
     if (tokens == 0 || x.size() != tokens * D) return fail("qwen router: hidden vector size mismatch");
     if (!all_finite(x)) return fail("qwen router: hidden vector contains non-finite value");
-    std::size_t E_max = 0, nslot_max = 0;
+    std::size_t E_max = 0;
     for (std::size_t i = 0; i < n; ++i) {
       auto* m = layers[i] ? MoeLayerAccess::impl(*layers[i]) : nullptr;
       const std::string at = "layer " + std::to_string(i) + ": ";
       if (m == nullptr || !layers[i]->valid()) return fail(at + "MoE layer is not valid");
       if (m->cfg.geometry.hidden != D) return fail("layers must share one hidden size");
-      if (m->cfg.top_k != K) return fail("given picks need one top_k");
+      if (m->cfg.top_k != K) return fail("layers of one stack need one top_k");
       if (tokens > m->max_tokens) return fail(at + "qwen router: hidden vector size mismatch");
       if (m->norm_weight.get() == nullptr) return fail(at + "MoE sublayer decode needs an RMSNorm weight");
-      for (std::size_t j = 0; j < tokens * K; ++j) {
-        const std::size_t o = i * tokens * K + j;
-        if (pick_ids[o] >= m->cfg.expert_count)
-          return fail(at + "routed MoE pick " + std::to_string(pick_ids[o]) + " is out of range");
-        if (!std::isfinite(pick_weights[o])) return fail(at + "routed MoE encountered a non-finite routing weight");
-      }
+      if (given)
+        for (std::size_t j = 0; j < tokens * K; ++j) {
+          const std::size_t o = i * tokens * K + j;
+          if (pick_ids[o] >= m->cfg.expert_count)
+            return fail(at + "routed MoE pick " + std::to_string(pick_ids[o]) + " is out of range");
+          if (!std::isfinite(pick_weights[o])) return fail(at + "routed MoE encountered a non-finite routing weight");
+        }
       E_max = std::max<std::size_t>(E_max, m->cfg.expert_count);
-      nslot_max = std::max<std::size_t>(nslot_max, m->nslot());
     }
     if (!context.activate(diagnostic)) return false;
     const osmd_stream st = context.stream();
+    for (std::size_t i = 0; i < n; ++i) MoeLayerAccess::impl(*layers[i])->begin_cached_call();
 
-    // Device block: two activation buffers (layer outputs alternate), every
-    // layer's pick weights and slot pointers, and the routing outputs one
-    // layer at a time. Pinned host mirror: x and the weights in, the slot
-    // pointers layer by layer, y out.
-    auto al = [](std::size_t v) { return (v + 255U) & ~static_cast<std::size_t>(255U); };
-    const std::size_t xb = x.size_bytes(), wb = n * tokens * K * 4U, pb = n * tokens * nslot_max * sizeof(void*);
-    const std::size_t o_a = 0, o_b = al(xb), o_w = o_b + al(xb), o_p = o_w + al(wb), o_norm = o_p + al(pb),
-                      o_lg = o_norm + al(xb), o_mass = o_lg + al(tokens * E_max * 4U), o_gate = o_mass + al(tokens * 4U),
-                      o_rid = o_gate + al(tokens * 4U), o_rw = o_rid + al(tokens * K * 4U),
-                      total = o_rw + al(tokens * K * 4U);
+    // Device block: two activation buffers (layer outputs alternate), the
+    // given picks' weights of every layer, and the routing outputs one layer
+    // at a time. Pinned host mirror: x and the weights in, each layer's
+    // routed ids out (device routing), y out.
+    const std::size_t xb = x.size_bytes(), wb = given ? n * tokens * K * 4U : 0U, kb = tokens * K * 4U;
+    const std::size_t o_a = 0, o_b = align256(xb), o_w = o_b + align256(xb), o_norm = o_w + align256(wb),
+                      o_lg = o_norm + align256(xb), o_mass = o_lg + align256(tokens * E_max * 4U),
+                      o_gate = o_mass + align256(tokens * 4U), o_rid = o_gate + align256(tokens * 4U),
+                      o_rw = o_rid + align256(kb), o_hid = o_rw + align256(kb),
+                      total = o_hid + (given ? 0U : n * align256(kb));
     DeviceBytes dev;
     PinnedBytes host;
     int rc = dev.allocate(total);
     if (rc == 0) rc = host.allocate(total);
-    if (rc != 0) return fail(hip_error("cached stack: staging allocation failed", rc));
+    if (rc == 0 && !given) rc = osmd_event_create(&ids_ready);
+    if (rc != 0) return cleanup(), fail(hip_error("cached stack: staging allocation failed", rc));
     auto* h = static_cast<std::uint8_t*>(host.get());
     auto* d = dev.as<std::uint8_t>();
     std::memcpy(h + o_a, x.data(), xb);
-    std::memcpy(h + o_w, pick_weights, wb);
-    rc = osmd_copy_d2d(d, h, o_p, st);  // x and every layer's weights
-    if (rc != 0) return fail(hip_error("cached stack: input copy failed", rc));
-    done.assign(n, nullptr);
-    for (std::size_t i = 0; i < n && rc == 0; ++i) rc = osmd_event_create(&done[i]);
-    if (rc != 0) return fail(hip_error("cached stack: event creation failed", rc));
+    if (given) std::memcpy(h + o_w, pick_weights, wb);
+    rc = osmd_copy_d2d(d, h, o_norm, st);  // x (and every layer's given weights)
+    if (rc != 0) return cleanup(), fail(hip_error("cached stack: input copy failed", rc));
 
     cache.begin_pipeline();
     pipelined = true;
     for (std::size_t i = 0; i < n; ++i) {
       auto* m = MoeLayerAccess::impl(*layers[i]);
-      const std::uint32_t nslot = m->nslot();
-      const std::uint32_t* ids = pick_ids + i * tokens * K;
-      const std::uint32_t cl = cache_layers[i];
       float* cur = reinterpret_cast<float*>(d + (i % 2 == 0 ? o_a : o_b));
       float* nxt = reinterpret_cast<float*>(d + (i % 2 == 0 ? o_b : o_a));
-      // Every pick resident (in pick order), the misses copied on the side
-      // streams; then every pick's slot from the final residency.
-      cache.begin_fills();
-      for (std::uint32_t t = 0; t < tokens; ++t)
-        for (std::size_t j = 0; j < K; ++j) {
-          std::string gd;
-          HipResidentExpert* e = cache.get(cl, ids[t * K + j], &gd);
-          if (e == nullptr) {
-            (void)cache.end_fills();
-            cleanup();
-            return fail("layer " + std::to_string(i) + ": Qwen sparse MoE routed expert " +
-                        std::to_string(ids[t * K + j]) + " load failed: " + gd);
-          }
-          if (e->input_dim() != D || e->output_dim() != D || e->intermediate_dim() != m->cfg.geometry.inter) {
-            (void)cache.end_fills();
-            cleanup();
-            return fail("layer " + std::to_string(i) + ": Qwen sparse MoE routed expert geometry mismatch");
-          }
-        }
-      auto* hp = reinterpret_cast<const std::uint8_t**>(h + o_p) + i * tokens * nslot_max;
-      for (std::uint32_t t = 0; t < tokens; ++t) {
-        for (std::size_t j = 0; j < K; ++j) hp[t * nslot + j] = cache.resident_blob(cl, ids[t * K + j]);
-        if (nslot > K) hp[t * nslot + K] = m->shared_blob.as<const std::uint8_t>();
-      }
-      for (std::size_t j = 0; j < tokens * K; ++j)
-        if (hp[(j / K) * nslot + j % K] == nullptr) {
-          (void)cache.end_fills();
-          cleanup();
-          return fail("layer " + std::to_string(i) +
-                      ": Qwen sparse MoE: the cache budget cannot hold every expert of this batch at once");
-        }
-      const std::size_t po = o_p + i * tokens * nslot_max * sizeof(void*);
-      rc = osmd_copy_d2d(d + po, h + po, al(tokens * nslot * sizeof(void*)), st);
-      const int frc = cache.end_fills();
-      if (rc == 0) rc = frc;
-      // The sublayer: RMSNorm + router (its outputs to the shared routing
-      // block), then the experts with the given weights and slots, plus the
-      // residual.
       osmd_moe_args ar = m->args(cur, nxt, tokens, nullptr, true);
       ar.x_norm = reinterpret_cast<float*>(d + o_norm);
       ar.logits = reinterpret_cast<float*>(d + o_lg);
@@ -807,20 +1025,42 @@ bool run_cached_stack_picks(HipComputeContext& context, HipResidentExpertCache& 
       ar.weights = reinterpret_cast<float*>(d + o_rw);
       ar.mass = reinterpret_cast<float*>(d + o_mass);
       ar.shared_gate = reinterpret_cast<float*>(d + o_gate);
+      const std::uint32_t* ids = nullptr;
       osmd_moe_args ae = ar;
-      ae.slot_ptrs = reinterpret_cast<const std::uint8_t**>(d + po);
-      ae.weights = reinterpret_cast<float*>(d + o_w) + i * tokens * K;
-      if (rc == 0) rc = osmd_moe_route(&ar, st);
-      if (rc == 0) rc = osmd_moe_experts(&ae, st);
-      if (rc == 0) rc = osmd_event_record(done[i], st);
+      if (given) {
+        // The router alone: the RMSNorm output and the shared gate (the
+        // selection would be discarded).
+        rc = osmd_moe_router(&ar, st);
+        ids = pick_ids + i * tokens * K;
+        ae.weights = reinterpret_cast<float*>(d + o_w) + i * tokens * K;
+      } else {
+        // Route and select on the device, then read the ids: the host decides
+        // residency from them, as the reference's cache does.
+        auto* hid = h + o_hid + i * align256(kb);
+        rc = osmd_moe_route(&ar, st);
+        if (rc == 0) rc = osmd_copy_d2d(hid, d + o_rid, align256(kb), st);
+        if (rc == 0) rc = osmd_event_record(ids_ready, st);
+        if (rc == 0) rc = osmd_event_synchronize(ids_ready);
+        ids = reinterpret_cast<const std::uint32_t*>(hid);
+      }
+      if (rc != 0) return cleanup(), fail("layer " + std::to_string(i) + ": " + hip_error("cached stack routing failed", rc));
+      std::string ld;
+      CachedLayerRun run(context, cache, *m);
+      run.cache_layer = cache_layers[i];
+      run.tokens = tokens;
+      run.ids = ids;
+      run.ae = ae;
+      run.pipelined = true;
+      run.split_hits = !given;
+      run.diag = &ld;
+      rc = run.run();
       if (rc != 0) {
         cleanup();
-        return fail("layer " + std::to_string(i) + ": " + hip_error("cached stack launch failed", rc));
+        return fail("layer " + std::to_string(i) + ": " + (rc < 0 ? ld : hip_error("cached stack launch failed", rc)));
       }
-      for (std::size_t j = 0; j < tokens * K; ++j) cache.mark_readers(cl, ids[j], done[i]);
     }
     const std::size_t o_y = n % 2 == 0 ? o_a : o_b;
-    rc = osmd_copy_d2d(h + o_y, d + o_y, al(xb), st);
+    rc = osmd_copy_d2d(h + o_y, d + o_y, align256(xb), st);
     if (rc == 0) rc = osmd_stream_synchronize(st);
     cleanup();
     if (rc != 0) return fail(hip_error("cached stack failed", rc));
@@ -874,24 +1114,21 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
       }
     }
     if (!context.activate(&r.diagnostic)) return r;
+    m->begin_cached_call();
     const osmd_stream st = context.stream();
     const std::size_t E = m->cfg.expert_count;
-    const std::uint32_t nslot = m->nslot();
     // Inputs and outputs of the call sit in one device block mirrored by
-    // pinned host staging: [x | pick ids | pick weights | slot pointers]
-    // then [y | normalised x | mass | shared gate | logits | ids | weights].
-    // With given picks that is one copy in and one out; with device routing
-    // the ids come back first (one wait) and the slot pointers go in after.
-    // The copies are the library's 16-byte copy kernel reading or writing the
-    // pinned staging directly (every block is a multiple of 256 bytes): for
-    // these few kilobytes it takes a third of the runtime's copy.
-    auto al = [](std::size_t n) { return (n + 255U) & ~static_cast<std::size_t>(255U); };
-    const std::size_t xb = hidden.size_bytes(), kb = tokens * K * 4U, tb = tokens * 4U, eb = tokens * E * 4U,
-                      pb = tokens * nslot * sizeof(void*);
-    const std::size_t o_x = 0, o_pid = al(xb), o_pw = o_pid + al(kb), o_ptr = o_pw + al(kb),
-                      o_out = o_ptr + al(pb), o_y = o_out, o_norm = o_y + al(xb), o_mass = o_norm + al(xb),
-                      o_gate = o_mass + al(tb), o_lg = o_gate + al(tb), o_rid = o_lg + al(eb),
-                      o_rw = o_rid + al(kb), io_bytes = o_rw + al(kb);
+    // pinned host staging: [x | pick weights] then [y | normalised x | mass |
+    // shared gate | logits | ids | weights]. With given picks that is one
+    // copy in and one out; with device routing the ids come back first (one
+    // wait). The copies are the library's 16-byte copy kernel reading or
+    // writing the pinned staging directly (every block is a multiple of 256
+    // bytes): for these few kilobytes it takes a third of the runtime's copy.
+    const std::size_t xb = hidden.size_bytes(), kb = tokens * K * 4U, tb = tokens * 4U, eb = tokens * E * 4U;
+    const std::size_t o_x = 0, o_pw = align256(xb), o_out = o_pw + align256(kb), o_y = o_out,
+                      o_norm = o_y + align256(xb), o_mass = o_norm + align256(xb), o_gate = o_mass + align256(tb),
+                      o_lg = o_gate + align256(tb), o_rid = o_lg + align256(eb), o_rw = o_rid + align256(kb),
+                      io_bytes = o_rw + align256(kb);
     if (m->host_io.size() < io_bytes || m->dev_io.size() < io_bytes) {
       m->host_io.reset();
       m->dev_io.reset();
@@ -914,101 +1151,72 @@ HipMoeResult run_qwen_sparse_moe_hip(HipComputeContext& context, HipResidentExpe
     ar.weights = dptr(o_rw);
     ar.mass = dptr(o_mass);
     ar.shared_gate = dptr(o_gate);
-    osmd_moe_args ae = ar;  // the experts read the host's slot pointers and the picks' weights
-    ae.slot_ptrs = reinterpret_cast<const std::uint8_t**>(dio + o_ptr);
+    osmd_moe_args ae = ar;  // the experts read the picks' weights
     if (picks != nullptr) ae.weights = dptr(o_pw);
 
     std::memcpy(io + o_x, hidden.data(), xb);
     const std::uint32_t* ids = nullptr;
     int rc = 0;
     if (picks != nullptr) {
-      std::memcpy(io + o_pid, picks->ids, kb);
+      // Given picks: x and their weights in, then the router alone (the
+      // RMSNorm output, logits and shared gate; no selection).
       std::memcpy(io + o_pw, picks->weights, kb);
+      rc = osmd_copy_d2d(dio, io, o_out, st);
+      if (rc == 0) rc = osmd_moe_router(&ar, st);
       ids = picks->ids;
     } else {
-      // 1. route on the device and read the ids back
-      rc = osmd_copy_d2d(dio + o_x, io + o_x, al(xb), st);
+      // Route on the device and read the ids back.
+      rc = osmd_copy_d2d(dio + o_x, io + o_x, align256(xb), st);
       if (rc == 0) rc = osmd_moe_route(&ar, st);
-      if (rc == 0) rc = osmd_copy_d2d(io + o_rid, dio + o_rid, al(kb), st);
+      if (rc == 0) rc = osmd_copy_d2d(io + o_rid, dio + o_rid, align256(kb), st);
       if (rc == 0) rc = osmd_stream_synchronize(st);
-      if (rc != 0) {
-        r.diagnostic = hip_error("Qwen sparse MoE routing failed", rc);
-        return r;
-      }
       ids = reinterpret_cast<const std::uint32_t*>(io + o_rid);
     }
-    // 2. make every pick resident (in pick order, as the reference does).
-    // The misses are copied back to back on the side stream, which waits
-    // once for the compute stream's earlier work; the compute stream waits
-    // once for the copies, before the expert kernels (with given picks the
-    // routing kernels run meanwhile: they read no expert slot).
-    auto* host_ptrs = reinterpret_cast<const std::uint8_t**>(io + o_ptr);
-    expert_cache.begin_fills();
-    for (std::uint32_t t = 0; t < tokens; ++t) {
-      for (std::size_t j = 0; j < K; ++j) {
-        const std::uint32_t id = ids[t * K + j];
-        std::string d;
-        HipResidentExpert* e = expert_cache.get(layer, id, &d);
-        if (e == nullptr) {
-          (void)expert_cache.end_fills();
-          r.diagnostic = "Qwen sparse MoE routed expert " + std::to_string(id) + " load failed: " + d;
-          return r;
-        }
-        if (e->input_dim() != D || e->output_dim() != D ||
-            e->intermediate_dim() != m->cfg.geometry.inter) {
-          (void)expert_cache.end_fills();
-          r.diagnostic = "Qwen sparse MoE routed expert geometry mismatch";
-          return r;
-        }
-      }
-      if (nslot > K) host_ptrs[t * nslot + K] = m->shared_blob.as<const std::uint8_t>();
-    }
-    // Every pick's slot from the final residency: a later miss of this batch
-    // can evict an expert admitted earlier in it and refill its slot (the
-    // expert, if picked again, was re-admitted elsewhere), so a pointer taken
-    // at the time of its get may name a slot that now holds another expert.
-    for (std::uint32_t t = 0; t < tokens; ++t)
-      for (std::size_t j = 0; j < K; ++j) host_ptrs[t * nslot + j] = expert_cache.resident_blob(layer, ids[t * K + j]);
-    if (picks != nullptr) {
-      rc = osmd_copy_d2d(dio, io, o_out, st);  // x, picks and slot pointers
-      if (rc == 0) rc = osmd_moe_route(&ar, st);
-    } else {
-      rc = osmd_copy_d2d(dio + o_ptr, io + o_ptr, al(pb), st);
-    }
-    const int frc = expert_cache.end_fills();
-    if (rc == 0) rc = frc;
     if (rc != 0) {
-      r.diagnostic = hip_error("Qwen sparse MoE: routing or expert fills failed", rc);
+      r.diagnostic = hip_error("Qwen sparse MoE routing failed", rc);
       return r;
     }
-    for (std::size_t i = 0; i < tokens * K; ++i)
-      if (host_ptrs[(i / K) * nslot + i % K] == nullptr) {
-        r.diagnostic = "Qwen sparse MoE: the cache budget cannot hold every expert of this batch at once";
-        return r;
-      }
-    // 3. expert kernels over the resident slots, then every output in one copy
-    rc = osmd_moe_experts(&ae, st);
+    // Every pick made resident in pick order and run (in rounds when the
+    // budget cannot hold them all; device-routed calls run the already
+    // resident picks while the misses are copied).
+    std::string ld;
+    CachedLayerRun run(context, expert_cache, *m);
+    run.cache_layer = layer;
+    run.tokens = tokens;
+    run.ids = ids;
+    run.ae = ae;
+    run.split_hits = picks == nullptr;
+    run.diag = &ld;
+    rc = run.run();
+    if (rc < 0) {
+      r.diagnostic = ld;
+      return r;
+    }
     if (rc == 0) rc = osmd_copy_d2d(io + o_out, dio + o_out, io_bytes - o_out, st);
     if (rc == 0) rc = osmd_stream_synchronize(st);
     if (rc != 0) {
       r.diagnostic = hip_error("Qwen sparse MoE expert phase failed", rc);
       return r;
     }
-    auto take = [&](std::size_t off, std::size_t n) {
+    auto take = [&](std::size_t off, std::size_t cnt) {
       const float* f = reinterpret_cast<const float*>(io + off);
-      return std::vector<float>(f, f + n);
+      return std::vector<float>(f, f + cnt);
     };
     r.values = take(o_y, hidden.size());
     if (sublayer) r.normalized = take(o_norm, hidden.size());
     if (picks != nullptr) {
       r.routing.ids.assign(picks->ids, picks->ids + tokens * K);
       r.routing.weights.assign(picks->weights, picks->weights + tokens * K);
+      // The given weights' sum in pick order (no selection ran).
+      r.routing.mass.assign(tokens, 0.0F);
+      for (std::uint32_t t = 0; t < tokens; ++t)
+        for (std::size_t j = 0; j < K; ++j) r.routing.mass[t] += picks->weights[t * K + j];
     } else {
       const auto* rid = reinterpret_cast<const std::uint32_t*>(io + o_rid);
       r.routing.ids.assign(rid, rid + tokens * K);
       r.routing.weights = take(o_rw, tokens * K);
+      r.routing.mass = take(o_mass, tokens);
     }
-    r.routing.mass = take(o_mass, tokens);
     r.routing.shared_gate = take(o_gate, tokens);
     if (!m->cfg.has_shared_expert) std::fill(r.routing.shared_gate.begin(), r.routing.shared_gate.end(), 0.0F);
     r.routing.logits = take(o_lg, tokens * E);

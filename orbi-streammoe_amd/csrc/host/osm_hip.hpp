@@ -17,9 +17,11 @@
 #include <memory>
 #include <mutex>
 #include <optional>
+#include <set>
 #include <span>
 #include <string>
 #include <string_view>
+#include <tuple>
 #include <unordered_map>
 #include <unordered_set>
 #include <vector>
@@ -551,6 +553,12 @@ class LfuRecencyPolicy {
   // Undo the insertion of a key whose fill failed.
   void forget(std::uint64_t key) noexcept;
   [[nodiscard]] bool contains(std::uint32_t layer, std::uint32_t expert) const noexcept;
+  // The keys a get of (layer, expert) would evict, in eviction order, with
+  // nothing changed: none on a hit or when it fits (a get's tick and
+  // frequency update touch no resident entry on a miss, so the victims are
+  // the same after it).
+  [[nodiscard]] std::vector<std::uint64_t> victims_of(std::uint32_t layer, std::uint32_t expert,
+                                                      std::size_t accounted_bytes) const;
   [[nodiscard]] static std::uint64_t make_key(std::uint32_t layer,
                                               std::uint32_t expert) noexcept {
     return (static_cast<std::uint64_t>(layer) << 32U) | expert;
@@ -570,10 +578,14 @@ class LfuRecencyPolicy {
     std::size_t frequency{};
     std::uint64_t last_use{};
   };
+  // Resident keys ordered by (frequency, last_use, key): the victim is the
+  // first (vulkan_resident_expert_cache.cpp's scan for the smallest triple).
+  using Rank = std::tuple<std::size_t, std::uint64_t, std::uint64_t>;
   [[nodiscard]] std::uint64_t victim() const;
   std::size_t budget_bytes_{};
   std::size_t resident_bytes_{};
   std::unordered_map<std::uint64_t, Node> entries_;
+  std::set<Rank> order_;
   std::unordered_map<std::uint64_t, std::size_t> history_;
   std::uint64_t tick_{};
 };
@@ -658,6 +670,9 @@ class HipResidentExpertCache {
   [[nodiscard]] HipValuesResult run(std::uint32_t layer, std::uint32_t expert,
                                     std::span<const float> x) noexcept;
   [[nodiscard]] bool contains(std::uint32_t layer, std::uint32_t expert) const noexcept;
+  // Keys ((layer << 32) | expert) that get(layer, expert) would evict, with
+  // no tick and no policy update (empty on a hit or when it fits).
+  [[nodiscard]] std::vector<std::uint64_t> victims_of(std::uint32_t layer, std::uint32_t expert) const;
   // Device blob of a resident expert, or null; no tick, no policy update.
   [[nodiscard]] const std::uint8_t* resident_blob(std::uint32_t layer, std::uint32_t expert) const noexcept;
   [[nodiscard]] HipResidentExpertCacheStats stats() const noexcept;
@@ -899,15 +914,21 @@ class HipGraph {
   int device_ = -1;
 };
 
-// routed_moe.hpp:58-65 -- one token through the resident cache: route on the
-// device, make every pick resident (misses filled on the side stream), then
-// the fused expert kernels. The cache decides residency on the host from the
-// routed ids, as the reference's cache does.
+// routed_moe.hpp:58-65 -- tokens through the resident cache: route on the
+// device, make every pick resident in pick order (misses filled on the side
+// streams), then the expert kernels. The cache decides residency on the host
+// from the routed ids, as the reference's cache does. When the budget cannot
+// hold a call's picks at once they run in rounds, each just before a get
+// would evict one of its picks (the reference runs each pick right after its
+// get, routed_moe.cpp:320-366); with device routing, picks already resident
+// run while the misses are copied. Outputs have the bits of the fused
+// kernels whatever the split.
 // picks: null, or caller-chosen routed experts ([tokens, top_k] ids and
-// weights) that replace the router's picks. The router still runs for the
-// shared gate (and the logits and RMSNorm), and routing returns the given
-// ids and weights. No counterpart in the reference, whose routed MoE always
-// routes itself: it drives the cache with an external routing trace.
+// weights) that replace the router's picks. The router alone then runs for
+// the shared gate (and the logits and RMSNorm); routing returns the given
+// ids and weights, and their sum as the mass. No counterpart in the
+// reference, whose routed MoE always routes itself: it drives the cache with
+// an external routing trace.
 struct HipMoePicks {
   const std::uint32_t* ids = nullptr;
   const float* weights = nullptr;
@@ -918,15 +939,18 @@ struct HipMoePicks {
     bool sublayer, const HipMoePicks* picks = nullptr) noexcept;
 
 // The decoder stack's layer loop (checkpoint_decoder_stack.cpp:191-204) as
-// chained MoE sublayers over the capped cache, with every layer's picks
-// given (ids and weights [n][tokens][k]): the activations stay on the
-// device, no layer waits for the host, and each layer's fills wait only for
-// the kernels that last read the slots they overwrite. Every output is the
-// bits of run_qwen_sparse_moe_hip called layer by layer. y = the last
-// layer's output [tokens][D] (host). Returns false with a diagnostic.
-[[nodiscard]] bool run_cached_stack_picks(HipComputeContext& context, HipResidentExpertCache& expert_cache,
-                                          std::span<HipMoeLayer* const> layers, const std::uint32_t* cache_layers,
-                                          std::span<const float> x, const std::uint32_t* pick_ids,
-                                          const float* pick_weights, float* y, std::string* diagnostic) noexcept;
+// chained MoE sublayers over the capped cache. The activations stay on the
+// device between layers and each layer's fills wait only for the kernels
+// that last read the slots they overwrite. With every layer's picks given
+// (ids and weights [n][tokens][k], both null otherwise) no layer waits for
+// the host, so fills overlap earlier layers' kernels; with device routing
+// each layer's ids come back to the host, which decides residency. Every
+// output is the bits of run_qwen_sparse_moe_hip called layer by layer, in
+// rounds or not. y = the last layer's output [tokens][D] (host). Returns
+// false with a diagnostic.
+[[nodiscard]] bool run_cached_stack(HipComputeContext& context, HipResidentExpertCache& expert_cache,
+                                    std::span<HipMoeLayer* const> layers, const std::uint32_t* cache_layers,
+                                    std::span<const float> x, const std::uint32_t* pick_ids,
+                                    const float* pick_weights, float* y, std::string* diagnostic) noexcept;
 
 }  // namespace osm

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from ctypes import POINTER, c_char_p, c_float, c_int, c_int64, c_size_t, c_uint16, c_uint32, c_uint64, c_void_p
 
 import numpy as np
@@ -138,6 +139,7 @@ _PROTOTYPES = {
     "osm_moe_layer_prefill_device": (c_int, [_H, _H, _H, c_uint32, c_void_p, c_void_p, c_uint32]),
     "osm_moe_layer_routing": (c_int, [_H, _H, c_uint32, POINTER(MoeOutputs)]),
     "osm_moe_layer_routing_stats": (c_int, [_H, _H, POINTER(c_uint32), c_int]),
+    "osm_libm_expf_checksums": (c_int, [_H, c_uint32, c_uint64, c_uint32, c_void_p]),
     "osm_decode_graph_create": (c_int, [_H, POINTER(_H), POINTER(c_uint32), c_uint32, _H, c_void_p, c_void_p, c_void_p, c_uint32, c_int, POINTER(_H)]),
     "osm_graph_capture_begin": (c_int, [_H]),
     "osm_graph_capture_end": (c_int, [_H, POINTER(_H)]),
@@ -237,6 +239,14 @@ def device_count() -> int:
     return n.value if st == OSM_OK else 0
 
 
+def libm_expf_checksums(ctx, first_bits: int, count: int, block: int) -> np.ndarray:
+    """Block checksums of the selection's exp on the device over float bit
+    patterns first_bits .. first_bits + count - 1 (osm_libm_expf_checksums)."""
+    out = np.zeros((count + block - 1) // block, np.uint64)
+    check(load().osm_libm_expf_checksums(ctx.h, first_bits, count, block, _p(out)))
+    return out
+
+
 def geometry(hidden: int, inter: int, group: int = 64, meta_dtype: int = BF16) -> Geometry:
     return Geometry(hidden, inter, group, meta_dtype)
 
@@ -271,14 +281,32 @@ class _Handle:
 
 # ---- context / events / memory ------------------------------------------------------
 class Context(_Handle):
-    """HipComputeContext: one device, a compute stream and a fill stream."""
+    """HipComputeContext: one device, a compute stream and a fill stream.
+
+    The library's objects must not outlive the context they were created on
+    (the resident cache, for one, keeps using its streams until it is
+    destroyed). close() therefore closes every handle still open on this
+    context first, newest first, then the context."""
 
     _destroy = "osm_context_destroy"
 
     def __init__(self, device: int = 0):
+        self._children = []
         h = c_void_p()
         check(load().osm_context_create(device, ctypes.byref(h)))
         super().__init__(h)
+
+    def _adopt(self, child):
+        self._children = [r for r in self._children if r() is not None]
+        self._children.append(weakref.ref(child))
+
+    def close(self):
+        for ref in reversed(getattr(self, "_children", [])):
+            child = ref()
+            if child is not None:
+                child.close()
+        self._children = []
+        super().close()
 
     def synchronize(self):
         check(load().osm_context_synchronize(self.h))
@@ -310,6 +338,7 @@ class Event(_Handle):
         h = c_void_p()
         check(load().osm_event_create(ctx.h, ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
 
     def record(self):
         check(load().osm_event_record(self.h))
@@ -329,6 +358,7 @@ class DeviceArray:
         p = c_void_p()
         check(load().osm_device_alloc(ctx.h, nbytes, ctypes.byref(p)))
         self.ptr = p
+        ctx._adopt(self)
 
     def upload(self, a: np.ndarray):
         a = np.ascontiguousarray(a)
@@ -362,6 +392,7 @@ class FloatBuffer(_Handle):
         h = c_void_p()
         check(load().osm_buffer_create(ctx.h, count, ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
         self.count = count
 
     def upload(self, values):
@@ -443,6 +474,7 @@ class Q4ProjectionWeights(_Handle):
         h = c_void_p()
         check(load().osm_q4_projection_create(ctx.h, _p(pk), pk.size, out_dim, packed_cols, _p(s), _p(b), meta_dtype, group_size, ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
 
 
 def run_q4_gemv_preloaded(ctx, weights: Q4ProjectionWeights, x: FloatBuffer, y: FloatBuffer):
@@ -468,6 +500,7 @@ class ResidentExpert(_Handle):
         h = c_void_p()
         check(load().osm_expert_create(ctx.h, _p(bl), bl.size, ctypes.byref(g), ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
         self.ctx, self.g = ctx, g
 
     def run(self, x) -> np.ndarray:
@@ -498,6 +531,7 @@ class SharedExpert(_Handle):
         h = c_void_p()
         check(load().osm_shared_expert_create(ctx.h, _p(bl), bl.size, ctypes.byref(g), _p(sg), sg.size, ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
         self.ctx, self.g = ctx, g
 
     def scalar_scale(self, hidden) -> float:
@@ -524,6 +558,7 @@ class ExpertSlab(_Handle):
         h = c_void_p()
         check(load().osm_expert_slab_create(ctx.h, ctypes.byref(g), layers, experts, ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
         self.ctx, self.g, self.layers, self.experts = ctx, g, layers, experts
         self.stride = load().osm_expert_slab_stride(h)
 
@@ -582,6 +617,7 @@ class MoeLayer(_Handle):
             _p(nw) if nw is not None else None, _p(sb) if sb is not None else None,
             sb.size if sb is not None else 0, max_tokens, ctypes.byref(h)))
         super().__init__(h)
+        ctx._adopt(self)
         self.ctx, self.g, self.E, self.k, self.max_tokens = ctx, g, expert_count, top_k, max_tokens
         self._keep = (r, sg, nw, sb)
 
@@ -650,10 +686,13 @@ class MoeLayer(_Handle):
 
     def routing_stats(self, reset=False) -> dict:
         """Selections, those that took the exact path, exact paths over every
-        expert, and unresolved adjacent picks, since creation or a reset."""
+        expert, and the adjacent near ties (exps close enough for their
+        probabilities to round to one value, the higher id first) that sent a
+        selection to the recompute over every expert, since creation or a
+        reset."""
         v = (c_uint32 * 4)()
         check(load().osm_moe_layer_routing_stats(self.ctx.h, self.h, v, 1 if reset else 0))
-        return dict(zip(("selections", "exact", "exact_all", "unresolved"), list(v)))
+        return dict(zip(("selections", "exact", "exact_all", "near_ties"), list(v)))
 
     def launch_phase(self, slab, slab_layer, x_ptr, y_ptr, tokens, sublayer, phase):
         check(load().osm_moe_layer_launch_phase(self.ctx.h, self.h, slab.h, slab_layer, x_ptr, y_ptr, tokens, 1 if sublayer else 0, phase))
@@ -674,6 +713,7 @@ class Graph(_Handle):
 
     def __init__(self, ctx, h, keep=()):
         super().__init__(h)
+        ctx._adopt(self)
         self.ctx = ctx
         self._keep = keep
 
@@ -933,6 +973,7 @@ class ExpertCache(_Handle):
             check(load().osm_expert_cache_create_from_host_cache(ctx.h, host_cache.h, ctypes.byref(g), budget, ctypes.byref(h)))
             self.g = g
         super().__init__(h)
+        ctx._adopt(self)
         self.ctx = ctx
         self._keep = (store, host_cache)
 

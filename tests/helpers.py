@@ -226,3 +226,30 @@ def blob_to_slot(blob, sections, stride, D, I, G, meta_dtype, fill=0xA5):
         if s["name"] in parts:
             slot[s["offset"]:s["offset"] + s["size"]] = parts[s["name"]]
     return slot
+
+
+def correlated_trace(rng, layers, steps, k, experts, repeat_p):
+    """Routed experts per (step, layer), each [1, k] uint32: each of a layer's
+    k picks repeats one of that layer's previous-step picks with probability
+    repeat_p, else it is a fresh expert; picks within a step are distinct.
+    The capped-cache workload of the 48-layer stack (p = 0.6)."""
+    prev = [None] * layers
+    trace = []
+    for _s in range(steps):
+        row = []
+        for layer in range(layers):
+            ids = []
+            for _j in range(k):
+                cands = [e for e in (prev[layer] or []) if e not in ids]
+                if cands and rng.random() < repeat_p:
+                    ids.append(int(rng.choice(cands)))
+                    continue
+                while True:
+                    e = int(rng.integers(experts))
+                    if e not in ids:
+                        break
+                ids.append(e)
+            prev[layer] = ids
+            row.append(np.array(ids, np.uint32).reshape(1, k))
+        trace.append(row)
+    return trace

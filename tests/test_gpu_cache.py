@@ -12,8 +12,8 @@ import pytest
 
 import oracle as O
 import osm_hip
-from helpers import (blob_to_slot, cache_fixture_expert, cache_fixture_token, max_abs, qpack_q4_sections, rel_l2,
-                     write_qpack)
+from helpers import (blob_to_slot, cache_fixture_expert, cache_fixture_token, correlated_trace, max_abs,
+                     qpack_q4_sections, rel_l2, write_qpack)
 
 pytestmark = pytest.mark.gpu
 
@@ -136,11 +136,13 @@ def test_cached_decode_with_given_picks(ctx):
 def test_cached_batch_refills_its_own_slot(ctx):
     # A 4-expert budget, experts 0-3 used twice each. Picks [4, 5, 0, 1]: 4
     # misses and takes 0's slot (oldest of equal frequency), 5 misses and
-    # evicts 4 (frequency 1, this call's own fill) into the same slot, 0
-    # misses and evicts 5 into it again (restated policy: 3 evictions). The
-    # call fails, since 4 and 5 are no longer resident, and the slot must
-    # then hold 0's bytes, the last of its three copies in one fill batch:
-    # the later all-hit calls are checked against the oracle.
+    # would evict 4 (frequency 1, this call's own fill), 0 misses and would
+    # evict 5 (restated policy: 3 evictions). As the reference runs each pick
+    # right after its get (routed_moe.cpp:320-366), the call runs in rounds
+    # -- {4}, then {5} once 4's round has read the slot, then {0, 1} -- and
+    # its output is the oracle's sum of all four. The slot then holds 0's
+    # bytes, the last of its three copies: the later all-hit calls are
+    # checked against the oracle too.
     seed, D, I, G, E, k = 23, 256, 128, 64, 16, 4
     g = osm_hip.geometry(D, I, G, osm_hip.BF16)
     store = osm_hip.ExpertStore(g, 1, E)
@@ -160,8 +162,7 @@ def test_cached_batch_refills_its_own_slot(ctx):
 
     check([0, 1, 2, 3], 0)
     check([0, 1, 2, 3], 1)
-    with pytest.raises(osm_hip.OsmError):
-        moe.run_cached(cache, 0, O.synth_tokens(seed, 2, 1, D), picks=(np.array([[4, 5, 0, 1]], np.uint32), w))
+    check([4, 5, 0, 1], 2)
     assert cache.stats()["evictions"] == 3
     check([0, 1, 2, 3], 3)
     check([1, 2, 3, 0], 4)
@@ -314,3 +315,119 @@ def test_cached_layer_stack_matches_layer_calls(ctx):
             ref = moes[l].run_cached(b, l, ref, sublayer=True, picks=p)["out"]
         assert np.array_equal(got, ref)
         assert a.stats()["misses"] == b.stats()["misses"] > 0
+
+
+class SmallStack:
+    """Four sublayers of top-4 over 32 experts (hidden 256): a pinned host copy
+    of every expert, an all-resident slab of the same weights, the layers."""
+
+    seed, D, I, G, E, k, L = 31, 256, 128, 64, 32, 4, 4
+
+    def __init__(self, ctx):
+        s = self
+        s.g = osm_hip.geometry(s.D, s.I, s.G, osm_hip.BF16)
+        s.store = osm_hip.ExpertStore(s.g, s.L, s.E)
+        s.store.synthesize(ctx, s.seed)
+        s.slab = osm_hip.ExpertSlab(ctx, s.g, s.L, s.E)
+        s.slab.synthesize(s.seed)
+        s.norm = [O.synth_norm_weight(s.seed, l, s.D) for l in range(s.L)]
+        s.sg = [O.synth_shared_gate_bf16(s.seed, l, s.D) for l in range(s.L)]
+        s.shared = [O.synth_expert_blob(s.seed, l, O.SHARED_EXPERT_ID, s.D, s.I, s.G) for l in range(s.L)]
+        s.moes = [osm_hip.MoeLayer(ctx, s.g, s.E, s.k, O.synth_router_bf16(s.seed, l, s.E, s.D), osm_hip.BF16,
+                                   s.sg[l], s.norm[l], s.shared[l], max_tokens=2) for l in range(s.L)]
+
+    def oracle_chain(self, x, ids, w):
+        """The given-picks sublayers chained on the oracle."""
+        s = self
+        for l in range(s.L):
+            blobs = [O.synth_expert_blob(s.seed, l, int(e), s.D, s.I, s.G) for e in ids[l][0]]
+            x = O.moe_sublayer_picks(x, s.norm[l], 1e-6, w[l][0], blobs, s.shared[l], O.bf16_bits_to_f32(s.sg[l]),
+                                     s.D, s.I, s.G, O.META_BF16)
+        return x
+
+
+@pytest.mark.parametrize("slots", [64, 6, 3, 1])
+def test_cached_stack_under_eviction_given_picks(ctx, slots):
+    # The capped-cache stack with given picks (the 48-layer bench's path) on
+    # a correlated trace (p = 0.6), with a budget of 64 experts (all fit),
+    # 6 (about 1.5 k: a slot is refilled within one or two layers), 3 and 1
+    # (below k: a layer's picks run in rounds, each ending just before a get
+    # would evict one of its picks, routed_moe.cpp:320-366):
+    #  - the stack in one native call equals the layer-by-layer calls on a
+    #    second cache, bit for bit, token after token;
+    #  - every budget gives the bits of the 64-expert budget (the fused
+    #    kernels), so the rounds' partials and their combine change nothing;
+    #  - both caches' counters equal the restated policy over the picks;
+    #  - two tokens' outputs are within 1e-3 of the oracle's chain.
+    S = SmallStack(ctx)
+    steps = 8
+    rng = np.random.default_rng(5)
+    trace = correlated_trace(rng, S.L, steps, S.k, S.E, 0.6)
+    w = rng.random((steps, S.L, 1, S.k)).astype(np.float32)
+    w /= w.sum(axis=-1, keepdims=True)
+    xs = O.synth_tokens(S.seed, 40, steps, S.D)
+    stride = S.store.stride
+
+    def run(budget):
+        a = osm_hip.ExpertCache(ctx, budget * stride, store=S.store)
+        b = osm_hip.ExpertCache(ctx, budget * stride, store=S.store)
+        policy = O.DeviceCachePolicy(budget * stride)
+        outs = []
+        for s in range(steps):
+            ids = np.stack(trace[s])
+            got = osm_hip.run_cached_layers(ctx, S.moes, list(range(S.L)), a, xs[s], (ids, w[s]))
+            ref = xs[s]
+            for l in range(S.L):
+                ref = S.moes[l].run_cached(b, l, ref, sublayer=True, picks=(ids[l], w[s][l]))["out"]
+                for e in ids[l][0]:
+                    policy.get(l, int(e), stride)
+            assert np.array_equal(got.reshape(-1), np.asarray(ref).reshape(-1)), (budget, s)
+            outs.append(got.reshape(-1))
+        st, sb, po = a.stats(), b.stats(), policy.stats()
+        for key in ("hits", "misses", "loads", "evictions", "resident_entries"):
+            assert st[key] == sb[key] == po[key], (budget, key, st, sb, po)
+        a.close()
+        b.close()
+        return outs, st
+
+    outs, st = run(slots)
+    if slots < 64:
+        assert st["evictions"] > 0, st
+        full, _ = run(64)
+        for s in range(steps):
+            assert np.array_equal(outs[s], full[s]), (slots, s)
+    for s in (0, steps - 1):
+        ids = np.stack(trace[s])
+        assert rel_l2(outs[s], S.oracle_chain(xs[s], ids, w[s])) <= 1e-3, (slots, s)
+
+
+@pytest.mark.parametrize("slots", [6, 3, 1])
+def test_cached_stack_under_eviction_device_routing(ctx, slots):
+    # The same stack routed on the device: each layer's ids come back to the
+    # host, the picks already resident run while the misses are copied, and
+    # below k a layer's picks run in rounds. The stack in one call, the
+    # layer-by-layer calls on a second cache and the all-resident slab decode
+    # give the same bits; the counters equal the restated policy over the
+    # slab decode's routing.
+    S = SmallStack(ctx)
+    steps = 8
+    xs = O.synth_tokens(S.seed, 70, steps, S.D)
+    stride = S.store.stride
+    a = osm_hip.ExpertCache(ctx, slots * stride, store=S.store)
+    b = osm_hip.ExpertCache(ctx, slots * stride, store=S.store)
+    policy = O.DeviceCachePolicy(slots * stride)
+    for s in range(steps):
+        got = osm_hip.run_cached_layers(ctx, S.moes, list(range(S.L)), a, xs[s])
+        ref = res = xs[s]
+        for l in range(S.L):
+            ref = S.moes[l].run_cached(b, l, ref, sublayer=True)["out"]
+            r = S.moes[l].run_slab(S.slab, l, res, sublayer=True)
+            res = r["out"]
+            for e in r["ids"][0]:
+                policy.get(l, int(e), stride)
+        assert np.array_equal(got.reshape(-1), np.asarray(ref).reshape(-1)), (slots, s)
+        assert np.array_equal(got.reshape(-1), np.asarray(res).reshape(-1)), (slots, s)
+    st, sb, po = a.stats(), b.stats(), policy.stats()
+    for key in ("hits", "misses", "loads", "evictions", "resident_entries"):
+        assert st[key] == sb[key] == po[key], (slots, key, st, sb, po)
+    assert st["evictions"] > 0, st

@@ -131,13 +131,11 @@ def test_far_apart_logits_take_the_fast_path(ctx):
         assert np.array_equal(gpu["ids"][t], ora["ids"]), t
 
 
-def test_ties_within_exp_rounding_are_counted(ctx):
-    # Logits 2.5e-7..4.5e-7 apart (one or two ulps of a logit near 2): their
-    # exps are within a few ulps, where the
-    # reference's order also rests on the last bit of its exp and on how the
-    # division by the softmax sum rounds. The selection still ranks them by
-    # the exp of the reference's logits (here the oracle's order) and counts
-    # each such adjacent pair.
+def test_logits_one_or_two_ulps_apart(ctx):
+    # Logits 2.5e-7..4.5e-7 apart (one or two ulps of a logit near 2): the
+    # exact path ranks them by the reference's exps, with the host libm's
+    # bits, and any adjacent pair close enough for the probabilities to tie
+    # goes to the recompute over every expert. Ids are the oracle's.
     rng = np.random.default_rng(5)
     g = osm_hip.geometry(D, I, G, osm_hip.BF16)
     blob = random_blob(rng, D, I, G, O.META_BF16)[0]
@@ -151,7 +149,7 @@ def test_ties_within_exp_rounding_are_counted(ctx):
     gpu = moe.run_slab(slab, 0, x[None, :])
     assert np.array_equal(gpu["ids"][0], ora["ids"]), (list(gpu["ids"][0]), list(ora["ids"]))
     st = moe.routing_stats()
-    assert st["exact"] == 1 and st["unresolved"] >= 1, st
+    assert st["exact"] == 1, st
 
 
 def test_router_gemm_bounds_prove_most_tokens(ctx):
@@ -175,3 +173,180 @@ def test_router_gemm_bounds_prove_most_tokens(ctx):
     for t in range(T):
         ora = O.route_qwen_top_k(xw[t], router, L.D, L.E, L.k, True)
         assert np.array_equal(routing["ids"][t], ora["ids"]), t
+
+
+# ---------------------------------------------------------------------------
+# Probabilities that tie although the logits differ.
+#
+# The reference's probabilities are p = fl(e / S), e = std::exp(fl(L - m))
+# (the host libm's expf) and S the fp32 sum of every e in id order, ranked
+# with the lower id first among equal p (reference_ops.cpp:135-196). Two
+# different logits can give one p in three ways, and the router below
+# builds each with the lower logit on the lower id, where the reference puts
+# the LOWER logit first:
+#   (a) fl(L - m) differs but the two exps round to one float;
+#   (b) fl(L - m) itself rounds two logits to one key;
+#   (c) the exps are one ulp apart but e_a / S and e_b / S round to one float
+#       (inside the picks, and for the k-th pick against the (k+1)-th, where
+#       the tie decides which of the two is picked);
+# plus (d) exps one ulp apart whose quotients do not tie (the higher logit
+# first, as usual). Logits are set exactly: the input is 1, 2^-8, 2^-16 in
+# its first three columns and 0 elsewhere, and each router row holds bf16
+# w0, w1, w2 with w0 + w1 2^-8 + w2 2^-16 the target, every partial sum
+# exact in fp32.
+
+def _libm_expf():
+    import ctypes
+    import ctypes.util
+    f = ctypes.CDLL(ctypes.util.find_library("m")).expf
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_float]
+    return lambda v: np.float32(f(float(v)))
+
+
+def _bf16_rne(v):
+    b = int(np.array([v], np.float32).view(np.uint32)[0])
+    return (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+
+
+def _bf16_val(bits):
+    return float(np.array([bits << 16], np.uint32).view(np.float32)[0])
+
+
+def _exact_logit_row(target):
+    """bf16 (w0, w1, w2) with fl(fl(w0 + w1 2^-8) + w2 2^-16) == target."""
+    t = float(np.float32(target))
+    w0 = _bf16_rne(t)
+    r1 = t - _bf16_val(w0)
+    w1 = _bf16_rne(r1 * 256.0)
+    r2 = r1 - _bf16_val(w1) / 256.0
+    w2 = _bf16_rne(r2 * 65536.0)
+    got = np.float32(np.float32(_bf16_val(w0)) + np.float32(_bf16_val(w1) / 256.0))
+    got = np.float32(got + np.float32(_bf16_val(w2) / 65536.0))
+    assert got == np.float32(t), (target, got)
+    return w0, w1, w2
+
+
+def _softmax_sum(logits, expf):
+    m = np.float32(np.max(logits))
+    s = np.float32(0.0)
+    for v in logits:
+        s = np.float32(s + expf(np.float32(v - m)))
+    return s
+
+
+def tie_router(rng):
+    """(router bits [E, D], f32 router, x, pairs): pairs maps each case to its
+    (lower id, higher id) with the lower logit on the lower id."""
+    expf = _libm_expf()
+    ulp24 = 2.0 ** -24
+    logits = np.float32(-1.0) - np.float32(2.0) * rng.random(E).astype(np.float32)  # [-3, -1)
+    ids = rng.permutation(E)
+    top, rest = ids[:16], ids[16:]
+    lid = lambda a, b: (int(min(a, b)), int(max(a, b)))
+    m_id = int(top[0])
+    logits[m_id] = 1.0
+    pairs = {}
+    # (a) distinct keys, equal exps, near 0.70 (keys 2^-24 apart, exps 0.74 ulp apart).
+    base = 0.70
+    for j in range(4096):
+        lb = np.float32(base + j * ulp24)
+        la = np.float32(lb + ulp24)
+        xa, xb = np.float32(la - 1.0), np.float32(lb - 1.0)
+        if xa != xb and expf(xa) == expf(xb):
+            break
+    else:
+        raise AssertionError("no exp tie found")
+    lo, hi = lid(top[1], top[2])
+    logits[lo], logits[hi] = lb, la
+    pairs["exp_tie"] = (lo, hi)
+    # (b) one key from two logits near 0.45 (logits 2^-25 apart, keys 2^-24 apart).
+    for j in range(4096):
+        lb = np.float32(0.45 + j * 2.0 ** -25)
+        la = np.float32(lb + 2.0 ** -25)
+        if la != lb and np.float32(la - 1.0) == np.float32(lb - 1.0):
+            break
+    else:
+        raise AssertionError("no key tie found")
+    lo, hi = lid(top[3], top[4])
+    logits[lo], logits[hi] = lb, la
+    pairs["key_tie"] = (lo, hi)
+
+    # (c), (d): exps one ulp apart, with S over the final logits.
+    def one_ulp_pairs(start):
+        j = 0
+        while True:
+            lb = np.float32(start + j * 2.0 ** -24)
+            la = np.float32(lb + 2.0 ** -24)
+            eb, ea = expf(np.float32(lb - 1.0)), expf(np.float32(la - 1.0))
+            if ea == np.nextafter(eb, np.float32(1.0)):
+                yield lb, la, eb, ea
+            j += 1
+
+    slots = {"quot_nontie": (top[5], top[6], 0.235), "quot_tie": (top[7], top[8], 0.21),
+             "boundary_tie": (top[9], top[10], 0.15)}
+    for name, (a, b, _) in slots.items():
+        pairs[name] = lid(a, b)
+    gens = {name: one_ulp_pairs(start) for name, (_, _, start) in slots.items()}
+    cur = {name: next(g) for name, g in gens.items()}
+    for _ in range(400):
+        for name, (lb, la, _, _) in cur.items():
+            lo, hi = pairs[name]
+            logits[lo], logits[hi] = lb, la
+        s = _softmax_sum(logits, expf)
+        want = {"quot_nontie": False, "quot_tie": True, "boundary_tie": True}
+        ok = True
+        for name, (lb, la, eb, ea) in cur.items():
+            if (np.float32(ea / s) == np.float32(eb / s)) != want[name]:
+                cur[name] = next(gens[name])
+                ok = False
+        if ok:
+            break
+    else:
+        raise AssertionError("no quotient ties found")
+    x = np.zeros(D, np.float32)
+    x[0], x[1], x[2] = 1.0, 2.0 ** -8, 2.0 ** -16
+    bits = bf16_bits(rng.normal(0, 0.02, (E, D)).astype(np.float32))
+    for e in range(E):
+        bits[e, 0], bits[e, 1], bits[e, 2] = _exact_logit_row(logits[e])
+    return bits, bf16_to_f32(bits), x, pairs, logits
+
+
+def test_probability_ties_decided_as_the_reference_does(ctx):
+    # Every kind of tie above, with the lower logit on the lower id, through
+    # every path: one token (selection inside gate/up), 16 tokens (the select
+    # kernel), grouped at 16 (per-token router) and 24 (router GEMM). Ids are
+    # the oracle's bit for bit; the three one-ulp pairs (higher id first by
+    # exp) send every selection to the recompute over every expert.
+    rng = np.random.default_rng(11)
+    bits, router_f, x, pairs, logits = tie_router(rng)
+    ora = O.route_qwen_top_k(x, router_f, D, E, K, True)
+    g = osm_hip.geometry(D, I, G, osm_hip.BF16)
+    blob = random_blob(rng, D, I, G, O.META_BF16)[0]
+    slab = osm_hip.ExpertSlab(ctx, g, 1, E)
+    for e in range(E):
+        slab.upload(0, e, blob)
+    moe = osm_hip.MoeLayer(ctx, g, E, K, bits, osm_hip.BF16, max_tokens=24)
+    for path, T in [(osm_hip.PATH_PER_TOKEN, 1), (osm_hip.PATH_PER_TOKEN, 16), (osm_hip.PATH_GROUPED, 16),
+                    (osm_hip.PATH_GROUPED, 24)]:
+        moe.routing_stats(reset=True)
+        moe.set_path(path)
+        gpu = moe.run_slab(slab, 0, np.tile(x, (T, 1)))
+        for t in range(T):
+            assert np.array_equal(gpu["ids"][t], ora["ids"]), (path, T, t, list(gpu["ids"][t]), list(ora["ids"]))
+            assert_weights(gpu["weights"][t], gpu["logits"][t], gpu["ids"][t], ora["weights"], ora["logits"])
+        st = moe.routing_stats()
+        assert st["selections"] == T and st["exact"] == T and st["exact_all"] == T, (path, T, st)
+        assert st["near_ties"] == 3 * T, (path, T, st)
+
+
+def test_device_exp_keys_equal_host_libm(ctx):
+    # The selection's exp (osm_libm_expf as compiled for gfx950) over every
+    # float <= 0, against std::exp(float) of this host: checksums of 2^16
+    # results at a time (sum of bits * (2 i + 1): any single wrong result
+    # changes its block's sum).
+    first, count, block = 0x80000000, 0x7F800001, 1 << 16
+    dev = osm_hip.libm_expf_checksums(ctx, first, count, block)
+    host = O.libm_expf_checksums(first, count, block)
+    bad = np.nonzero(dev != host)[0]
+    assert bad.size == 0, [hex(first + int(b) * block) for b in bad[:8]]

@@ -13,7 +13,13 @@ QwenCheckpointMoeSublayer::run, src/model/checkpoint_moe_sublayer.cpp:138-199).
     the 43.5 GB: decode steps until the cache has evicted for 16 steps,
     bit-identical to the resident stack, with
     the cache counters equal to the restated LFU+recency policy replayed over
-    the resident stack's routing.
+    the resident stack's routing;
+(c) the same capped cache driven by a correlated routing trace (each of a
+    layer's 10 picks repeats one of its previous-step picks with p = 0.6,
+    the benchmark's workload) through the pipelined stack: bit-identical to
+    the layer-by-layer calls on a second cache until both have evicted for
+    16 steps, counters equal to the restated policy, and two tokens within
+    1e-3 of the oracle's chain of given-picks sublayers.
 """
 
 import numpy as np
@@ -21,7 +27,7 @@ import pytest
 
 import oracle as O
 import osm_hip
-from helpers import pmap, rel_l2
+from helpers import correlated_trace, pmap, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -138,4 +144,55 @@ def test_capped_cache_stack_matches_resident(ctx, stack):
         assert st[key] == po[key], (key, st, po)
     assert st["evictions"] > 0 and st["resident_bytes"] <= CACHE_BYTES, st
     cache.close()
+    store.close()
+
+
+def test_capped_cache_given_trace_matches_layer_calls(ctx, stack):
+    store = osm_hip.ExpertStore(stack.g, LAYERS, E)
+    store.synthesize(ctx, SEED)
+    a = osm_hip.ExpertCache(ctx, CACHE_BYTES, store=store)
+    b = osm_hip.ExpertCache(ctx, CACHE_BYTES, store=store)
+    policy = O.DeviceCachePolicy(CACHE_BYTES)
+    stride = store.stride
+    rng = np.random.default_rng(SEED + 7)
+    steps = 120
+    trace = correlated_trace(rng, LAYERS, steps, K, E, 0.6)
+    w = np.arange(K, 0, -1, dtype=np.float32)
+    w = np.broadcast_to((w / w.sum()).astype(np.float32).reshape(1, 1, K), (LAYERS, 1, K)).copy()
+    xs = O.synth_tokens(SEED, 900000, steps, D)
+    evicting, first_evicting, s = 0, None, 0
+    checked = []
+    while evicting < 16:
+        assert s < steps, a.stats()
+        ids = np.stack(trace[s])
+        got = osm_hip.run_cached_layers(ctx, stack.layers, list(range(LAYERS)), a, xs[s], (ids, w))
+        ref = xs[s]
+        for l in range(LAYERS):
+            ref = stack.layers[l].run_cached(b, l, ref, sublayer=True, picks=(ids[l], w[l]))["out"]
+            for e in ids[l][0]:
+                policy.get(l, int(e), stride)
+        assert np.array_equal(got.reshape(D), np.asarray(ref).reshape(D)), s
+        if a.stats()["evictions"] > 0:
+            evicting += 1
+            if first_evicting is None:
+                first_evicting = s
+        if s == 0 or evicting == 1:
+            checked.append((s, got.reshape(D).copy()))
+        s += 1
+    st, sb, po = a.stats(), b.stats(), policy.stats()
+    for key in ("hits", "misses", "loads", "evictions", "resident_entries"):
+        assert st[key] == sb[key] == po[key], (key, st, sb, po)
+    assert st["evictions"] > 0 and st["resident_bytes"] <= CACHE_BYTES, st
+    # Two tokens (the first, and the first step that evicted) against the
+    # oracle's chain of given-picks sublayers.
+    for s, y in checked[:2]:
+        ids = np.stack(trace[s])
+        x = xs[s].copy()
+        for l in range(LAYERS):
+            picked = pmap(lambda e: O.synth_expert_blob(SEED, l, int(e), D, I, G), list(ids[l][0]))
+            x = O.moe_sublayer_picks(x, stack.norm[l], 1e-6, w[l][0], picked, stack.shared[l],
+                                     O.bf16_bits_to_f32(stack.sg[l]), D, I, G, O.META_BF16)
+        assert rel_l2(y, x) <= 1e-3, s
+    a.close()
+    b.close()
     store.close()

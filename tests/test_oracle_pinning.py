@@ -350,6 +350,28 @@ def test_sublayer_is_norm_moe_residual():
     assert np.array_equal(sub["ids"], moe["ids"])
 
 
+def test_sublayer_with_given_picks_is_the_routed_sublayer():
+    # The given-picks sublayer fed the router's own picks is the routed
+    # sublayer bit for bit (routed_moe.cpp:31-62 accumulates the picks in
+    # order, as the routed path does), for several tokens; with the picks
+    # reversed it still matches to rounding (a reordered sum), so the weights
+    # and blobs are paired by pick, not by position in the expert table.
+    seed, h, inter, E, k = 19, 256, 64, 16, 4
+    blobs = [O.synth_expert_blob(seed, 0, e, h, inter) for e in range(E)]
+    shared = O.synth_expert_blob(seed, 0, O.SHARED_EXPERT_ID, h, inter)
+    router = O.bf16_bits_to_f32(O.synth_router_bf16(seed, 0, E, h))
+    sg = O.bf16_bits_to_f32(O.synth_shared_gate_bf16(seed, 0, h))
+    nw = O.synth_norm_weight(seed, 0, h)
+    for t, x in enumerate(O.synth_tokens(seed, 0, 4, h)):
+        sub = O.moe_sublayer(x, nw, 1e-6, router, blobs, shared, sg, h, inter, 64, O.META_BF16, k)
+        picked = [blobs[int(e)] for e in sub["ids"]]
+        got = O.moe_sublayer_picks(x, nw, 1e-6, sub["weights"], picked, shared, sg, h, inter, 64, O.META_BF16)
+        assert np.array_equal(got, sub["out"]), t
+        rev = O.moe_sublayer_picks(x, nw, 1e-6, sub["weights"][::-1].copy(), picked[::-1], shared, sg, h, inter, 64,
+                                   O.META_BF16)
+        assert np.max(np.abs(rev - sub["out"])) <= 1e-5 * np.max(np.abs(sub["out"])), t
+
+
 # ---- single_expert_pilot.cpp: quantize_affine_q4_rows (a16) ------------------------------
 # The reference's source needs nlohmann/json, so it is not in oracle/_ref; the
 # restatement is pinned by the reference's own test and by properties that fix
