@@ -98,16 +98,30 @@ def routing_counts(moes, reset=False):
     return tot
 
 
-def time_steps(ctx, n, fn):
-    start, stop = ctx.event(), ctx.event()
+def time_steps(ctx, n, fn, per_step=None):
+    """Device time of n steps (ms). per_step: a list that gets each step's
+    time (an event after every step; the events ride the same stream)."""
+    evs = [ctx.event() for _ in range(n + 1)] if per_step is not None else [ctx.event(), ctx.event()]
     ctx.synchronize()
-    start.record()
+    evs[0].record()
     for i in range(n):
         fn(i)
-    stop.record()
-    ms = start.elapsed_ms(stop)
+        if per_step is not None:
+            evs[i + 1].record()
+    if per_step is None:
+        evs[1].record()
+    ms = evs[0].elapsed_ms(evs[-1])
+    if per_step is not None:
+        per_step.extend(evs[i].elapsed_ms(evs[i + 1]) for i in range(n))
     ctx.synchronize()
     return ms
+
+
+def spread(per_step_ms, scale):
+    """Median, p10 and p90 of per-step times, each times `scale`."""
+    a = np.asarray(per_step_ms, np.float64) * scale
+    return {"p50": round(float(np.median(a)), 3), "p10": round(float(np.percentile(a, 10)), 3),
+            "p90": round(float(np.percentile(a, 90)), 3)}
 
 
 def traffic_from_profiles(kernel):
@@ -188,7 +202,7 @@ def decode_batches(ctx, moes, slab, args):
     shared) x expert bytes + router + shared-gate vector + activations."""
     L = len(moes)
     out = {}
-    steps = max(3, args.steps // 20)
+    steps = max(10, args.steps // 10)
     for B in (4, 16, 64):
         n_tok = (steps + 1) * L * B
         xs = ctx.alloc(n_tok * D * 4)
@@ -224,7 +238,7 @@ def prefill(ctx, moes, slab, args, layers=8):
     """Config 4: a 512-token bf16 prefill chunk through `layers` layer copies
     (grouped GEMMs on the matrix cores), one fresh chunk per step."""
     T = PREFILL_TOKENS
-    steps = max(3, args.steps // 20)
+    steps = max(10, args.steps // 10)
     xs = []
     for l in range(layers):
         xf = osm_hip.synth_tokens(ctx, args.seed, 400000 + l * T, T, D)
@@ -257,7 +271,7 @@ def prefill(ctx, moes, slab, args, layers=8):
 def grouped_decode(ctx, moes, slab, args, T, layers=8):
     """T fp32 tokens per layer step through the grouped MFMA path (config 2's
     largest batch), one fresh batch per layer copy."""
-    steps = max(3, args.steps // 20)
+    steps = max(10, args.steps // 10)
     xs = [ctx.alloc(T * D * 4) for _ in range(layers)]
     for l in range(layers):
         osm_hip.synth_tokens_device(ctx, args.seed, 600000 + l * T, T, D, xs[l].ptr)
@@ -459,7 +473,8 @@ def main():
     for i in range(warm):
         step_graph(i)
     routing_counts(moes, reset=True)
-    ms = time_steps(ctx, steps, lambda i: step_graph(warm + i))
+    per_step = []
+    ms = time_steps(ctx, steps, lambda i: step_graph(warm + i), per_step)
     route_indep = routing_counts(moes)
     ms_per_step = ms / steps
     us_per_token_layer = ms_per_step * 1000.0 / L
@@ -489,7 +504,8 @@ def main():
     for i in range(warm):
         step_chained(i)
     routing_counts(moes, reset=True)
-    us_chained = time_steps(ctx, steps, lambda i: step_chained(warm + i)) / steps * 1000.0 / L
+    per_step_c = []
+    us_chained = time_steps(ctx, steps, lambda i: step_chained(warm + i), per_step_c) / steps * 1000.0 / L
     route_chained = routing_counts(moes)
     log(f"[bench] routing counters, independent / chained: {route_indep} / {route_chained}")
     log(f"[bench] chained sublayers, graph: {us_chained:.2f} us/token-layer")
@@ -498,26 +514,27 @@ def main():
     # replayed; each layer's workspace holds the routing of its last decode.
     step_eager(0)
     ctx.synchronize()
-    phase_names = {0: "route_kernel", 1: "gate_up_kernel", 2: "down_kernel"}
+    gate_up_bytes = (K + 1) * (2 * (I * D // 2) + 4 * (I * D // G) * 2)
+    down_bytes = (K + 1) * ((D * I // 2) + 2 * (D * I // G) * 2)
     phase_bytes = {
-        0: ROUTER_BYTES + SHARED_GATE_BYTES + tok_bytes + E * 4,
-        1: (K + 1) * (2 * (I * D // 2) + 4 * (I * D // G) * 2) + tok_bytes + (K + 1) * I * 4 + E * 4,
-        2: (K + 1) * ((D * I // 2) + 2 * (D * I // G) * 2) + (K + 1) * I * 4 + tok_bytes,
+        "route_kernel": ROUTER_BYTES + SHARED_GATE_BYTES + tok_bytes + E * 4,
+        "gate_up_kernel": gate_up_bytes + tok_bytes + (K + 1) * I * 4 + E * 4,
+        "down_kernel": down_bytes + (K + 1) * I * 4 + tok_bytes,
     }
-    kernels = {}
-    for ph in (0, 1, 2):
+
+    def graph_us(phases):
         with ctx.capture() as cap:
             for l in range(L):
-                moes[l].launch_phase(slab, l, xs.ptr.value + l * tok_bytes, ys.ptr.value + l * tok_bytes, 1, False, ph)
+                for ph in phases:
+                    moes[l].launch_phase(slab, l, xs.ptr.value + l * tok_bytes, ys.ptr.value + l * tok_bytes, 1,
+                                         False, ph)
         rounds = args.phase_rounds
         cap.graph.launch()
-        ms_p = time_steps(ctx, rounds, lambda _i: cap.graph.launch())
-        avg_us = ms_p / (rounds * L) * 1000.0
-        kernels[phase_names[ph]] = {
-            "avg_us": round(avg_us, 3),
-            "bytes_per_launch": phase_bytes[ph],
-            "GBps": round(phase_bytes[ph] / (avg_us * 1e-6) / 1e9, 1),
-        }
+        return time_steps(ctx, rounds, lambda _i: cap.graph.launch()) / (rounds * L) * 1000.0
+
+    avg = {"route_kernel": graph_us((0,)), "gate_up_kernel": graph_us((1,)), "down_kernel": graph_us((2,))}
+    kernels = {name: {"avg_us": round(us, 3), "bytes_per_launch": phase_bytes[name],
+                      "GBps": round(phase_bytes[name] / (us * 1e-6) / 1e9, 1)} for name, us in avg.items()}
     dominant = max(kernels, key=lambda k: kernels[k]["avg_us"])
     dk = kernels[dominant]
     log(f"[bench] kernels: {json.dumps(kernels)}")
@@ -559,7 +576,9 @@ def main():
         "hbm_GBps": round(hbm_gbps, 1),
         "hbm_frac": round(hbm_gbps / HBM_PEAK_GBPS, 4),
         "bytes_per_token_layer": bytes_per_token_layer,
+        "us_per_token_layer_spread": spread(per_step, 1000.0 / L),
         "chained_sublayer_us_per_token_layer": round(us_chained, 3),
+        "chained_us_per_token_layer_spread": spread(per_step_c, 1000.0 / L),
         "stream_launch_us_per_token_layer": round(us_eager, 3),
         "routing_exact_path": {
             "what": "selections whose order the per-logit bounds did not prove, recomputed in the reference's order",
