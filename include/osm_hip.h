@@ -75,7 +75,17 @@ const char* osm_last_error(void);
 int osm_device_count(int* count);
 
 /* ---- context: VulkanComputeContext (include/orbi/streammoe/backend/vulkan_compute_context.hpp:19-49) */
+/* A context with a compute stream of its own. */
 int osm_context_create(int device, osm_context* out);
+/* A context whose operators are all ordered on the caller's stream
+ * (a hipStream_t of `device`; OSM_E_DEVICE if it belongs to another device,
+ * OSM_E_INVALID if NULL). The caller keeps the stream alive until the
+ * context is destroyed; destroying the context leaves it alone. The
+ * reference's context owns its one queue (vulkan_compute_context.hpp:19-49);
+ * here the caller may share a stream with its own kernels, so that their
+ * order needs no events. Fills of the capped expert cache still run on side
+ * streams the library owns, joined to this stream by events. */
+int osm_context_create_on_stream(int device, void* hip_stream, osm_context* out);
 void osm_context_destroy(osm_context ctx);
 int osm_context_synchronize(osm_context ctx);
 /* Device name, NUL-terminated into buf. */
@@ -92,8 +102,21 @@ int osm_event_elapsed_ms(osm_event start, osm_event stop, float* ms);
 /* Raw device memory for callers that pass device pointers. */
 int osm_device_alloc(osm_context ctx, size_t bytes, void** out);
 int osm_device_free(osm_context ctx, void* ptr);
+/* Synchronous: they return once the copy is done. */
 int osm_memcpy_h2d(osm_context ctx, void* dst, const void* src, size_t bytes);
 int osm_memcpy_d2h(osm_context ctx, void* dst, const void* src, size_t bytes);
+/* Enqueued on the context's stream, returning before the copy runs: the host
+ * memory must stay valid (and, for an upload, unchanged) until the stream has
+ * passed the copy (osm_context_synchronize, an event, or the caller's own
+ * wait on its stream). Host memory from osm_host_alloc is pinned, so the copy
+ * is a DMA that overlaps the host; pageable memory is staged by the HIP
+ * runtime. No reference counterpart: the reference's staging copies block on
+ * a fence (vulkan_float_buffer.hpp:23-58). */
+int osm_memcpy_h2d_async(osm_context ctx, void* dst, const void* src, size_t bytes);
+int osm_memcpy_d2h_async(osm_context ctx, void* dst, const void* src, size_t bytes);
+/* Pinned (page-locked) host memory for asynchronous copies. */
+int osm_host_alloc(osm_context ctx, size_t bytes, void** out);
+int osm_host_free(osm_context ctx, void* ptr);
 /* Device-to-device copy enqueued on the context's compute stream; returns
  * before it runs (no synchronisation), so it may be captured into a graph or
  * refresh a graph's input between launches. 16-byte aligned copies run as a
@@ -105,8 +128,13 @@ int osm_buffer_create(osm_context ctx, size_t element_count, osm_buffer* out);
 void osm_buffer_destroy(osm_buffer b);
 size_t osm_buffer_size(osm_buffer b);
 float* osm_buffer_device_ptr(osm_buffer b);
+/* Synchronous, as the reference's upload/download. */
 int osm_buffer_upload(osm_buffer b, const float* values, size_t count);
 int osm_buffer_download(osm_buffer b, float* values, size_t count);
+/* The same copies enqueued on the context's stream without waiting (the
+ * rules of osm_memcpy_h2d_async); count must equal the buffer's size. */
+int osm_buffer_upload_async(osm_buffer b, const float* values, size_t count);
+int osm_buffer_download_async(osm_buffer b, float* values, size_t count);
 
 /* ---- single operators over host arrays -------------------------------------
  * run_vulkan_q4_dequant (vulkan_q4_dequant.hpp:23-30): out has rows*packed_cols*8 floats. */
@@ -274,7 +302,9 @@ int osm_moe_layer_decode_device(osm_context ctx, osm_moe_layer l, osm_expert_sla
  * [1, osm_moe_layer_static_tokens_capacity(l)] (119 at the Qwen3-Next
  * shape), else OSM_E_INVALID. Every call on one GPU shares that array, and
  * the routing it leaves there is overwritten by the next call: calls that
- * overlap in time on one GPU (several streams or contexts) race. */
+ * overlap in time on one GPU (several streams or contexts) race. That
+ * routing cannot be queried: osm_moe_layer_routing returns OSM_E_INVALID
+ * until the layer's next other call. */
 int osm_moe_layer_decode_device_static(osm_context ctx, osm_moe_layer l, osm_expert_slab slab,
                                        uint32_t slab_layer, const float* x_dev, float* y_dev,
                                        uint32_t tokens, int sublayer);
@@ -302,7 +332,10 @@ int osm_moe_layer_prefill_device(osm_context ctx, osm_moe_layer l, osm_expert_sl
  * return only y. ids, weights, mass, shared_gate, logits and normalized (the
  * RMSNorm output of a sublayer decode, the input of a per-token MoE decode)
  * are filled where non-NULL; out is ignored. Synchronises the context's
- * stream. tokens must be in [1, max_tokens]. */
+ * stream. tokens must be in [1, max_tokens]. After
+ * osm_moe_layer_decode_device_static, whose routing lives in the shared
+ * fixed workspace, it returns OSM_E_INVALID until the layer's next other
+ * call. */
 int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens,
                           const osm_moe_outputs* outputs);
 /* Routing exactness counters of the layer since its creation or the last

@@ -445,13 +445,19 @@ uint64_t stream_of(uint64_t seed, uint32_t a, uint32_t b, uint32_t t) {
   return mix64(mix64(mix64(seed) ^ a) ^ ((static_cast<uint64_t>(b) << 8) | t));
 }
 
-// Irwin-Hall(4) over 16-bit uniforms, centred and scaled to unit variance:
-// the integer sum is exact, then one fp32 multiply by 1/sqrt((2^32-1)/3).
+uint32_t fields16(uint64_t hsh) {
+  return static_cast<uint32_t>((hsh & 0xFFFFU) + ((hsh >> 16) & 0xFFFFU) +
+                               ((hsh >> 32) & 0xFFFFU) + (hsh >> 48));
+}
+
+// Irwin-Hall(12) over 16-bit uniforms taken from three chained hashes,
+// centred and scaled to unit variance: the integer sum is exact (standard
+// deviation sqrt(2^32-1), i.e. 2^16 to 6e-11), then one exact multiply by
+// 2^-16. Support is [-6, 6].
 float normal_at(uint64_t stream, uint64_t i) {
-  const uint64_t hsh = mix64(stream + i);
-  const int32_t s = static_cast<int32_t>((hsh & 0xFFFFU) + ((hsh >> 16) & 0xFFFFU) +
-                                         ((hsh >> 32) & 0xFFFFU) + (hsh >> 48));
-  return static_cast<float>(s - 131070) * 0x1.bb67aep-16F;
+  const uint64_t h0 = mix64(stream + i), h1 = mix64(h0), h2 = mix64(h1);
+  const int32_t s = static_cast<int32_t>(fields16(h0) + fields16(h1) + fields16(h2));
+  return static_cast<float>(s - 393210) * 0x1p-16F;
 }
 
 uint16_t bf16_rne(float f) {

@@ -160,6 +160,18 @@ int osm_context_create(int device, osm_context* out) {
   return ok();
   OSM_GUARD_END
 }
+int osm_context_create_on_stream(int device, void* stream, osm_context* out) {
+  OSM_GUARD_BEGIN
+  if (!out) return fail(OSM_E_INVALID, "out is null");
+  *out = nullptr;
+  if (!stream) return fail(OSM_E_INVALID, "stream is null (osm_context_create makes a context with its own stream)");
+  std::string d;
+  auto c = osm::HipComputeContext::create(device, &d, stream);
+  if (!c) return fail(OSM_E_DEVICE, d);
+  *out = new osm_context_s{std::move(*c)};
+  return ok();
+  OSM_GUARD_END
+}
 void osm_context_destroy(osm_context ctx) { delete ctx; }
 int osm_context_synchronize(osm_context ctx) {
   if (!ctx) return fail(OSM_E_INVALID, "context is null");
@@ -236,6 +248,36 @@ int osm_memcpy_d2h(osm_context ctx, void* dst, const void* src, size_t bytes) {
   return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipMemcpy D2H", rc));
 }
 
+int osm_memcpy_h2d_async(osm_context ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(OSM_E_INVALID, "invalid arguments");
+  std::string d;
+  if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
+  const int rc = osmd_memcpy_h2d(dst, src, bytes, ctx->ctx.stream());
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipMemcpyAsync H2D", rc));
+}
+int osm_memcpy_d2h_async(osm_context ctx, void* dst, const void* src, size_t bytes) {
+  if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(OSM_E_INVALID, "invalid arguments");
+  std::string d;
+  if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
+  const int rc = osmd_memcpy_d2h(dst, src, bytes, ctx->ctx.stream());
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipMemcpyAsync D2H", rc));
+}
+int osm_host_alloc(osm_context ctx, size_t bytes, void** out) {
+  if (!ctx || !out || bytes == 0) return fail(OSM_E_INVALID, "invalid arguments");
+  *out = nullptr;
+  std::string d;
+  if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
+  const int rc = osmd_host_malloc(out, bytes);
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipHostMalloc", rc));
+}
+int osm_host_free(osm_context ctx, void* ptr) {
+  if (!ctx) return fail(OSM_E_INVALID, "context is null");
+  std::string d;
+  if (!ctx->ctx.activate(&d)) return fail(OSM_E_DEVICE, d);
+  const int rc = osmd_host_free(ptr);
+  return rc == 0 ? ok() : fail(OSM_E_DEVICE, osm::hip_error("hipHostFree", rc));
+}
+
 int osm_memcpy_d2d_async(osm_context ctx, void* dst, const void* src, size_t bytes) {
   if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(OSM_E_INVALID, "invalid arguments");
   std::string d;
@@ -262,6 +304,16 @@ int osm_buffer_upload(osm_buffer b, const float* values, size_t count) {
   if (!b || (!values && count)) return fail(OSM_E_INVALID, "invalid arguments");
   std::string d;
   return b->buf.upload(std::span<const float>(values, count), &d) ? ok() : fail(OSM_E_INVALID, d);
+}
+int osm_buffer_upload_async(osm_buffer b, const float* values, size_t count) {
+  if (!b || !values) return fail(OSM_E_INVALID, "invalid arguments");
+  std::string d;
+  return b->buf.upload_async(values, count, &d) ? ok() : fail(OSM_E_INVALID, d);
+}
+int osm_buffer_download_async(osm_buffer b, float* values, size_t count) {
+  if (!b || !values) return fail(OSM_E_INVALID, "invalid arguments");
+  std::string d;
+  return b->buf.download_async(values, count, &d) ? ok() : fail(OSM_E_INVALID, d);
 }
 int osm_buffer_download(osm_buffer b, float* values, size_t count) {
   if (!b || !values) return fail(OSM_E_INVALID, "invalid arguments");
@@ -786,6 +838,9 @@ int osm_moe_layer_routing(osm_context ctx, osm_moe_layer l, uint32_t tokens, con
   if (!ctx || !l || !outputs) return fail(OSM_E_INVALID, "null argument");
   if (tokens == 0 || tokens > l->layer.max_tokens())
     return fail(OSM_E_INVALID, "routing download: token count must be in [1, max_tokens]");
+  if (!l->layer.routing_queryable())
+    return fail(OSM_E_INVALID,
+                "routing download: the layer's last decode ran without allocation (its routing is not kept)");
   if (!ctx->ctx.activate(nullptr)) return fail(OSM_E_DEVICE, "HIP compute context cannot be made current");
   osm::HipMoeResult r;
   std::string d;

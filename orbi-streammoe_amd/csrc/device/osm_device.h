@@ -46,6 +46,8 @@ int osmd_zero(void* dst, size_t bytes, osmd_stream s);
 int osmd_stream_create(osmd_stream* s);
 int osmd_stream_destroy(osmd_stream s);
 int osmd_stream_synchronize(osmd_stream s);
+/* The device a stream was created on. */
+int osmd_stream_device(osmd_stream s, int* device);
 int osmd_event_create(osmd_event* e);
 int osmd_event_destroy(osmd_event e);
 int osmd_event_record(osmd_event e, osmd_stream s);

@@ -139,6 +139,12 @@ int osmd_stream_create(osmd_stream* s) {
   *s = h;
   return r;
 }
+int osmd_stream_device(osmd_stream s, int* device) {
+  hipDevice_t d = -1;
+  const int r = rc(hipStreamGetDevice(static_cast<hipStream_t>(s), &d));
+  *device = static_cast<int>(d);
+  return r;
+}
 int osmd_stream_destroy(osmd_stream s) {
   return s ? rc(hipStreamDestroy(static_cast<hipStream_t>(s))) : 0;
 }

@@ -3,8 +3,8 @@
 // A 48-layer expert stack is ~43.5 GB, too large to build on the host, so the
 // benchmark and the full-size tests generate it on the device. Every element
 // is a pure function of (seed, a, b, tensor, index): a SplitMix64-style
-// finaliser over a counter, an Irwin-Hall(4) normal from four 16-bit draws
-// scaled to unit variance, and round-to-nearest-even to bf16. Only exact
+// finaliser over a counter, an Irwin-Hall(12) normal from twelve 16-bit
+// draws scaled to unit variance (support +-6 sigma), and round-to-nearest-even to bf16. Only exact
 // integer steps and separately rounded IEEE multiplies and adds are used
 // (contraction is off for this file), so the same element computed on the
 // host is bit-identical.
@@ -44,11 +44,20 @@ __host__ __device__ __forceinline__ uint64_t stream_of(uint64_t seed, uint32_t a
   return mix64(mix64(mix64(seed) ^ a) ^ ((static_cast<uint64_t>(b) << 8) | t));
 }
 
+// Sum of the four 16-bit fields of a 64-bit hash.
+__device__ __forceinline__ uint32_t fields16(uint64_t h) {
+  return static_cast<uint32_t>((h & 0xFFFFu) + ((h >> 16) & 0xFFFFu) + ((h >> 32) & 0xFFFFu) +
+                               (h >> 48));
+}
+
+// Irwin-Hall(12): twelve 16-bit uniforms from three chained hashes. The sum
+// has mean 393210 and standard deviation sqrt(2^32 - 1), which is 2^16 to
+// within 6e-11, so one exact multiply by 2^-16 gives unit variance with
+// support [-6, 6].
 __device__ __forceinline__ float normal_at(uint64_t stream, uint64_t i) {
-  const uint64_t h = mix64(stream + i);
-  const int32_t s = static_cast<int32_t>((h & 0xFFFFu) + ((h >> 16) & 0xFFFFu) +
-                                         ((h >> 32) & 0xFFFFu) + (h >> 48));
-  return static_cast<float>(s - 131070) * 0x1.bb67aep-16f;
+  const uint64_t h0 = mix64(stream + i), h1 = mix64(h0), h2 = mix64(h1);
+  const int32_t s = static_cast<int32_t>(fields16(h0) + fields16(h1) + fields16(h2));
+  return static_cast<float>(s - 393210) * 0x1p-16f;
 }
 
 __device__ __forceinline__ uint16_t bf16_rne(float f) {

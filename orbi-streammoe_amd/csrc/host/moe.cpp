@@ -228,8 +228,13 @@ struct HipMoeLayer::Impl {
 
   std::uint32_t nslot() const { return cfg.top_k + (cfg.has_shared_expert ? 1U : 0U); }
 
+  // Whether the last decode wrote its routing into the fixed workspace of
+  // the allocation-free entry rather than into this layer's buffers. Every
+  // other launch builds its arguments here, which clears it.
+  mutable bool routing_in_static = false;
   osmd_moe_args args(const float* x, float* y, std::uint32_t tokens,
                      const std::uint8_t* const* table, bool sublayer) const {
+    routing_in_static = false;
     osmd_moe_args a{};
     a.geom = cfg.geometry;
     a.expert_count = cfg.expert_count;
@@ -563,6 +568,7 @@ int HipMoeLayer::decode_device_static(HipComputeContext& context, const float* x
   // selection the picks and slot pointers, gate/up every slot's h. The
   // routing counters are the layer's own.
   if (osmd_moe_decode(&a, context.stream()) != 0) return say("MoE decode launch failed"), OSM_E_DEVICE;
+  impl_->routing_in_static = true;
   say("");
   return OSM_OK;
 }
@@ -645,11 +651,17 @@ HipDispatchResult HipMoeLayer::launch_phase(HipComputeContext& context, const fl
   return r;
 }
 
+bool HipMoeLayer::routing_queryable() const noexcept { return impl_ && !impl_->routing_in_static; }
+
 bool HipMoeLayer::download_routing(HipComputeContext& context, std::uint32_t tokens, HipMoeRouting& out,
                                    std::string* diagnostic) const noexcept {
   try {
     if (!valid() || tokens == 0 || tokens > impl_->max_tokens)
       return set_diag(diagnostic, "routing download: invalid layer or token count"), false;
+    if (!routing_queryable())
+      return set_diag(diagnostic, "routing download: the last decode ran without allocation, so its routing "
+                                  "lives in the shared fixed workspace and cannot be queried"),
+             false;
     const std::size_t K = impl_->cfg.top_k, E = impl_->cfg.expert_count;
     out.ids.resize(tokens * K);
     out.weights.resize(tokens * K);

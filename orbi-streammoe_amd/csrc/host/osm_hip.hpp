@@ -93,8 +93,11 @@ class HipComputeContext {
   HipComputeContext(HipComputeContext&&) noexcept;
   HipComputeContext& operator=(HipComputeContext&&) noexcept;
 
+  // stream: nullptr for a stream the context creates and owns, else a
+  // caller's stream on `device`, which every operator of the context is then
+  // ordered on and which the caller keeps alive until the context is gone.
   [[nodiscard]] static std::optional<HipComputeContext> create(
-      int device = 0, std::string* diagnostic = nullptr) noexcept;
+      int device = 0, std::string* diagnostic = nullptr, osmd_stream stream = nullptr) noexcept;
 
   [[nodiscard]] bool valid() const noexcept;
   [[nodiscard]] int device() const noexcept;
@@ -142,6 +145,14 @@ class HipFloatBuffer {
                             std::string* diagnostic = nullptr) noexcept;
   [[nodiscard]] std::optional<std::vector<float>> download(
       std::string* diagnostic = nullptr) const noexcept;
+  // Enqueued on the context's compute stream, returning before the copy
+  // runs: `values` must stay valid (and unchanged, for an upload) until the
+  // stream has passed it. Pinned host memory makes the copy a DMA that
+  // overlaps the host; pageable memory is staged by the runtime.
+  [[nodiscard]] bool upload_async(const float* values, std::size_t count,
+                                  std::string* diagnostic = nullptr) noexcept;
+  [[nodiscard]] bool download_async(float* values, std::size_t count,
+                                    std::string* diagnostic = nullptr) const noexcept;
 
  private:
   struct Impl;
@@ -845,6 +856,9 @@ class HipMoeLayer {
   [[nodiscard]] bool download_routing(HipComputeContext& context, std::uint32_t tokens,
                                       HipMoeRouting& out,
                                       std::string* diagnostic = nullptr) const noexcept;
+  // False after decode_device_static (its routing sits in the shared fixed
+  // workspace, which later calls overwrite), true after any other decode.
+  [[nodiscard]] bool routing_queryable() const noexcept;
   // The routing counters of every selection since creation or the last
   // reset: selections, selections that took the exact path, exact paths that
   // recomputed every expert, and unresolved adjacent picks. Synchronises the

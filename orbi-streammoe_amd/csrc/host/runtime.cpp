@@ -74,6 +74,7 @@ struct HipComputeContext::Impl {
   std::string name;
   osmd_stream stream = nullptr;
   osmd_stream copy = nullptr;
+  bool owns_stream = true;  // false: a caller's stream, left alive
   DeviceBytes workspace;
   std::vector<DeviceBytes> outgrown;  // kept for graphs captured over them
   ~Impl() {
@@ -81,7 +82,7 @@ struct HipComputeContext::Impl {
     workspace.reset();
     if (device >= 0) osmd_set_device(device);
     if (copy) osmd_stream_destroy(copy);
-    if (stream) osmd_stream_destroy(stream);
+    if (stream && owns_stream) osmd_stream_destroy(stream);
   }
 };
 
@@ -113,8 +114,8 @@ HipComputeContext::~HipComputeContext() = default;
 HipComputeContext::HipComputeContext(HipComputeContext&&) noexcept = default;
 HipComputeContext& HipComputeContext::operator=(HipComputeContext&&) noexcept = default;
 
-std::optional<HipComputeContext> HipComputeContext::create(int device,
-                                                           std::string* diagnostic) noexcept {
+std::optional<HipComputeContext> HipComputeContext::create(int device, std::string* diagnostic,
+                                                           osmd_stream stream) noexcept {
   try {
     int count = 0;
     int rc = osmd_device_count(&count);
@@ -131,11 +132,25 @@ std::optional<HipComputeContext> HipComputeContext::create(int device,
       set_diag(diagnostic, std::string("hipSetDevice failed: ") + osmd_error_string(rc));
       return std::nullopt;
     }
+    if (stream != nullptr) {
+      int on = -1;
+      if ((rc = osmd_stream_device(stream, &on)) != 0) {
+        set_diag(diagnostic, std::string("the caller's stream cannot be queried: ") + osmd_error_string(rc));
+        return std::nullopt;
+      }
+      if (on != device) {
+        set_diag(diagnostic, "the caller's stream belongs to device " + std::to_string(on) + ", not " +
+                                 std::to_string(device));
+        return std::nullopt;
+      }
+    }
     auto impl = std::make_unique<Impl>();
     impl->device = device;
     char name[256] = {0};
     if (osmd_device_name(device, name, sizeof(name)) == 0) impl->name = name;
-    if ((rc = osmd_stream_create(&impl->stream)) != 0 ||
+    impl->owns_stream = stream == nullptr;
+    impl->stream = stream;
+    if ((stream == nullptr && (rc = osmd_stream_create(&impl->stream)) != 0) ||
         (rc = osmd_stream_create(&impl->copy)) != 0) {
       set_diag(diagnostic, std::string("stream creation failed: ") + osmd_error_string(rc));
       return std::nullopt;
@@ -232,6 +247,24 @@ bool HipFloatBuffer::upload(std::span<const float> values, std::string* diagnost
   if (rc == 0) rc = osmd_memcpy_h2d(impl_->mem.get(), values.data(), values.size_bytes(), impl_->stream);
   if (rc == 0) rc = osmd_stream_synchronize(impl_->stream);
   if (rc != 0) return set_diag(diagnostic, std::string("float buffer upload failed: ") + osmd_error_string(rc)), false;
+  return true;
+}
+
+bool HipFloatBuffer::upload_async(const float* values, std::size_t count, std::string* diagnostic) noexcept {
+  if (!valid()) return set_diag(diagnostic, "float buffer is not valid"), false;
+  if (count != impl_->count) return set_diag(diagnostic, "float buffer upload size mismatch"), false;
+  int rc = osmd_set_device(impl_->device);
+  if (rc == 0) rc = osmd_memcpy_h2d(impl_->mem.get(), values, size_bytes(), impl_->stream);
+  if (rc != 0) return set_diag(diagnostic, std::string("float buffer upload failed: ") + osmd_error_string(rc)), false;
+  return true;
+}
+
+bool HipFloatBuffer::download_async(float* values, std::size_t count, std::string* diagnostic) const noexcept {
+  if (!valid()) return set_diag(diagnostic, "float buffer is not valid"), false;
+  if (count != impl_->count) return set_diag(diagnostic, "float buffer download size mismatch"), false;
+  int rc = osmd_set_device(impl_->device);
+  if (rc == 0) rc = osmd_memcpy_d2h(values, impl_->mem.get(), size_bytes(), impl_->stream);
+  if (rc != 0) return set_diag(diagnostic, std::string("float buffer download failed: ") + osmd_error_string(rc)), false;
   return true;
 }
 

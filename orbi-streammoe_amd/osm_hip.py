@@ -77,6 +77,7 @@ _PROTOTYPES = {
     "osm_last_error": (c_char_p, []),
     "osm_device_count": (c_int, [POINTER(c_int)]),
     "osm_context_create": (c_int, [c_int, POINTER(_H)]),
+    "osm_context_create_on_stream": (c_int, [c_int, c_void_p, POINTER(_H)]),
     "osm_context_destroy": (None, [_H]),
     "osm_context_synchronize": (c_int, [_H]),
     "osm_context_device_name": (c_int, [_H, c_char_p, c_size_t]),
@@ -89,12 +90,18 @@ _PROTOTYPES = {
     "osm_device_free": (c_int, [_H, c_void_p]),
     "osm_memcpy_h2d": (c_int, [_H, c_void_p, c_void_p, c_size_t]),
     "osm_memcpy_d2h": (c_int, [_H, c_void_p, c_void_p, c_size_t]),
+    "osm_memcpy_h2d_async": (c_int, [_H, c_void_p, c_void_p, c_size_t]),
+    "osm_memcpy_d2h_async": (c_int, [_H, c_void_p, c_void_p, c_size_t]),
+    "osm_host_alloc": (c_int, [_H, c_size_t, POINTER(c_void_p)]),
+    "osm_host_free": (c_int, [_H, c_void_p]),
     "osm_buffer_create": (c_int, [_H, c_size_t, POINTER(_H)]),
     "osm_buffer_destroy": (None, [_H]),
     "osm_buffer_size": (c_size_t, [_H]),
     "osm_buffer_device_ptr": (c_void_p, [_H]),
     "osm_buffer_upload": (c_int, [_H, c_void_p, c_size_t]),
     "osm_buffer_download": (c_int, [_H, c_void_p, c_size_t]),
+    "osm_buffer_upload_async": (c_int, [_H, c_void_p, c_size_t]),
+    "osm_buffer_download_async": (c_int, [_H, c_void_p, c_size_t]),
     "osm_q4_dequant": (c_int, [_H, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t]),
     "osm_q4_gemv": (c_int, [_H, c_void_p, c_size_t, c_size_t, c_size_t, c_void_p, c_void_p, c_size_t, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t]),
     "osm_swiglu": (c_int, [_H, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
@@ -290,10 +297,16 @@ class Context(_Handle):
 
     _destroy = "osm_context_destroy"
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0, stream=None):
+        """stream: None for a stream of the context's own, else a caller's
+        hipStream_t (an int or c_void_p) on `device` that every operator of
+        the context is then ordered on; the caller keeps it alive."""
         self._children = []
         h = c_void_p()
-        check(load().osm_context_create(device, ctypes.byref(h)))
+        if stream is None:
+            check(load().osm_context_create(device, ctypes.byref(h)))
+        else:
+            check(load().osm_context_create_on_stream(device, c_void_p(int(stream) if not isinstance(stream, c_void_p) else stream.value), ctypes.byref(h)))
         super().__init__(h)
 
     def _adopt(self, child):
@@ -319,6 +332,14 @@ class Context(_Handle):
 
     def alloc(self, nbytes: int) -> "DeviceArray":
         return DeviceArray(self, nbytes)
+
+    def pinned(self, dtype, count) -> "PinnedArray":
+        return PinnedArray(self, dtype, count)
+
+    @property
+    def stream(self) -> int:
+        """The hipStream_t every operator of this context is ordered on."""
+        return load().osm_context_stream(self.h) or 0
 
     def copy_d2d(self, dst_ptr, src_ptr, nbytes: int):
         """Enqueued device-to-device copy on the compute stream (no sync)."""
@@ -371,9 +392,50 @@ class DeviceArray:
         check(load().osm_memcpy_d2h(self.ctx.h, _p(out), self.ptr, out.nbytes))
         return out
 
+    def upload_async(self, src: "PinnedArray", count=None):
+        """Enqueued copy from pinned host memory; src must stay unchanged
+        until the context's stream has passed it."""
+        n = src.array.nbytes if count is None else count * src.array.itemsize
+        assert n <= self.nbytes
+        check(load().osm_memcpy_h2d_async(self.ctx.h, self.ptr, src.ptr, n))
+
+    def download_async(self, dst: "PinnedArray", count=None):
+        """Enqueued copy into pinned host memory, valid after the context's
+        stream has passed it."""
+        n = dst.array.nbytes if count is None else count * dst.array.itemsize
+        assert n <= self.nbytes
+        check(load().osm_memcpy_d2h_async(self.ctx.h, dst.ptr, self.ptr, n))
+
     def close(self):
         if self.ptr is not None and self.ptr.value:
             check(load().osm_device_free(self.ctx.h, self.ptr))
+        self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class PinnedArray:
+    """Page-locked host memory (osm_host_alloc) seen as a numpy array: the
+    source or target of asynchronous copies."""
+
+    def __init__(self, ctx: Context, dtype, count: int):
+        self.ctx = ctx
+        dt = np.dtype(dtype)
+        p = c_void_p()
+        check(load().osm_host_alloc(ctx.h, max(1, count * dt.itemsize), ctypes.byref(p)))
+        self.ptr = p
+        buf = (ctypes.c_char * (count * dt.itemsize)).from_address(p.value)
+        self.array = np.frombuffer(buf, dtype=dt, count=count)
+        ctx._adopt(self)
+
+    def close(self):
+        if self.ptr is not None and self.ptr.value:
+            self.array = None
+            check(load().osm_host_free(self.ctx.h, self.ptr))
         self.ptr = None
 
     def __del__(self):
@@ -403,6 +465,12 @@ class FloatBuffer(_Handle):
         out = np.empty(self.count, np.float32)
         check(load().osm_buffer_download(self.h, _p(out), out.size))
         return out
+
+    def upload_async(self, src: PinnedArray):
+        check(load().osm_buffer_upload_async(self.h, src.ptr, src.array.size))
+
+    def download_async(self, dst: PinnedArray):
+        check(load().osm_buffer_download_async(self.h, dst.ptr, dst.array.size))
 
 
 # ---- single operators ----------------------------------------------------------------

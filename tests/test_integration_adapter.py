@@ -2,13 +2,15 @@
 include/osm_hip.h and links against libosm_hip.so. CPU only: nothing runs on a
 device.
 
-The adapter includes three reference headers. The test writes, under its
-temporary directory, the few public types of them that the adapter touches
-(ExpertId / ExpertReadRequest / ExpertStorage of storage/expert_storage.hpp:
-10-29, RoutedExpert / QwenRouterResult of model/qwen_router.hpp:17-29 and
-QwenSparseMoeResult of model/routed_moe.hpp:21-27), so the check is of the
-adapter's use of this library's C ABI: every call, struct field and handle
-type as INTEGRATION.md writes them."""
+The adapter includes two reference headers, storage/expert_storage.hpp and
+model/routed_moe.hpp. Where the reference checkout is present, the adapter is
+compiled against those headers themselves, so the check covers its use of the
+reference's types (ExpertId / ExpertReadRequest / ExpertStorage of
+expert_storage.hpp:10-29, RoutedExpert / QwenRouterResult of
+qwen_router.hpp:17-29, QwenSparseMoeResult of routed_moe.hpp:21-27) as well
+as every call, struct field and handle type of this library's C ABI. Without
+the checkout (a machine that has only this repository) the test writes
+stand-ins of those few types under its temporary directory instead."""
 
 import os
 import re
@@ -19,6 +21,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_DIR = os.path.join(ROOT, "orbi-streammoe_amd")
+REFERENCE_INCLUDE = "/root/reference/include"
 
 TYPES = {
     "orbi/streammoe/storage/expert_storage.hpp": """#pragma once
@@ -91,14 +94,19 @@ def test_adapter_compiles_and_links(tmp_path):
     lib = os.path.join(LIB_DIR, "libosm_hip.so")
     if not os.path.exists(lib):
         pytest.skip("libosm_hip.so is not built")
-    for rel, body in TYPES.items():
-        path = tmp_path / rel
-        path.parent.mkdir(parents=True, exist_ok=True)
-        path.write_text(body)
+    if all(os.path.exists(os.path.join(REFERENCE_INCLUDE, rel)) for rel in TYPES):
+        headers = REFERENCE_INCLUDE  # the reference's own types
+    else:
+        headers = str(tmp_path)
+        for rel, body in TYPES.items():
+            path = tmp_path / rel
+            path.parent.mkdir(parents=True, exist_ok=True)
+            path.write_text(body)
     (tmp_path / "hip_sparse_moe.cpp").write_text(adapter_source())
     (tmp_path / "main.cpp").write_text(MAIN)
     exe = tmp_path / "adapter_check"
-    cmd = ["g++", "-std=c++20", "-Wall", "-Werror", "-I", str(tmp_path), "-I", os.path.join(ROOT, "include"),
+    print(f"adapter compiled against {headers}")
+    cmd = ["g++", "-std=c++20", "-Wall", "-Werror", "-I", headers, "-I", os.path.join(ROOT, "include"),
            str(tmp_path / "hip_sparse_moe.cpp"), str(tmp_path / "main.cpp"), "-L", LIB_DIR, "-losm_hip",
            "-Wl,-rpath-link,/opt/rocm/lib", "-o", str(exe)]
     r = subprocess.run(cmd, capture_output=True, text=True)

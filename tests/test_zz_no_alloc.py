@@ -46,6 +46,13 @@ def test_static_decode_matches_decode_device(ctx, model, sublayer):
         got = y.download(np.float32, n * D)
         assert np.all(np.isfinite(ref))
         assert np.array_equal(got, ref), (sublayer, n)
+    # The static call's routing is not kept, so the query refuses it until
+    # the layer's next other call.
+    with pytest.raises(osm_hip.OsmError) as e:
+        moe.routing(3)
+    assert e.value.status == osm_hip.OSM_E_INVALID and "without allocation" in e.value.diagnostic
+    moe.decode_device(slab, 0, x.ptr, y_ref.ptr, 3, sublayer=sublayer)
+    assert moe.routing(3)["ids"].shape == (3, K)
 
 
 def test_static_decode_rejects_beyond_capacity(ctx, model):
