@@ -1483,26 +1483,25 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   const uint32_t n4 = nslot * I / 4u;  // a multiple of 8 (I % 32 == 0)
   constexpr int kH4PerThread = 8;
   float4 hv[kH4PerThread];
+  // Every lane issues all kH4PerThread loads, an index past the end reading
+  // the last element: with no branch around them, a wait for a load issued
+  // earlier counts exactly these behind it. Such a value is never stored:
+  // the 8 lanes of a chunk are all in range or all past it (n4 % 8 == 0).
   auto load_h = [&](uint32_t pass) {
 #pragma unroll
     for (int u = 0; u < kH4PerThread; ++u) {
       const uint32_t f = (pass * kH4PerThread + u) * kDownThreads + tid;
-      hv[u] = f < n4 ? h4[f] : make_float4(0.f, 0.f, 0.f, 0.f);
+      hv[u] = h4[f < n4 ? f : n4 - 1u];
     }
   };
-  if constexpr (MODE != kDownCombine) load_h(0);  // h does not depend on the slot pointers: its first batch is issued first
-
-  // This wavefront's slots: lane l loads slot l's pointer and weight (vector
-  // loads, in flight with h's), each slot's are then read from its lane, and
-  // the packed chunk and metadata of each are loaded with no branch between
-  // them. Slots past nslot and null pointers read a valid blob with weight 0
-  // (the combine reads no pointer: every slot it adds was resident).
-  const uint32_t ls = lane < nslot ? lane : 0u;
-  const uint8_t* lp = MODE == kDownCombine ? nullptr : p.src.blob(t, ls);
-  // Per-lane addresses (a routing weight, or the shared gate): one vector load.
-  const float* wsrc = ls < p.top_k ? (p.weights ? p.weights + static_cast<size_t>(t) * p.top_k + ls : nullptr)
-                                   : (p.shared_gate ? p.shared_gate + t : nullptr);
-  const float lw = wsrc ? ldg<float>(wsrc) : 1.0f;
+  if constexpr (MODE != kDownCombine) load_h(0);
+  // This wavefront's slots. Their pointers and weights sit at wavefront-
+  // uniform addresses, so they are scalar loads, which complete on their own
+  // counter: waiting for them does not wait for h's vector loads issued
+  // before them. The packed chunk and metadata of each slot are then loaded
+  // with no branch between them. Slots past nslot and null pointers read a
+  // valid blob with weight 0 (the combine reads no pointer: every slot it
+  // adds was resident).
   const uint8_t* bp[kSlotsPerWave];
   float w[kSlotsPerWave];
   uint32_t js[kSlotsPerWave];
@@ -1510,13 +1509,12 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
   for (int i = 0; i < kSlotsPerWave; ++i) {
     const uint32_t ci = half + 2u * i;
     const uint32_t j = ci < ncover ? (MODE == kDownParts ? slot_at(p.list, ci) : ci) : nslot;
-    const int src = static_cast<int>(j < nslot ? j : 0u);
-    const uint64_t pv = reinterpret_cast<uint64_t>(lp);
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pv), src));
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(pv >> 32), src));
-    bp[i] = reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
-    w[i] = readlane_f(lw, src);
-    js[i] = j < nslot ? j : 0u;
+    const uint32_t jj = j < nslot ? j : 0u;
+    bp[i] = MODE == kDownCombine ? p.fallback : p.src.blob(t, jj);
+    const float* ws = jj < p.top_k ? (p.weights ? p.weights + static_cast<size_t>(t) * p.top_k + jj : nullptr)
+                                   : (p.shared_gate ? p.shared_gate + t : nullptr);
+    w[i] = ws ? *ws : 1.0f;
+    js[i] = jj;
     if (j >= nslot || (MODE != kDownCombine && bp[i] == nullptr)) w[i] = 0.0f;
     if (bp[i] == nullptr) bp[i] = p.fallback;
   }
