@@ -393,6 +393,12 @@ uint32_t slot_magic(uint32_t nslot) {
   return nslot > 1u ? static_cast<uint32_t>((0x100000000ull + nslot - 1u) / nslot) : 0u;
 }
 
+// Pairs a thread holds in registers from the first load to the scatter: 8
+// cover P <= 8,192 (a 512-token chunk of top-10 + shared is 5,632); pairs
+// beyond are read again from memory in each pass.
+constexpr int kBucketRegPairs = 8;
+constexpr uint32_t kNoBucket = 0xFFFFFFFFu;
+
 __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t* __restrict__ ids, const float* __restrict__ weights, const float* __restrict__ shared_gate,
     uint32_t T, uint32_t k, uint32_t nslot, uint32_t E, const uint8_t* const* __restrict__ expert_table,
@@ -409,18 +415,53 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
   const uint32_t P = T * nslot;
   // Token of pair i as a high product (slot_magic; one slot: the pair index).
   auto token_of = [&](uint32_t i) { return nslot > 1u ? __umulhi(i, magic) : i; };
+  // Bucket and weight of pair i: slot < k is routed (ids clamped to E - 1,
+  // as an out-of-range id is never produced), slot k the shared expert E.
+  auto pair_of = [&](uint32_t i, uint32_t& e, float& w) {
+    const uint32_t t = token_of(i), j = i - t * nslot;
+    if (j < k) {
+      const size_t o = static_cast<size_t>(t) * k + j;
+      e = ids[o];
+      e = e < E ? e : E - 1u;
+      w = weights[o];
+    } else {
+      e = E;
+      w = shared_gate ? shared_gate[t] : 1.0f;
+    }
+  };
+
+  // Every global read of the pass is requested here, before any wait: the
+  // experts and weights of this thread's first pairs and the blobs of
+  // buckets tid and tid + 1024 (nb <= 1025).
+  uint32_t pe[kBucketRegPairs];
+  float pw[kBucketRegPairs];
+#pragma unroll
+  for (int r = 0; r < kBucketRegPairs; ++r) {
+    const uint32_t i = tid + r * kBucketThreads;
+    pe[r] = kNoBucket;
+    pw[r] = 0.0f;
+    if (i < P) pair_of(i, pe[r], pw[r]);
+  }
+  auto blob_of = [&](uint32_t b) -> const uint8_t* {
+    const uint8_t* blob = b < E ? expert_table[b] : shared_expert;
+    return blob ? blob : fallback;
+  };
+  const uint8_t* blob0 = tid < nb ? blob_of(tid) : fallback;
+  const uint8_t* blob1 = tid + kBucketThreads < nb ? blob_of(tid + kBucketThreads) : fallback;
+  constexpr uint32_t kRegSpan = kBucketRegPairs * kBucketThreads;
+
   for (uint32_t b = tid; b < nb; b += kBucketThreads) counts[b] = 0u, cursor[b] = 0u;
   __syncthreads();
   // Routed pairs only: the shared expert's bucket (E) holds one pair per
   // token, in token order, so it needs no counting or cursor.
-#pragma unroll 4
-  for (uint32_t i = tid; i < P; i += kBucketThreads) {
-    const uint32_t t = token_of(i), j = i - t * nslot;
-    if (j < k) {
-      uint32_t e = ids[static_cast<size_t>(t) * k + j];
-      e = e < E ? e : E - 1u;
-      atomicAdd(&counts[e], 1u);
-    }
+#pragma unroll
+  for (int r = 0; r < kBucketRegPairs; ++r)
+    if (pe[r] < E) atomicAdd(&counts[pe[r]], 1u);
+  for (uint32_t i = kRegSpan + tid; i < P; i += kBucketThreads) {
+    uint32_t e;
+    float w;
+    pair_of(i, e, w);
+    if (e < E) atomicAdd(&counts[e], 1u);
   }
   if (nb > E && tid == 0) counts[E] = T;
   __syncthreads();
@@ -464,13 +505,13 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     }
     __syncthreads();
   }
-  for (uint32_t b = tid; b < nb; b += kBucketThreads) {
+  for (uint32_t h = 0; h < 2u; ++h) {
+    const uint32_t b = tid + h * kBucketThreads;
+    if (b >= nb) break;
     const uint32_t n = counts[b];
-    const uint8_t* blob = b < E ? expert_table[b] : shared_expert;
-    if (blob == nullptr) blob = fallback;
     for (uint32_t s = 0; s * kTileTokens < n; ++s) {
       Tile tl;
-      tl.blob = blob;
+      tl.blob = h == 0u ? blob0 : blob1;
       tl.start = offsets[b] + s * kTileTokens;
       tl.count = n - s * kTileTokens < kTileTokens ? n - s * kTileTokens : kTileTokens;
       tiles[tbase[b] + s] = tl;
@@ -478,18 +519,11 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
   }
   const uint32_t ntiles = s_tiles;  // written before the last scan's barrier
   const bool stage = ntiles * kTileTokens <= kBucketStageRows && P <= kBucketStagePairs;
-#pragma unroll 4
-  for (uint32_t i = tid; i < P; i += kBucketThreads) {
-    const uint32_t t = token_of(i), j = i - t * nslot;
-    uint32_t e = E;  // the shared expert's bucket
-    if (j < k) {
-      e = ids[static_cast<size_t>(t) * k + j];
-      e = e < E ? e : E - 1u;  // as counted above
-    }
+  auto scatter = [&](uint32_t i, uint32_t e, float w) {
+    const uint32_t t = token_of(i);
     const uint32_t in_bucket = e == E ? t : atomicAdd(&cursor[e], 1u);
     const uint32_t pos = offsets[e] + in_bucket;
     const uint32_t slot = (tbase[e] + in_bucket / kTileTokens) * kTileTokens + in_bucket % kTileTokens;
-    const float w = j < k ? weights[static_cast<size_t>(t) * k + j] : (shared_gate ? shared_gate[t] : 1.0f);
     pair_pos[i] = pos;
     if (stage) {
       s_rows[slot] = t;
@@ -498,6 +532,15 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
       tile_rows[slot] = t;
       pair_w[pos] = w;
     }
+  };
+#pragma unroll
+  for (int r = 0; r < kBucketRegPairs; ++r)
+    if (pe[r] != kNoBucket) scatter(tid + r * kBucketThreads, pe[r], pw[r]);
+  for (uint32_t i = kRegSpan + tid; i < P; i += kBucketThreads) {
+    uint32_t e;
+    float w;
+    pair_of(i, e, w);
+    scatter(i, e, w);
   }
   if (stage) {
     // In order: entries of a tile past its count hold whatever LDS held
@@ -542,6 +585,10 @@ struct SplitParams {
   uint32_t chunks;      // items per tile and K range
   uint32_t items;       // tiles (rounded to whole XCD rounds) x K ranges x chunks
   float* out;
+  // Gate/up with SwiGLU fused (one partial per row, group 64): h as bf16
+  // terms and per-group sums, the layout swiglu_terms_kernel writes.
+  uint16_t* h_terms;
+  float* h_sums;
 };
 
 // Work item -> (tile, K range, first row block). Workgroups are dealt to the
@@ -756,12 +803,16 @@ struct SplitLds {
 // `total` (cleared first when `first`), then, when `last`, its partial sums.
 // MFMA row m reads tile row min(m, count - 1); the D rows of lane q are tile
 // rows 4q .. 4q+3 (those past count are not stored).
-template <int META, int PROJ, int S, int NSTEP, int NT, int H, uint32_t kWgRows>
+// SwiGLU fused into gate/up: a 16-pair x 64-row exchange of the up sums, then
+// of h (padded row against bank conflicts).
+using FuseLds = float[kTileTokens][65];
+
+template <int META, int PROJ, int S, int NSTEP, int NT, int H, uint32_t kWgRows, bool FUSE>
 __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitLds<PROJ, NSTEP, NT, H>& lds,
                                               const BlockWeights<META, S, NSTEP>& W, const WaveMatrix& mx,
                                               uint32_t block, uint32_t split, uint32_t half, bool first, bool last,
                                               f32x4 (&total)[2], const float (&pw4)[4], uint32_t start,
-                                              uint32_t rows, uint32_t pr, uint32_t m, uint32_t q) {
+                                              uint32_t rows, uint32_t pr, uint32_t m, uint32_t q, FuseLds& fu) {
   constexpr int GPR = NSTEP / S;
   constexpr uint32_t G8 = (32u * S) / 8u;  // 16-byte units per group
   // The tile row indices pass through an opaque copy per block: every block
@@ -834,6 +885,66 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
       for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(total[nb][j]));
     return;
   }
+  if constexpr (FUSE) {
+    // The block's 64 rows are one group of h (G = 64) and the whole of K is
+    // summed (one partial): h = SwiGLU(gate, up) is formed here, as
+    // swiglu_terms_kernel forms it from the partials (0 + sum, the same
+    // expression), and written as its bf16 terms and group sum. Up waves
+    // hand their sums to the gate waves through LDS; the gate waves leave h
+    // there; then 128 threads take (pair, 8-row word) each.
+    static_assert(PROJ == 2 && kWgRows == 64u, "fused SwiGLU: gate/up blocks of 64 rows");
+#pragma unroll
+    for (uint32_t nb = 0; nb < 2u; ++nb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (pr == 1u) fu[4u * q + j][mx.wave_row + nb * kBlockRows + m] = total[nb][j];
+    __syncthreads();
+    if (pr == 0u) {
+#pragma unroll
+      for (uint32_t nb = 0; nb < 2u; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float& cell = fu[4u * q + j][mx.wave_row + nb * kBlockRows + m];
+          const float g = 0.0f + total[nb][j], u = 0.0f + cell;
+          const float sig = __builtin_amdgcn_rcpf(1.0f + expf(-g));
+          cell = g * sig * u;
+        }
+    }
+    __syncthreads();
+    const uint32_t tid = threadIdx.x;
+    if (tid < kTileTokens * 8u) {
+      const uint32_t pj = tid / 8u, wd = tid % 8u;
+      const uint32_t I = mx.N;
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = fu[pj][wd * 8u + k];
+      const size_t pair = start + pj;
+      float rep[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (uint32_t t = 0; t < kActSplit; ++t) {
+        uint16_t o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int k = word_k(e);
+          o[e] = bf16_rne(v[k] - rep[k]);
+          rep[k] += bf16_to_f32(o[e]);
+        }
+        uint4 pk;
+        pk.x = o[0] | (static_cast<uint32_t>(o[1]) << 16);
+        pk.y = o[2] | (static_cast<uint32_t>(o[3]) << 16);
+        pk.z = o[4] | (static_cast<uint32_t>(o[5]) << 16);
+        pk.w = o[6] | (static_cast<uint32_t>(o[7]) << 16);
+        if (pj < rows) *reinterpret_cast<uint4*>(p.h_terms + (pair * kActSplit + t) * I + block * 64u + wd * 8u) = pk;
+      }
+      float gsum = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) gsum += rep[k];
+      for (uint32_t x = 1; x < 8u; x <<= 1) gsum += __shfl_xor(gsum, static_cast<int>(x));
+      if (pj < rows && wd == 0u) p.h_sums[pair * (I / 64u) + block] = gsum;
+    }
+    __syncthreads();  // fu is rewritten by the next block's epilogue
+    return;
+  }
 #pragma unroll
   for (uint32_t nb = 0; nb < 2u; ++nb) {
     const uint32_t r = block * kWgRows + mx.wave_row + nb * kBlockRows + m;
@@ -857,7 +968,7 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
 // one. The next item's tile record is fetched while the current one is
 // staged, and the next item's first block is in flight while the current
 // item's last block computes.
-template <int META, int PROJ, int S, int NSTEP, int NT, int H>
+template <int META, int PROJ, int S, int NSTEP, int NT, int H, bool FUSE>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2))) void split_kernel(SplitParams p) {
   constexpr uint32_t KS = 32u * NSTEP;
   constexpr int GPR = NSTEP / S;  // groups per range
@@ -871,6 +982,8 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
   constexpr uint32_t kIB = item_blocks(H);
   constexpr uint32_t kProjWaves = PROJ == 2 ? kSplitWaves / 2u : kSplitWaves;
   __shared__ __align__(16) SplitLds<PROJ, NSTEP, NT, H> lds;
+  __shared__ float fuse_lds[FUSE ? kTileTokens : 1][FUSE ? 65 : 1];
+  FuseLds& fu = *reinterpret_cast<FuseLds*>(&fuse_lds[0][0]);  // referenced only when FUSE
 
   // Per-lane indices and the wave's matrix, derived from the thread index.
   // Inside the item loop the index is re-read opaquely, so that what derives
@@ -904,10 +1017,23 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
   // An empty first tile ends the workgroup at once (a tile past the capacity
   // has no blob at all).
   if (tl.count == 0u) return;
-  BlockWeights<META, S, NSTEP> W0, W1;
-  // The first item's first block.
-  load_block<META, S, NSTEP, kWgRows>(W0, wave_matrix(uniform_u32(tid0 / kWave)), tl.blob, wk.first_block,
-                                      wk.split * H, tid0 % 16u, tid0 % kWave / 16u);
+  // Weight register sets: sub-block s of an item is computed from W[s %
+  // kNBuf] while the next kNBuf - 1 sub-blocks are in flight. (Three sets,
+  // two sub-blocks in flight, measured no faster for the fused gate/up at 254
+  // registers: its waves do not wait on the weights' latency.) kSub is even,
+  // so every item starts at W[0].
+  constexpr uint32_t kSub = kIB * H;  // sub-blocks per item
+  constexpr uint32_t kNBuf = 2u;
+  static_assert(kSub % kNBuf == 0u, "items start at W[0]");
+  BlockWeights<META, S, NSTEP> W[kNBuf];
+  // The first item's first kNBuf - 1 sub-blocks.
+  {
+    const WaveMatrix mx0 = wave_matrix(uniform_u32(tid0 / kWave));
+#pragma unroll
+    for (uint32_t s0 = 0; s0 + 1u < kNBuf; ++s0)
+      load_block<META, S, NSTEP, kWgRows>(W[s0], mx0, tl.blob, wk.first_block + s0 / H, wk.split * H + s0 % H,
+                                          tid0 % 16u, tid0 % kWave / 16u);
+  }
   while (tl.count != 0u) {
     uint32_t tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
@@ -995,33 +1121,33 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(2
     __syncthreads();
 
     // The item's blocks, straight-line, so that each wait is for exactly the
-    // block about to be computed. The next record has arrived by the end of
+    // block about to be computed. Before computing sub-block sb the loads of
+    // sub-block sb + kNBuf - 1 are issued: this item's, or past its end the
+    // next item's first ones (or, with no next item, this item's first ones
+    // again, read and not used). The next record has arrived by the end of
     // the first block (its wait covers every older load) and turns into
-    // scalars there. After the last block W0 loads the next item's first
-    // block, or (no next item) this item's first block again, read and not
-    // used.
+    // scalars there.
     // Sub-block sb is range sb % H of block fb + sb / H; a block's H ranges
     // are consecutive sub-blocks and share its totals.
     TileRec next_rec{blob, 0u, 0u};
-    constexpr uint32_t kSub = kIB * H;
     f32x4 total[2];
 #pragma unroll
-    for (uint32_t sb = 0; sb < kSub; sb += 2u) {
-      const uint32_t b0 = fb + sb / H, h0 = sb % H, b1 = fb + (sb + 1u) / H, h1 = (sb + 1u) % H;
-      load_block<META, S, NSTEP, kWgRows>(W1, mx, blob, b1, split * H + h1, m, q);
+    for (uint32_t sb = 0; sb < kSub; ++sb) {
+      const uint32_t t = sb + kNBuf - 1u;
+      if (t < kSub) {
+        load_block<META, S, NSTEP, kWgRows>(W[t % kNBuf], mx, blob, fb + t / H, split * H + t % H, m, q);
+      } else {
+        const uint32_t u = t - kSub;
+        const bool has_next = next_rec.count != 0u;
+        load_block<META, S, NSTEP, kWgRows>(W[t % kNBuf], mx, has_next ? next_rec.blob : blob,
+                                            (has_next ? wk_next.first_block : fb) + u / H,
+                                            (has_next ? wk_next.split : split) * H + u % H, m, q);
+      }
       __builtin_amdgcn_sched_barrier(0);
-      compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows>(p, lds, W0, mx, b0, split, h0, h0 == 0u, h0 == H - 1u,
-                                                         total, pw4, start, rows, pr, m, q);
+      compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows, FUSE>(p, lds, W[sb % kNBuf], mx, fb + sb / H, split,
+                                                               sb % H, sb % H == 0u, sb % H == H - 1u, total, pw4,
+                                                               start, rows, pr, m, q, fu);
       if (sb == 0u) next_rec = uniform_rec(tl_next);
-      const bool last = sb + 2u >= kSub;
-      const bool has_next = next_rec.count != 0u;
-      const uint32_t b2 = fb + (sb + 2u) / H, h2 = (sb + 2u) % H;
-      load_block<META, S, NSTEP, kWgRows>(W0, mx, last && has_next ? next_rec.blob : blob,
-                                          last ? (has_next ? wk_next.first_block : fb) : b2,
-                                          last ? (has_next ? wk_next.split * H : split * H) : split * H + h2, m, q);
-      __builtin_amdgcn_sched_barrier(0);
-      compute_block<META, PROJ, S, NSTEP, NT, H, kWgRows>(p, lds, W1, mx, b1, split, h1, h1 == 0u, h1 == H - 1u,
-                                                         total, pw4, start, rows, pr, m, q);
     }
     __syncthreads();  // the LDS tile is restaged by the next item
     item = next;
@@ -1194,11 +1320,12 @@ void set_item_blocks(SplitParams& sp, uint32_t row_blocks, uint32_t nsplit, uint
 // a multiple of 8, and no more than there are items (also a multiple of 8).
 // A larger grid would leave workgroups waiting for a free slot, to start
 // their whole item list after the others end.
-template <int META, int PROJ, int S, int NSTEP, int NT, int H>
+template <int META, int PROJ, int S, int NSTEP, int NT, int H, bool FUSE>
 uint32_t split_grid(uint32_t items) {
   static const uint32_t per_cu = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP, NT, H>, kSplitThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, split_kernel<META, PROJ, S, NSTEP, NT, H, FUSE>,
+                                                     kSplitThreads, 0) !=
             hipSuccess ||
         n < 1)
       n = 1;
@@ -1213,43 +1340,45 @@ uint32_t split_grid(uint32_t items) {
   return items < grid ? items : grid;
 }
 
-template <int META, int PROJ, int S, int NSTEP, int NT, int H>
+template <int META, int PROJ, int S, int NSTEP, int NT, int H, bool FUSE>
 void launch_split_r(const SplitParams& sp, hipStream_t st) {
   // Only the ranges range_cols() can choose for this metadata and group are
   // instantiated (a wider one would not fit the registers).
   constexpr uint32_t kMetaBytes = META == OSM_META_F32 ? 4u : 2u;
-  // Two ranges per item only with 512-column ranges (staged directly).
-  if constexpr (NSTEP / S * kMetaBytes <= 16u && (H == 1 || NSTEP == 16))
-    split_kernel<META, PROJ, S, NSTEP, NT, H>
-        <<<split_grid<META, PROJ, S, NSTEP, NT, H>(sp.items), kSplitThreads, 0, st>>>(sp);
+  // Two ranges per item only with 512-column ranges (staged directly); the
+  // fused SwiGLU only for gate/up at group 64 (S = 2).
+  if constexpr (NSTEP / S * kMetaBytes <= 16u && (H == 1 || NSTEP == 16) && (!FUSE || (PROJ == 2 && S == 2)))
+    split_kernel<META, PROJ, S, NSTEP, NT, H, FUSE>
+        <<<split_grid<META, PROJ, S, NSTEP, NT, H, FUSE>(sp.items), kSplitThreads, 0, st>>>(sp);
 }
 
-template <int META, int PROJ, int S, int NT, int H>
+template <int META, int PROJ, int S, int NT, int H, bool FUSE>
 void launch_split_s(const SplitParams& sp, hipStream_t st) {
   switch (range_cols(sp.g, PROJ == 2 ? sp.g.hidden : sp.g.inter)) {
-    case 512: launch_split_r<META, PROJ, S, 16, NT, H>(sp, st); break;
-    case 256: launch_split_r<META, PROJ, S, 8, NT, H>(sp, st); break;
-    default: launch_split_r<META, PROJ, S, 4, NT, H>(sp, st); break;
+    case 512: launch_split_r<META, PROJ, S, 16, NT, H, FUSE>(sp, st); break;
+    case 256: launch_split_r<META, PROJ, S, 8, NT, H, FUSE>(sp, st); break;
+    default: launch_split_r<META, PROJ, S, 4, NT, H, FUSE>(sp, st); break;
   }
 }
 
-template <int META, int PROJ, int NT, int H>
+template <int META, int PROJ, int NT, int H, bool FUSE>
 void launch_split_meta(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.group) {
-    case 32: launch_split_s<META, PROJ, 1, NT, H>(sp, st); break;
-    case 64: launch_split_s<META, PROJ, 2, NT, H>(sp, st); break;
-    default: launch_split_s<META, PROJ, 4, NT, H>(sp, st); break;
+    case 32: launch_split_s<META, PROJ, 1, NT, H, FUSE>(sp, st); break;
+    case 64: launch_split_s<META, PROJ, 2, NT, H, FUSE>(sp, st); break;
+    default: launch_split_s<META, PROJ, 4, NT, H, FUSE>(sp, st); break;
   }
 }
 
 // NT: activation terms (2 for fp32 activations, 1 for an exact bf16 input);
-// H: K ranges per work item (2 only with 512-column ranges).
-template <int PROJ, int NT, int H>
+// H: K ranges per work item (2 only with 512-column ranges); FUSE: gate/up
+// writes h itself (one partial, group 64).
+template <int PROJ, int NT, int H, bool FUSE = false>
 void launch_split(const SplitParams& sp, hipStream_t st) {
   switch (sp.g.meta_dtype) {
-    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ, NT, H>(sp, st); break;
-    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ, NT, H>(sp, st); break;
-    default: launch_split_meta<OSM_META_BF16, PROJ, NT, H>(sp, st); break;
+    case OSM_META_F32: launch_split_meta<OSM_META_F32, PROJ, NT, H, FUSE>(sp, st); break;
+    case OSM_META_F16: launch_split_meta<OSM_META_F16, PROJ, NT, H, FUSE>(sp, st); break;
+    default: launch_split_meta<OSM_META_BF16, PROJ, NT, H, FUSE>(sp, st); break;
   }
 }
 
@@ -1437,8 +1566,15 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   const uint32_t gu_h = gu_quads ? 4u : gu_pairs ? 2u : 1u;
   const uint32_t gu_splits = gu_ranges / gu_h;
   set_item_blocks(sp, (I + split_rows<2>() - 1) / split_rows<2>(), gu_splits, item_blocks(static_cast<int>(gu_h)));
+  // One partial per row and groups of 64 (a gate/up block's rows): the
+  // SwiGLU and h's terms are formed in the gate/up epilogue.
+  const bool fuse = one_term && gu_quads && gu_splits == 1u && G == 64u && I % 64u == 0u;
+  sp.h_terms = a->h_terms;
+  sp.h_sums = a->h_sums;
   if (one_term) {
-    if (gu_quads)
+    if (fuse)
+      launch_split<2, 1, 4, true>(sp, st);
+    else if (gu_quads)
       launch_split<2, 1, 4>(sp, st);
     else if (gu_pairs)
       launch_split<2, 1, 2>(sp, st);
@@ -1451,8 +1587,9 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
       launch_split<2, kActSplit, 1>(sp, st);
   }
   const size_t hwords = static_cast<size_t>(P) * (I / 8u);
-  swiglu_terms_kernel<<<blocks_for(hwords, 4096), 256, 0, st>>>(a->gu_part, gu_splits, P, I, G, a->h_terms,
-                                                                a->h_sums);
+  if (!fuse)
+    swiglu_terms_kernel<<<blocks_for(hwords, 4096), 256, 0, st>>>(a->gu_part, gu_splits, P, I, G, a->h_terms,
+                                                                  a->h_sums);
   sp.terms = a->h_terms;
   sp.term_count = kActSplit;
   sp.sums = a->h_sums;
