@@ -280,6 +280,7 @@ struct Selection {
   uint32_t fid[OSMD_MAX_TOP_K + 1];           // exact path: candidates by rank
   float scal[3];                              // exact path: threshold, RMS scale, softmax sum
   uint32_t nneartie, ncand, thr, flags, wcount[kSelWaves];  // nneartie: near ties sent to the full recompute
+  uint32_t again;                             // exact path: recompute every expert
   uint16_t cl[kSelThreads * PER];             // exact path: candidate list
   __attribute__((aligned(16))) float xe[2][kExactCols];  // exact path: the inputs of two chunks
   __attribute__((aligned(16))) float prod[2][kExactRows][kExactStride];  // exact path: rounded products of two chunks
@@ -623,14 +624,11 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
   const uint32_t E = rv.expert_count, k = rv.top_k;
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const uint32_t base = tid * PER;
-  if (tid == 0) {
-    float th = INFINITY;
-    for (uint32_t i = 0; i < k; ++i) th = fminf(th, out.lg[i] - kBoundSlack * out.bd[i]);
-    out.scal[0] = th;
-  }
-  const float scale = rv.rms ? exact_rms_scale<PER>(rv, t, out) : 1.0f;  // its barriers publish scal[0]
-  if (!rv.rms) __syncthreads();
-  const float th = out.scal[0];
+  // The picks' lowest lower bound, by every thread from the ranking in LDS
+  // (stable since the certificate's barrier).
+  float th = INFINITY;
+  for (uint32_t i = 0; i < k; ++i) th = fminf(th, out.lg[i] - kBoundSlack * out.bd[i]);
+  const float scale = rv.rms ? exact_rms_scale<PER>(rv, t, out) : 1.0f;
   bool full = false;
   float m = -INFINITY;
   for (;;) {
@@ -660,6 +658,54 @@ __device__ bool select_exact(const RouteView& rv, uint32_t t, const float (&l)[P
     for (uint32_t first = 0; first < nc; first += kExactRows)
       exact_logits<PER, DEEP>(rv, t, out, first, nc - first < kExactRows ? nc - first : kExactRows, scale);
     __syncthreads();
+    if (!full && nc <= kWave) {
+      // Up to 64 candidates: wavefront 0 ranks them in registers (lane i
+      // holds candidate i of the list) with the keys, ranks, near-tie and
+      // underflow tests of the general form below, and one barrier instead
+      // of five.
+      if (tid < kWave) {
+        const bool act = lane < nc;
+        const uint32_t e = act ? out.cl[lane] : 0u;
+        const float x = act ? out.ex[e] : -INFINITY;
+        const float mm = wave_max(x);
+        const float key = act ? osm_libm_expf(x - mm) : -1.0f;
+        if (act) out.aux[e] = key;
+        uint32_t rk = 0u;
+        for (uint32_t i = 0; i < nc; ++i) {
+          const float w = readlane_f(key, static_cast<int>(i));
+          const uint32_t ei = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), static_cast<int>(i)));
+          rk += (w > key || (w == key && ei < e)) ? 1u : 0u;
+        }
+        if (act && rk <= k) out.fid[rk] = e;
+        // This candidate (rank rk) against the one ranked rk + 1.
+        const uint32_t n = nc < k + 1u ? nc : k + 1u;
+        float ec = 0.0f;
+        uint32_t c = 0u;
+        for (uint32_t i = 0; i < nc; ++i) {
+          const uint32_t ri = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(rk), static_cast<int>(i)));
+          if (ri == rk + 1u) {
+            ec = readlane_f(key, static_cast<int>(i));
+            c = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(e), static_cast<int>(i)));
+          }
+        }
+        const bool near = act && rk + 1u < n && e > c && key != ec && key - ec <= 0x1p-22f * key + 0x1p-138f;
+        const uint64_t nb = __ballot(near);
+        const uint64_t kb = __ballot(act && rk == k - 1u);  // one lane: nc >= k (the picks are candidates)
+        const float xk = readlane_f(x, static_cast<int>(__builtin_ctzll(kb)));
+        if (lane == 0u) {
+          out.nneartie = static_cast<uint32_t>(__popcll(nb));
+          out.again = (nb != 0u || !(xk - mm >= -kUnderflowGap)) ? 1u : 0u;
+        }
+      }
+      __syncthreads();
+      if (out.again == 0u) {
+        if (tid == 0) out.ncand = nc;
+        break;
+      }
+      full = true;
+      __syncthreads();
+      continue;
+    }
     float lm = -INFINITY;
 #pragma unroll
     for (int j = 0; j < PER; ++j)

@@ -393,12 +393,13 @@ uint32_t slot_magic(uint32_t nslot) {
   return nslot > 1u ? static_cast<uint32_t>((0x100000000ull + nslot - 1u) / nslot) : 0u;
 }
 
-// Pairs a thread holds in registers from the first load to the scatter: 8
-// cover P <= 8,192 (a 512-token chunk of top-10 + shared is 5,632); pairs
-// beyond are read again from memory in each pass.
-constexpr int kBucketRegPairs = 8;
+// Pairs a thread holds in registers from the first load to the scatter
+// (REG): 8 cover P <= 8,192 (a 512-token chunk of top-10 + shared is 5,632),
+// 1 covers P <= 1,024 (a 64-token decode step is 704) with a fraction of the
+// code; pairs beyond are read again from memory in each pass.
 constexpr uint32_t kNoBucket = 0xFFFFFFFFu;
 
+template <int REG>
 __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t* __restrict__ ids, const float* __restrict__ weights, const float* __restrict__ shared_gate,
     uint32_t T, uint32_t k, uint32_t nslot, uint32_t E, const uint8_t* const* __restrict__ expert_table,
@@ -433,10 +434,10 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
   // Every global read of the pass is requested here, before any wait: the
   // experts and weights of this thread's first pairs and the blobs of
   // buckets tid and tid + 1024 (nb <= 1025).
-  uint32_t pe[kBucketRegPairs];
-  float pw[kBucketRegPairs];
+  uint32_t pe[REG];
+  float pw[REG];
 #pragma unroll
-  for (int r = 0; r < kBucketRegPairs; ++r) {
+  for (int r = 0; r < REG; ++r) {
     const uint32_t i = tid + r * kBucketThreads;
     pe[r] = kNoBucket;
     pw[r] = 0.0f;
@@ -448,14 +449,14 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
   };
   const uint8_t* blob0 = tid < nb ? blob_of(tid) : fallback;
   const uint8_t* blob1 = tid + kBucketThreads < nb ? blob_of(tid + kBucketThreads) : fallback;
-  constexpr uint32_t kRegSpan = kBucketRegPairs * kBucketThreads;
+  constexpr uint32_t kRegSpan = REG * kBucketThreads;
 
   for (uint32_t b = tid; b < nb; b += kBucketThreads) counts[b] = 0u, cursor[b] = 0u;
   __syncthreads();
   // Routed pairs only: the shared expert's bucket (E) holds one pair per
   // token, in token order, so it needs no counting or cursor.
 #pragma unroll
-  for (int r = 0; r < kBucketRegPairs; ++r)
+  for (int r = 0; r < REG; ++r)
     if (pe[r] < E) atomicAdd(&counts[pe[r]], 1u);
   for (uint32_t i = kRegSpan + tid; i < P; i += kBucketThreads) {
     uint32_t e;
@@ -534,7 +535,7 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     }
   };
 #pragma unroll
-  for (int r = 0; r < kBucketRegPairs; ++r)
+  for (int r = 0; r < REG; ++r)
     if (pe[r] != kNoBucket) scatter(tid + r * kBucketThreads, pe[r], pw[r]);
   for (uint32_t i = kRegSpan + tid; i < P; i += kBucketThreads) {
     uint32_t e;
@@ -1538,11 +1539,16 @@ int osmd_moe_grouped(const osmd_moe_grouped_args* a, osmd_stream s) {
   }
   r = osmd_moe_select(&ms, s);
   if (r != 0) return r;
-  bucket_kernel<<<1, kBucketThreads, 0, st>>>(m.ids, m.weights, has_shared ? m.shared_gate : nullptr, T, m.top_k,
-                                              nslot, m.expert_count, m.expert_table, m.shared_expert,
-                                              m.fallback_blob, a->pair_pos, a->pair_w, static_cast<Tile*>(a->tiles),
-                                              tile_rows, a->tile_count, static_cast<uint32_t>(max_tiles),
-                                              slot_magic(nslot));
+  auto bucket = [&](auto kernel) {
+    kernel<<<1, kBucketThreads, 0, st>>>(m.ids, m.weights, has_shared ? m.shared_gate : nullptr, T, m.top_k, nslot,
+                                         m.expert_count, m.expert_table, m.shared_expert, m.fallback_blob,
+                                         a->pair_pos, a->pair_w, static_cast<Tile*>(a->tiles), tile_rows,
+                                         a->tile_count, static_cast<uint32_t>(max_tiles), slot_magic(nslot));
+  };
+  if (P <= kBucketThreads)
+    bucket(bucket_kernel<1>);
+  else
+    bucket(bucket_kernel<8>);
 
   SplitParams sp{};
   sp.g = g;
