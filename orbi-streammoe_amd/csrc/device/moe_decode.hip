@@ -468,6 +468,10 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
   fetch_x(kExactCols);
   __syncthreads();
   float acc = 0.0f;
+  // The adders' wavefront issues first on its SIMD while it adds (as in
+  // exact_logits_deep).
+  const bool adder_wave = tid < kWave;
+  if (adder_wave) __builtin_amdgcn_s_setprio(2);
   for (uint32_t k = 0; k <= nchunks; ++k) {
     if (active && k < nchunks) {
       float4* dst = reinterpret_cast<float4*>(&out.prod[k & 1u][r][seg]);
@@ -492,6 +496,7 @@ __device__ void exact_logits_rd(const RouteView& rv, uint32_t t, Selection<PER>&
     }
     __syncthreads();
   }
+  if (adder_wave) __builtin_amdgcn_s_setprio(0);
   if (tid < nr) out.ex[out.cl[first + tid]] = acc;
 }
 
@@ -583,11 +588,17 @@ __device__ void exact_logits_deep(const RouteView& rv, uint32_t t, Selection<PER
   if (nchunks > 1u) fetch_x(xb, 1);
   if (nchunks > 2u) fetch_x(xa, 2);
   __syncthreads();
+  // The adders' wavefront issues first on its SIMD while it adds: each
+  // addition waits for the one before it, and a wavefront of another
+  // workgroup sharing the SIMD would otherwise take the slots in between.
+  const bool adder_wave = tid < kWave;
+  if (adder_wave) __builtin_amdgcn_s_setprio(2);
   // Even steps stage odd chunks from xb, odd steps even chunks from xa.
   for (uint32_t k = 0; k <= nchunks; k += 2u) {
     step(k, wa, xb);
     if (k + 1u <= nchunks) step(k + 1u, wb, xa);
   }
+  if (adder_wave) __builtin_amdgcn_s_setprio(0);
   if (tid < nr) out.ex[out.cl[first + tid]] = acc;
 }
 
