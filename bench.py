@@ -231,6 +231,9 @@ def decode_batches(ctx, moes, slab, args):
         out[str(B)] = entry
         log(f"[bench] decode batch {B}: {json.dumps(entry)}")
         del xs, ys
+    out["grouped_precision"] = ("the grouped GEMMs take fp32 activations (x, h) as two bf16 terms, 16 significant "
+                                "bits: median relative L2 error 5.5e-6 against float64, against 1.2e-6 for the "
+                                "reference's fp32 arithmetic (tests/test_gpu_grouped.py)")
     return out
 
 
@@ -263,7 +266,8 @@ def prefill(ctx, moes, slab, args, layers=8):
            "us_per_token_layer": round(us / T, 4), "distinct_experts": round(uniq, 1),
            "bytes_per_chunk_layer": int(bytes_chunk), "GBps": round(bytes_chunk / (us * 1e-6) / 1e9, 1),
            "algorithmic_TFLOPs": round(flops / (us * 1e-6) / 1e12, 2),
-           "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+           "mfma_frac": round(flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+           "precision": "bf16 input exact in one bf16 term; h (fp32 after SwiGLU) as two bf16 terms"}
     log(f"[bench] prefill: {json.dumps(res)}")
     return res
 
