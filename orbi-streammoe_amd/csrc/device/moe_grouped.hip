@@ -797,7 +797,7 @@ struct SplitLds {
   static constexpr uint32_t KS = 32u * NSTEP;
   static constexpr uint32_t RS = KS + 8u;  // row stride (bf16), padded against bank conflicts
   uint16_t a[H][NT][kTileTokens][RS];
-  float xs[H][NSTEP][kTileTokens];  // group sums (at most NSTEP groups per range)
+  __attribute__((aligned(16))) float xs[H][NSTEP][kTileTokens];  // group sums (at most NSTEP groups per range)
 };
 
 // MFMAs of one block against staged range `half` of the tile, added to
@@ -821,12 +821,6 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
   // all of them in registers across the blocks instead of re-reading them.
   uint32_t ar = m < rows ? m : rows - 1u;
   asm volatile("" : "+v"(ar));
-  uint32_t xr[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    xr[j] = 4u * q + j < rows ? 4u * q + j : rows - 1u;
-    asm volatile("" : "+v"(xr[j]));
-  }
   if (first) total[0] = total[1] = f32x4{0.f, 0.f, 0.f, 0.f};
   // k-slot of this lane within a group: its words are S * slot .. S * slot + S-1.
   const uint32_t slot = kPairLoads<S> ? pair_slot(q) : q;
@@ -851,9 +845,11 @@ __device__ __forceinline__ void compute_block(const SplitParams& p, const SplitL
 #pragma unroll
       for (int t = 0; t < NT; ++t)
         a[s2][t] = as_operand(*reinterpret_cast<const uint4*>(&lds.a[half][t][ar][(gg * G8 + S * slot + s2) * 8u]));
-    float xs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xs[j] = lds.xs[half][gg][xr[j]];
+    // The group sums of the lane's four D rows (tile rows 4q .. 4q+3) in one
+    // read; rows past the count read stale sums, and their totals are
+    // never stored.
+    const float4 x4 = *reinterpret_cast<const float4*>(&lds.xs[half][gg][4u * q]);
+    const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
     for (uint32_t nb = 0; nb < 2u; ++nb) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
