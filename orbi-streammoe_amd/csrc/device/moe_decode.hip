@@ -1036,7 +1036,10 @@ constexpr uint32_t kMaxPlanes = 8;
 
 // Loads token t's logits and their bounds (and table pointers) and selects;
 // every thread of the workgroup calls it.
-template <int PER, bool DEEP = false>
+// PLANES = false: the logits are final (the per-token router's), so the
+// router GEMM's plane sums are not compiled in and the loads below are the
+// first thing the workgroup issues.
+template <int PER, bool DEEP = false, bool PLANES = true>
 __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out, bool count) {
   const uint32_t E = rv.expert_count;
   const uint32_t D = rv.hidden;
@@ -1047,7 +1050,7 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint32_t e = (base + j < E) ? base + j : E - 1u;  // clamped: every load in bounds
-    if (rv.planes != nullptr) {
+    if (PLANES && rv.planes != nullptr) {
       // Partial sums of the router GEMM's K ranges, added in plane order.
       // Range r of R columns starts at the running sum P_r, so its prefix
       // sums are bounded by R |P_r| plus the plane's own part.
@@ -1095,7 +1098,7 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
     }
     tab[j] = rv.expert_table ? rv.expert_table[e] : nullptr;
   }
-  if (rv.planes != nullptr && rv.has_shared && threadIdx.x == 0) {
+  if (PLANES && rv.planes != nullptr && rv.has_shared && threadIdx.x == 0) {
     const size_t ps = static_cast<size_t>(rv.tokens) * (E + 1u);
     const float* pl = rv.planes + static_cast<size_t>(t) * (E + 1u) + E;
     float g = pl[0];
@@ -1455,7 +1458,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
     const RouteView& rv = p.rv;
     __shared__ Selection<PER> sel;
     if (j < rv.top_k) {
-      select_block<PER>(rv, t, sel, false);
+      select_block<PER, false, false>(rv, t, sel, false);  // the per-token router's final logits
       rows(pick_blob(rv, sel, j));
       if (blockIdx.x == 0 && j == 0) {
         publish_selection(rv, t, threadIdx.x, sel);
@@ -1874,6 +1877,9 @@ int osmd_moe_route(const osmd_moe_args* a, osmd_stream s) {
 
 int osmd_moe_gate_up(const osmd_moe_args* a, osmd_stream s) {
   const int per = a->expert_table ? selection_per(a->expert_count) : 0;
+  // gate/up's own selection reads final logits (the per-token router's);
+  // router GEMM planes go through the select kernel.
+  if (per > 0 && a->logit_planes != nullptr) return static_cast<int>(hipErrorInvalidValue);
   return launch_gate_up(gate_up_params(*a), a->tokens, per, static_cast<hipStream_t>(s));
 }
 
