@@ -942,12 +942,15 @@ __device__ __forceinline__ void rank_device(const RouteView& rv, const float (&l
 // Selection from this thread's device logits l[j] and bounds b[j] of experts
 // tid*PER + j (entries past E are ignored) and their table pointers. Every
 // thread of the workgroup calls it; it ends with a barrier, after which
-// out.id, out.p and out.flags are complete. `count`: add this selection to
-// the routing counters now (otherwise count_selection does it later).
+// out.id and out.flags are complete, and out.p when need_p (workgroup-
+// uniform; the softmax denominator and the probabilities are skipped
+// otherwise, for workgroups that only read their slot's expert). `count`:
+// add this selection to the routing counters now (otherwise
+// count_selection does it later).
 template <int PER, bool DEEP = false>
 __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, const float (&l)[PER],
                                               const float (&b)[PER], const uint8_t* const (&tab)[PER],
-                                              Selection<PER>& out, bool count) {
+                                              Selection<PER>& out, bool count, bool need_p = true) {
   const uint32_t E = rv.expert_count;
   const uint32_t k = rv.top_k;
   const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
@@ -978,10 +981,12 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
   // The softmax denominator over every expert (reference_ops.cpp:135-151),
   // its four wavefront sums combined in a fixed order.
   float sum = 0.0f;
+  if (need_p) {
 #pragma unroll
-  for (int j = 0; j < PER; ++j) sum += (base + j < E) ? expf(l[j] - mx) : 0.0f;
-  sum = wave_sum(sum);
-  if (lane == 0) out.red[2][wave] = sum;
+    for (int j = 0; j < PER; ++j) sum += (base + j < E) ? expf(l[j] - mx) : 0.0f;
+    sum = wave_sum(sum);
+    if (lane == 0) out.red[2][wave] = sum;
+  }
 
   // The certificate: every expert outside the picks below the k-th's lower
   // bound, each adjacent pair of picks far enough apart (one thread per
@@ -1004,10 +1009,10 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
   }
   if (tid == 0 && !(lk - mx >= -kUnderflowGap)) bad = true;
   bad = __syncthreads_or(bad) != 0;
-  sum = ((out.red[2][0] + out.red[2][1]) + out.red[2][2]) + out.red[2][3];
+  if (need_p) sum = ((out.red[2][0] + out.red[2][1]) + out.red[2][2]) + out.red[2][3];
   bool full = false;
   if (bad) full = select_exact<PER, DEEP>(rv, t, l, b, out, mx);
-  if (tid < k) out.p[tid] = expf(out.lg[tid] - mx) / sum;
+  if (need_p && tid < k) out.p[tid] = expf(out.lg[tid] - mx) / sum;
   if (tid == 0) out.flags = (bad ? 1u : 0u) | (full ? 2u : 0u);
   if (count && tid == 0 && rv.stats != nullptr) {
     atomicAdd(rv.stats + 0, 1u);
@@ -1040,7 +1045,8 @@ constexpr uint32_t kMaxPlanes = 8;
 // router GEMM's plane sums are not compiled in and the loads below are the
 // first thing the workgroup issues.
 template <int PER, bool DEEP = false, bool PLANES = true>
-__device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out, bool count) {
+__device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Selection<PER>& out, bool count,
+                                             bool need_p = true) {
   const uint32_t E = rv.expert_count;
   const uint32_t D = rv.hidden;
   const float* lg = rv.logits + static_cast<size_t>(t) * E;
@@ -1105,7 +1111,7 @@ __device__ __forceinline__ void select_block(const RouteView& rv, uint32_t t, Se
     for (uint32_t part = 1; part < rv.parts; ++part) g += pl[part * ps];
     rv.gate_out[t] = 1.0f / (1.0f + expf(-g));  // reference_ops.cpp:214-216
   }
-  select_values<PER, DEEP>(rv, t, p, bnd, tab, out, count);
+  select_values<PER, DEEP>(rv, t, p, bnd, tab, out, count, need_p);
 }
 
 template <int PER>
@@ -1458,9 +1464,12 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
     const RouteView& rv = p.rv;
     __shared__ Selection<PER> sel;
     if (j < rv.top_k) {
-      select_block<PER, false, false>(rv, t, sel, false);  // the per-token router's final logits
+      // The per-token router's final logits; only the publishing workgroup
+      // forms the probabilities.
+      const bool publisher = blockIdx.x == 0 && j == 0;
+      select_block<PER, false, false>(rv, t, sel, false, publisher);
       rows(pick_blob(rv, sel, j));
-      if (blockIdx.x == 0 && j == 0) {
+      if (publisher) {
         publish_selection(rv, t, threadIdx.x, sel);
         if (threadIdx.x == 0) count_selection(rv, sel);
       }
