@@ -67,6 +67,9 @@ def parse():
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="after the run, one device-to-device copy of this many MiB: the known-size "
                          "reference for scaling HBM traffic counters")
+    ap.add_argument("--timeline", action="store_true",
+                    help="no benchmark line: phase clocks of the last layer of the batch-1 graph, from the "
+                         "timeline build (make -C orbi-streammoe_amd timeline)")
     return ap.parse_args()
 
 
@@ -451,8 +454,71 @@ def cpu_baseline(seed, tokens):
     }
 
 
+# Timeline slots written by the timeline build's decode kernels (workgroup 0
+# of each kernel unless named), in the order a token-layer reaches them.
+TIMELINE_PHASES = [
+    (0, "router: first workgroup starts"),
+    (1, "router: first workgroup ends"),
+    (2, "router: last workgroup starts"),
+    (3, "router: last workgroup ends"),
+    (4, "gate/up (publishing workgroup) starts"),
+    (5, "logits, bounds and table pointers loaded; block max/min"),
+    (6, "histogram, threshold and candidates ranked"),
+    (7, "certificate decided"),
+    (8, "selection done"),
+    (9, "gate/up weights requested"),
+    (10, "rows stored (h)"),
+    (11, "selection published, workgroup ends"),
+    (15, "gate/up: last workgroup ends"),
+    (12, "down starts"),
+    (13, "down weights requested"),
+    (14, "down: workgroup 0 ends"),
+    (16, "down: last workgroup ends"),
+]
+
+
+def timeline(args):
+    """Median phase clocks (100 MHz, so 0.01 µs) of one batch-1 token-layer:
+    the last of the graph's 48 layers, over --steps replays of fresh tokens,
+    relative to the router's first workgroup start."""
+    lib = osm_hip.load(os.path.join(osm_hip.HERE, "libosm_hip_timeline.so"))
+    lib.osmd_timeline_read.restype = ctypes.c_int
+    lib.osmd_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_uint32]
+    ctx = osm_hip.Context(0)
+    L = args.layers
+    g, slab, moes = build_model(ctx, L, args.seed)
+    tok_bytes = D * 4
+    n = args.steps + args.warmup
+    xs = ctx.alloc(n * L * tok_bytes)
+    osm_hip.synth_tokens_device(ctx, args.seed, 0, n * L, D, xs.ptr)
+    xg, ys, scratch = ctx.alloc(L * tok_bytes), ctx.alloc(L * tok_bytes), ctx.alloc(L * tok_bytes)
+    graph = osm_hip.decode_graph(ctx, moes, list(range(L)), slab, xg.ptr, ys.ptr, scratch.ptr, 1, chained=False)
+    nslots = 17
+    buf = (ctypes.c_ulonglong * nslots)()
+    rows = []
+    for i in range(n):
+        ctx.copy_d2d(xg.ptr, xs.ptr.value + i * L * tok_bytes, L * tok_bytes)
+        graph.launch()
+        ctx.synchronize()
+        if lib.osmd_timeline_read(buf, nslots) != 0:
+            raise RuntimeError("osmd_timeline_read failed")
+        if i >= args.warmup:
+            rows.append([(buf[j] - buf[0]) / 100.0 for j in range(nslots)])
+    med = np.median(np.array(rows), axis=0)
+    p10, p90 = np.percentile(np.array(rows), [10, 90], axis=0)
+    print(f"| step | µs (median) | p10 | p90 |")
+    print("|---|---|---|---|")
+    for slot, name in TIMELINE_PHASES:
+        print(f"| {name} | {med[slot]:.2f} | {p10[slot]:.2f} | {p90[slot]:.2f} |")
+    print(json.dumps({"timeline_us": {name: round(float(med[slot]), 2) for slot, name in TIMELINE_PHASES},
+                      "replays": len(rows), "layer": L - 1}), flush=True)
+
+
 def main():
     args = parse()
+    if args.timeline:
+        timeline(args)
+        return
     if args.counters:
         print(json.dumps(summarize_counters(args.counters[0], args.counters[1], args.copy_probe_mb), indent=1))
         return

@@ -36,6 +36,41 @@ using namespace osmk;
 
 constexpr uint32_t kMaxSlots = OSMD_MAX_TOP_K + 1u;
 
+// Timeline build (make timeline -> libosm_hip_timeline.so, OSMD_TIMELINE):
+// workgroup 0 of each decode kernel, and the last workgroup, note the
+// constant 100 MHz clock (s_memrealtime) at their phases in LDS and copy the
+// notes to osmd_timeline when they end (a store at each phase would make the
+// kernel's later waits on its vector memory operations wait for it too);
+// osmd_timeline_read copies the slots out. Every launch overwrites them, so
+// after a graph replay they hold its last layer's. The product build
+// compiles all of this to nothing.
+#ifdef OSMD_TIMELINE
+constexpr int kTimelineSlots = 32;
+__device__ unsigned long long osmd_timeline[kTimelineSlots];
+__shared__ unsigned long long osmd_timeline_lds[kTimelineSlots];
+__device__ __forceinline__ bool timeline_first() { return blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0; }
+__device__ __forceinline__ bool timeline_last() {
+  return blockIdx.x == gridDim.x - 1u && blockIdx.y == gridDim.y - 1u && blockIdx.z == gridDim.z - 1u;
+}
+#define OSMD_STAMP(slot, who)                                                                      \
+  do {                                                                                             \
+    if ((who) && threadIdx.x == 0) osmd_timeline_lds[(slot)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#define OSMD_STAMP_FLUSH(lo, hi, who)                                                \
+  do {                                                                               \
+    if ((who) && threadIdx.x == 0)                                                   \
+      for (int s_ = (lo); s_ < (hi); ++s_) osmd_timeline[s_] = osmd_timeline_lds[s_]; \
+  } while (0)
+#else
+#define OSMD_STAMP(slot, who) ((void)0)
+#define OSMD_STAMP_FLUSH(lo, hi, who) ((void)0)
+#endif
+// Slots: route 0-1 (first workgroup start, end), 2-3 (last workgroup);
+// gate/up's workgroup 0 (slot 0, the publisher) 4 start, 5 logits loaded
+// and reduced, 6 ranked, 7 certificate decided, 8 selection done, 9 weights
+// requested, 10 rows stored, 11 end; down's workgroup 0 12 start, 13 weights
+// requested, 14 end; the last workgroup's end: gate/up 15, down 16.
+
 // Blob of slot j for token t: resolved pointers, or one fixed expert (the
 // single-expert operator).
 struct SlotSource {
@@ -975,8 +1010,10 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
   __syncthreads();
   mx = fmaxf(fmaxf(out.red[0][0], out.red[0][1]), fmaxf(out.red[0][2], out.red[0][3]));
   mn = fminf(fminf(out.red[1][0], out.red[1][1]), fminf(out.red[1][2], out.red[1][3]));
+  OSMD_STAMP(5, timeline_first());
 
   rank_device<PER>(rv, l, b, out, mx, mn);
+  OSMD_STAMP(6, timeline_first());
 
   // The softmax denominator over every expert (reference_ops.cpp:135-151),
   // its four wavefront sums combined in a fixed order.
@@ -1009,6 +1046,7 @@ __device__ __forceinline__ void select_values(const RouteView& rv, uint32_t t, c
   }
   if (tid == 0 && !(lk - mx >= -kUnderflowGap)) bad = true;
   bad = __syncthreads_or(bad) != 0;
+  OSMD_STAMP(7, timeline_first());
   if (need_p) sum = ((out.red[2][0] + out.red[2][1]) + out.red[2][2]) + out.red[2][3];
   bool full = false;
   if (bad) full = select_exact<PER, DEEP>(rv, t, l, b, out, mx);
@@ -1335,7 +1373,13 @@ __device__ __forceinline__ void route_block(const osmd_moe_args& a, uint32_t t, 
 template <int RD>
 __global__ __launch_bounds__(256) void route_kernel(osmd_moe_args a) {
   extern __shared__ __align__(16) float xs[];  // normalised input of this token, at xs_index(column)
+  OSMD_STAMP(0, timeline_first());
+  OSMD_STAMP(2, timeline_last());
   route_block<RD, 16>(a, blockIdx.y, blockIdx.x, xs);
+  OSMD_STAMP(1, timeline_first());
+  OSMD_STAMP(3, timeline_last());
+  OSMD_STAMP_FLUSH(0, 2, timeline_first());
+  OSMD_STAMP_FLUSH(2, 4, timeline_last());
 }
 
 // ---------------------------------------------------------------------------
@@ -1409,6 +1453,7 @@ __device__ __forceinline__ void gate_up_rows(const GateUpParams& p, uint32_t t, 
       bu[i][ci] = meta_bits<META>(blob + off.up_b, gi);
     }
   }
+  OSMD_STAMP(9, timeline_first());
   // The lane's slices of x (and their sums), loaded while the weights are in flight.
   load_xr<CPL>(p.x + static_cast<size_t>(t) * D, nch, lane, xr);
   float xsum[CPL];
@@ -1467,15 +1512,22 @@ __global__ __launch_bounds__(256) void gate_up_kernel(GateUpParams p) {
       // The per-token router's final logits; only the publishing workgroup
       // forms the probabilities.
       const bool publisher = blockIdx.x == 0 && j == 0;
+      OSMD_STAMP(4, timeline_first());
       select_block<PER, false, false>(rv, t, sel, false, publisher);
+      OSMD_STAMP(8, timeline_first());
       rows(pick_blob(rv, sel, j));
+      OSMD_STAMP(10, timeline_first());
       if (publisher) {
         publish_selection(rv, t, threadIdx.x, sel);
         if (threadIdx.x == 0) count_selection(rv, sel);
       }
+      OSMD_STAMP(11, timeline_first());
+      OSMD_STAMP_FLUSH(4, 12, timeline_first());
     } else {
       rows(rv.shared_expert);
     }
+    OSMD_STAMP(15, timeline_last());
+    OSMD_STAMP_FLUSH(15, 16, timeline_last());
   } else {
     // Host-driven slots: every slot in order, or the listed ones.
     const uint32_t js = p.list.count ? slot_at(p.list, j) : j;
@@ -1602,6 +1654,7 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
       bb[i] = meta_bits<META>(bp[i] + off.down_b, gi);
     }
   }
+  OSMD_STAMP(13, MODE == kDownFused && timeline_first());
 
   if constexpr (MODE != kDownCombine) {
     // Stage h and its per-chunk sums: 8 consecutive threads hold one 32-float
@@ -1668,7 +1721,12 @@ __device__ __forceinline__ void down_block(const DownParams& p, uint32_t t, uint
 template <int META, int LPR, int MAXS, int MODE>
 __global__ __launch_bounds__(kDownThreads) void down_kernel(DownParams p) {
   extern __shared__ __align__(16) float hs[];  // chunks, then chunk sums, then [2][rows] halves
+  OSMD_STAMP(12, MODE == kDownFused && timeline_first());
   down_block<META, LPR, MAXS, MODE>(p, blockIdx.y, blockIdx.x, hs);
+  OSMD_STAMP(14, MODE == kDownFused && timeline_first());
+  OSMD_STAMP(16, MODE == kDownFused && timeline_last());
+  OSMD_STAMP_FLUSH(12, 15, MODE == kDownFused && timeline_first());
+  OSMD_STAMP_FLUSH(16, 17, MODE == kDownFused && timeline_last());
 }
 
 
@@ -1953,6 +2011,15 @@ int osmd_moe_decode(const osmd_moe_args* a, osmd_stream s) {
   return r != 0 ? r : osmd_moe_experts(a, s);
 }
 
+
+#ifdef OSMD_TIMELINE
+// The timeline slots (timeline build only): n <= 32 values of the 100 MHz
+// clock, 0 for a slot no launch wrote since the library loaded.
+int osmd_timeline_read(unsigned long long* out, uint32_t n) {
+  if (out == nullptr || n > static_cast<uint32_t>(kTimelineSlots)) return static_cast<int>(hipErrorInvalidValue);
+  return static_cast<int>(hipMemcpyFromSymbol(out, HIP_SYMBOL(osmd_timeline), n * sizeof(unsigned long long)));
+}
+#endif
 
 int osmd_expert_forward(const uint8_t* blob, osm_expert_geometry g, const float* x, float* h,
                         float* out, osmd_stream s) {
