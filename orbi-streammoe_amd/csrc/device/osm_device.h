@@ -41,6 +41,10 @@ int osmd_memcpy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s);
 /* Device-to-device copy with a kernel when dst, src and bytes are 16-byte
  * aligned (a kernel node when captured), else hipMemcpyAsync. */
 int osmd_copy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s);
+/* Host-to-device copy by a kernel that reads pinned host memory (from
+ * osmd_host_malloc) over PCIe itself, on a grid of at most `blocks`
+ * workgroups; hipMemcpyAsync when dst, src or bytes is not 16-byte aligned. */
+int osmd_copy_from_pinned(void* dst, const void* src, size_t bytes, unsigned blocks, osmd_stream s);
 /* Zero-fill with a kernel (safe inside captured graphs). */
 int osmd_zero(void* dst, size_t bytes, osmd_stream s);
 int osmd_stream_create(osmd_stream* s);

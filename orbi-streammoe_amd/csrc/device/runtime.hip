@@ -132,6 +132,18 @@ int osmd_copy_d2d(void* dst, const void* src, size_t bytes, osmd_stream s) {
   return osmk::launch_status();
 }
 
+int osmd_copy_from_pinned(void* dst, const void* src, size_t bytes, unsigned blocks, osmd_stream s) {
+  if (bytes == 0) return 0;
+  const uintptr_t a = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes;
+  if (a % 16 != 0 || blocks == 0) return osmd_memcpy_h2d(dst, src, bytes, s);
+  const size_t n16 = bytes / 16;
+  size_t grid = (n16 + 255) / 256;
+  if (grid > blocks) grid = blocks;
+  copy16_kernel<<<static_cast<unsigned>(grid), 256, 0, static_cast<hipStream_t>(s)>>>(
+      static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
+  return osmk::launch_status();
+}
+
 int osmd_stream_create(osmd_stream* s) {
   hipStream_t h = nullptr;
   // Default priority, non-blocking with respect to the null stream.

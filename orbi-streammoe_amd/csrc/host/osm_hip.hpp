@@ -510,6 +510,7 @@ class HostExpertCache {
       std::uint32_t layer, std::uint32_t expert) const noexcept;
   [[nodiscard]] ExpertCacheStats stats() const noexcept;
   [[nodiscard]] std::size_t stride_bytes() const noexcept { return stride_; }
+  [[nodiscard]] bool pinned() const noexcept { return pinned_; }
 
  private:
   struct SlotMeta {
@@ -614,6 +615,9 @@ class ExpertBlobSource {
   // True when returned pointers stay valid after later calls, so a fill
   // may still be in flight when the next one starts.
   [[nodiscard]] virtual bool stable_pointers() const noexcept { return false; }
+  // True when the returned memory is pinned and mapped for the device, so a
+  // fill may be a kernel that reads it over PCIe itself.
+  [[nodiscard]] virtual bool device_readable() const noexcept { return false; }
 };
 
 // Whole model (layers x experts blobs) in one pinned host allocation.
@@ -624,6 +628,7 @@ class PinnedExpertStore final : public ExpertBlobSource {
   [[nodiscard]] const osm_expert_geometry& geometry() const noexcept override { return geom_; }
   [[nodiscard]] const std::byte* host_blob(std::uint32_t layer, std::uint32_t expert) override;
   [[nodiscard]] bool stable_pointers() const noexcept override { return true; }
+  [[nodiscard]] bool device_readable() const noexcept override { return true; }
   [[nodiscard]] std::byte* mutable_blob(std::uint32_t layer, std::uint32_t expert);
   [[nodiscard]] std::size_t stride() const noexcept { return stride_; }
   [[nodiscard]] std::uint32_t layers() const noexcept { return layers_; }
@@ -644,6 +649,7 @@ class HostCacheSource final : public ExpertBlobSource {
   HostCacheSource(HostExpertCache& cache, const osm_expert_geometry& geometry);
   [[nodiscard]] const osm_expert_geometry& geometry() const noexcept override { return geom_; }
   [[nodiscard]] const std::byte* host_blob(std::uint32_t layer, std::uint32_t expert) override;
+  [[nodiscard]] bool device_readable() const noexcept override { return cache_.pinned(); }
 
  private:
   HostExpertCache& cache_;
