@@ -218,9 +218,12 @@ def test_cached_two_tokens_refill_an_earlier_pick(ctx):
     assert cache.contains(0, 0) and cache.contains(0, 1) and not cache.contains(0, 10)
 
 
-def test_cached_decode_from_pread_storage(ctx, tmp_path):
-    # The whole miss path from files: pread storage -> pinned host L1 cache
-    # -> HBM cache, against the all-resident decode (bit-identical outputs).
+@pytest.mark.parametrize("pinned", [True, False], ids=["pinned-kernel-fill", "pageable-dma-fill"])
+def test_cached_decode_from_pread_storage(ctx, tmp_path, pinned):
+    # The whole miss path from files: pread storage -> host L1 cache -> HBM
+    # cache, against the all-resident decode (bit-identical outputs). With
+    # pinned L1 slots a miss is filled by a kernel that reads the host pages;
+    # with pageable slots, by the DMA engine.
     seed, D, I, G, E, k = 24, 256, 128, 64, 32, 4
     g = osm_hip.geometry(D, I, G, osm_hip.BF16)
     slab = osm_hip.ExpertSlab(ctx, g, 1, E)
@@ -234,7 +237,7 @@ def test_cached_decode_from_pread_storage(ctx, tmp_path):
     # evicts 13 times and never a pick of the batch being made resident (at
     # 12 slots the last two tokens would lose one; the layer needs all of a
     # token's picks resident at once).
-    host = osm_hip.HostExpertCache.from_storage(storage, 20 * stride, pinned=True)
+    host = osm_hip.HostExpertCache.from_storage(storage, 20 * stride, pinned=pinned)
     cache = osm_hip.ExpertCache(ctx, 16 * stride, host_cache=host, g=g)
     moe = osm_hip.MoeLayer(ctx, g, E, k, O.synth_router_bf16(seed, 0, E, D), osm_hip.BF16,
                            O.synth_shared_gate_bf16(seed, 0, D), O.synth_norm_weight(seed, 0, D),
