@@ -417,7 +417,10 @@ int osm_moe_layer_launch_phase(osm_context ctx, osm_moe_layer l, osm_expert_slab
                                uint32_t tokens, int sublayer, int phase);
 
 /* ---- expert sources and caches ---------------------------------------------
- * Whole model in pinned host memory: the fill source of the capped cache. */
+ * Whole model in pinned host memory: the fill source of the capped cache.
+ * A miss is copied by a 32-workgroup kernel that reads these pages over PCIe
+ * (a pinned host L1 cache is read the same way; a pageable one by
+ * hipMemcpyAsync), on the cache's side streams. */
 int osm_expert_store_create(const osm_expert_geometry_c* g, uint32_t layers, uint32_t experts,
                             osm_expert_store* out);
 void osm_expert_store_destroy(osm_expert_store s);
